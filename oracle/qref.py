@@ -1,0 +1,143 @@
+"""ctypes binding of the CPU oracle (liboracle.so built from this folder).
+
+TEST INFRASTRUCTURE ONLY: the parity checker for the HIP library and the
+timed CPU baseline. Only tests/, ``__graft_entry__.smoke()`` and bench.py's
+``cpu_baseline`` leg may import it; the product never does.
+
+The C sources restate candle's CPU path as SwarmLLM vendors it
+(vendor/candle/candle-core/src/quantized/{k_quants,avx,utils}.rs); see
+qref.h for the map.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, IQ4_NL, MXFP4 = 2, 8, 12, 14, 15, 20, 39
+BLOCK = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256, IQ4_NL: 32, MXFP4: 32}
+TYPE_SIZE = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292, IQ4_NL: 18, MXFP4: 17}
+VEC_DOT = {Q4_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q6_K: Q8_K, IQ4_NL: Q8_0, MXFP4: Q8_0}
+
+
+def build() -> str:
+    """Compile liboracle.so with the Makefile beside this file."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.qref_f32_to_f16.argtypes, L.qref_f32_to_f16.restype = [ctypes.c_float], ctypes.c_uint16
+        L.qref_f16_to_f32.argtypes, L.qref_f16_to_f32.restype = [ctypes.c_uint16], ctypes.c_float
+        L.qref_from_float.argtypes, L.qref_from_float.restype = [I, P, P, I64], I
+        L.qref_to_float.argtypes, L.qref_to_float.restype = [I, P, P, I64], I
+        L.qref_vec_dot.argtypes, L.qref_vec_dot.restype = [I, I64, P, P], ctypes.c_float
+        L.qref_vec_dot_unopt.argtypes, L.qref_vec_dot_unopt.restype = [I, I64, P, P], ctypes.c_float
+        L.qref_vec_dot_rows.argtypes, L.qref_vec_dot_rows.restype = [I, I64, P, P, I, P, I], None
+        L.qref_matmul.argtypes, L.qref_matmul.restype = [I, I64, I64, I64, P, P, P, I], I
+        L.qref_matmul_prequantized.argtypes = [I, I64, I64, I64, P, P, P, I]
+        L.qref_matmul_prequantized.restype = I
+        L.qref_matmul_upstream.argtypes, L.qref_matmul_upstream.restype = [I, I64, I64, I64, P, P, P], I
+        L.qref_quantize_rows.argtypes, L.qref_quantize_rows.restype = [I, I64, I64, P, P, I], I
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def nbytes(qtype: int, n: int) -> int:
+    return n // BLOCK[qtype] * TYPE_SIZE[qtype]
+
+
+def from_float(qtype: int, x: np.ndarray) -> np.ndarray:
+    """Blocks (as uint8 bytes) of ``x`` quantized as ``qtype``: the type's from_float."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.zeros(nbytes(qtype, x.size), dtype=np.uint8)
+    if lib().qref_from_float(qtype, _p(x), _p(out), x.size) != 0:
+        raise ValueError(f"from_float: type {qtype}, {x.size} values")
+    return out
+
+
+def to_float(qtype: int, blocks: np.ndarray, n: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    assert blocks.size >= nbytes(qtype, n)
+    out = np.empty(n, dtype=np.float32)
+    if lib().qref_to_float(qtype, _p(blocks), _p(out), n) != 0:
+        raise ValueError(f"to_float: type {qtype}, {n} values")
+    return out
+
+
+def vec_dot(qtype: int, n: int, xs: np.ndarray, ys: np.ndarray) -> np.float32:
+    return np.float32(lib().qref_vec_dot(qtype, n, _p(np.ascontiguousarray(xs)), _p(np.ascontiguousarray(ys))))
+
+
+def vec_dot_unopt(qtype: int, n: int, xs: np.ndarray, ys: np.ndarray) -> np.float32:
+    return np.float32(
+        lib().qref_vec_dot_unopt(qtype, n, _p(np.ascontiguousarray(xs)), _p(np.ascontiguousarray(ys))))
+
+
+def quantize_rows(qtype: int, x: np.ndarray, threads: int = 0) -> np.ndarray:
+    """The activation rows as the driver quantizes them (VecDotType blocks)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    vt = VEC_DOT[qtype]
+    out = np.zeros(m * nbytes(vt, k), dtype=np.uint8)
+    if lib().qref_quantize_rows(qtype, m, k, _p(x), _p(out), threads) != 0:
+        raise ValueError("quantize_rows")
+    return out
+
+
+def matmul(qtype: int, x: np.ndarray, w: np.ndarray, n: int, threads: int = 0) -> np.ndarray:
+    """k_quants::matmul: x [m, k] f32 against n weight rows of k values (bytes ``w``)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    assert w.size >= n * nbytes(qtype, k)
+    dst = np.empty((m, n), dtype=np.float32)
+    if lib().qref_matmul(qtype, m, k, n, _p(x), _p(w), _p(dst), threads) != 0:
+        raise ValueError("matmul")
+    return dst
+
+
+def matmul_prequantized(qtype: int, xq: np.ndarray, m: int, k: int, w: np.ndarray, n: int,
+                        threads: int = 0) -> np.ndarray:
+    dst = np.empty((m, n), dtype=np.float32)
+    rc = lib().qref_matmul_prequantized(qtype, m, k, n, _p(np.ascontiguousarray(xq)),
+                                        _p(np.ascontiguousarray(w)), _p(dst), threads)
+    if rc != 0:
+        raise ValueError("matmul_prequantized")
+    return dst
+
+
+def matmul_upstream(qtype: int, x: np.ndarray, w: np.ndarray, n: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    dst = np.empty((m, n), dtype=np.float32)
+    if lib().qref_matmul_upstream(qtype, m, k, n, _p(x), _p(np.ascontiguousarray(w)), _p(dst)) != 0:
+        raise ValueError("matmul_upstream")
+    return dst
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib().qref_f32_to_f16(float(x)))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().qref_f16_to_f32(int(h)))
