@@ -1,0 +1,149 @@
+/*
+ * qmm.h — C ABI of libqmm: quantized matrix products over GGUF block
+ * formats (Q8_0, Q4_K, Q6_K, IQ4_NL, MXFP4) on AMD Instinct MI355X (gfx950).
+ *
+ * It is the drop-in device arm below candle's QTensor / QMatMul::forward as
+ * SwarmLLM vendors it. The entry points and their conventions follow the C
+ * ABI the reference already binds from Rust for its card kernels
+ * (vendor/candle/candle-kernels/src/ffi.rs:58-107, implemented in
+ * vendor/candle/candle-kernels/src/ggml_mmq/mmq_entry.cu:100-223) and the
+ * device-arm surface QCudaStorage exposes
+ * (vendor/candle/candle-core/src/quantized/dummy_cuda.rs:10-143):
+ *   - every call returns an int status (QMM_OK ... ) and never aborts;
+ *   - buffers are raw device pointers the caller allocates and owns;
+ *     the library allocates nothing and frees nothing;
+ *   - `stream` is a hipStream_t passed as int64 (0 = the null stream);
+ *   - weight types are GGUF type ids; weights are the bytes a GGUF holds
+ *     (row-major [n][k], k a multiple of the block size);
+ *   - outputs are fully overwritten (callers need not zero them);
+ *   - stale runtime errors are cleared before a launch, so a failure
+ *     reported is this call's own.
+ *
+ * Outputs: dst[r][j] = sum_i x[r][i] * W[j][i] for activation rows r and
+ * weight rows j, row-major [rows][n] with leading dimension `ldd` (>= n).
+ */
+#ifndef QMM_H
+#define QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: the swarm_mmq_status values
+ * (vendor/candle/candle-kernels/src/ggml_mmq/swarm_mmq.cuh:85-93), plus NO_ROOM. */
+enum qmm_status {
+    QMM_OK = 0,
+    QMM_UNSUPPORTED = 1,          /* type or shape not covered                    */
+    QMM_WORKSPACE_TOO_SMALL = 2,  /* the caller's workspace is under *need        */
+    QMM_DEVICE_ERROR = 3,         /* a HIP runtime call or launch failed          */
+    QMM_NO_TILE = 4,              /* no kernel configuration fits this device     */
+    QMM_NO_ROOM = 5,              /* fault injection: this product must fall back */
+};
+
+/* GGUF type ids this library covers (vendor/candle/candle-core/src/quantized/mod.rs:319-371). */
+enum qmm_type {
+    QMM_Q8_0 = 8,
+    QMM_Q4_K = 12,
+    QMM_Q6_K = 14,
+    QMM_IQ4_NL = 20,
+    QMM_MXFP4 = 39,
+};
+
+/* Activation layouts (qmm_act_layout).
+ *   QMM_ACT_Q8K:  per 256 values, the codes / f32 scale / 16-value sums of
+ *                 candle's BlockQ8K::from_float (k_quants.rs:2882-2927);
+ *   QMM_ACT_Q8_0: per 32 values, the codes / f16 scale of
+ *                 BlockQ8_0::from_float (k_quants.rs:1240-1269), with each
+ *                 block's exact code sum.
+ * Both hold those values bit for bit, stored as planes (codes, scales,
+ * sums; see qmm_act_planes) rather than interleaved structs. */
+enum qmm_act_layout_id { QMM_ACT_Q8K = 0, QMM_ACT_Q8_0 = 1 };
+
+/* 1 when the library's kernels run on the current device (gfx950), else 0.
+ * Replaces swarm_mmq_available (mmq_entry.cu:100-117). */
+int qmm_available(void);
+
+/* The activation layout a product of `rows` activation rows against a weight
+ * of `type` reads, or -1 for a type not covered. Products whose layouts agree
+ * can share one quantized activation (QMatMul::forward_shared).
+ * Replaces swarm_mmq_q8_1_layout (mmq_entry.cu:130-135). */
+int qmm_act_layout(int type, int64_t rows);
+
+/* Bytes of a quantized activation of `rows` x `k` in `layout`.
+ * Replaces swarm_mmq_q8_1_bytes (mmq_entry.cu:137-141). */
+size_t qmm_act_bytes(int layout, int64_t k, int64_t rows);
+
+/* Byte offsets of the planes inside an activation buffer: codes (int8
+ * [rows][k]), scales (f32 [rows][k/256] or [rows][k/32]) and sums (int16
+ * [rows][k/16] for QMM_ACT_Q8K, int32 [rows][k/32] for QMM_ACT_Q8_0). */
+int qmm_act_planes(int layout, int64_t k, int64_t rows, size_t *codes_off, size_t *scales_off,
+                   size_t *sums_off);
+
+/* Quantize `rows` f32 rows of `k` values (`stride` floats apart) into `xq`
+ * in `layout`. Replaces swarm_mmq_quantize (mmq_entry.cu:144-158); the
+ * codes and scales are bit-exact to candle's CPU from_float. */
+int qmm_quantize_act(const float *x, void *xq, int layout, int64_t k, int64_t rows, int64_t stride,
+                     int64_t stream);
+
+/* Largest `rows` qmm_matvec takes in one launch. */
+int qmm_matvec_max_rows(void);
+
+/* dst = x · Wᵀ for 1 <= rows <= qmm_matvec_max_rows(), from an activation
+ * already quantized in qmm_act_layout(type, rows): the fused dequant + dot
+ * decode kernel. Replaces the reference's vector kernels
+ * mul_mat_vec_*_q8_1_cuda (launched from quantized/cuda.rs:519-620). */
+int qmm_matvec(int type, const void *w, const void *xq, float *dst, int64_t ldd, int64_t k, int64_t n,
+               int64_t rows, int64_t stream);
+
+/* dst = x · Wᵀ for any rows, from an f32 activation: quantizes it into the
+ * workspace and picks the kernel by rows (the QCudaStorage::fwd policy,
+ * quantized/cuda.rs:1653-1680). With launch == 0 nothing is enqueued and
+ * *need is set to the workspace bytes the launch will want; with
+ * launch != 0 the product is enqueued, and QMM_WORKSPACE_TOO_SMALL is
+ * returned (nothing enqueued) when workspace_bytes < that size.
+ * Replaces the plan/launch pair of swarm_mmq_matmul (mmq_entry.cu:162-203). */
+int qmm_forward(int type, const void *w, const float *x, int64_t x_stride, float *dst, int64_t ldd,
+                void *workspace, size_t workspace_bytes, size_t *need, int64_t k, int64_t n, int64_t rows,
+                int launch, int64_t stream);
+
+/* Dequantize `nelem` values of weight type `type` into f32 (out_f16 == 0)
+ * or IEEE f16 (out_f16 != 0; each value is f16 of the f32 one).
+ * Replaces QCudaStorage::dequantize / dequantize_f16
+ * (dummy_cuda.rs:44-52; kernels quantized.cu:828-1230). */
+int qmm_dequantize(int type, const void *w, void *out, int out_f16, int64_t nelem, int64_t stream);
+
+/* Quantize `nelem` f32 values on the device into GGUF blocks of `type`,
+ * bit-exact to candle's from_float (QTensor::quantize / quantize_onto,
+ * dummy_cuda.rs:54-70). `scratch` must hold qmm_quantize_scratch_bytes(). */
+size_t qmm_quantize_scratch_bytes(int type, int64_t nelem);
+int qmm_quantize_weights(int type, const float *x, void *w, int64_t nelem, void *scratch,
+                         size_t scratch_bytes, int64_t stream);
+
+/* Bytes of `nelem` values of `type` in GGUF blocks (GgmlDType::type_size x
+ * elements / block_size, quantized/mod.rs:421-461); 0 for a type not covered
+ * or a count that is not a whole number of blocks. */
+size_t qmm_type_bytes(int type, int64_t nelem);
+int qmm_block_size(int type);
+
+/* Fault injection, host side (the reference's fail_the_next_mmq_allocation,
+ * quantized/cuda.rs:972-991): the next qmm_forward launch returns
+ * QMM_NO_ROOM without enqueuing anything, once. */
+void qmm_fail_next_launch(void);
+
+/* Synthetic data: `n` f32 values from N(mean, std) on the device,
+ * reproducible from `seed` (splitmix64 counters, Box-Muller in double). */
+int qmm_fill_normal(float *out, int64_t n, uint64_t seed, float mean, float std, int64_t stream);
+
+/* Kernel launches enqueued by this library since the process started
+ * (the evidence of which kernel ran, like mmq_mma_products,
+ * quantized/cuda.rs:937-945): matvec launches, GEMM launches. */
+uint64_t qmm_matvec_launches(void);
+uint64_t qmm_gemm_launches(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QMM_H */

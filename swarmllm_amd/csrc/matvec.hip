@@ -1,0 +1,458 @@
+// matvec.hip — fused dequant + dot products for decode (1 activation row)
+// and small-batch verification (2..8 rows) on gfx950.
+//
+// dst[r][row] = sum over the weight row's blocks of the block dot against
+// activation row r, the arithmetic of candle's vec_dot per type
+// (vendor/candle/candle-core/src/quantized/k_quants.rs: Q4_K 2031-2111,
+// Q6_K 2598-2655, Q8_0 1294-1312, MXFP4 517-527, IQ4_NL 754-764) with
+// exact int32 inner sums (v_dot4_i32_i8) and f32 scaling; only the f32
+// summation order differs from the CPU's.
+//
+// Weights are read in GGUF bytes. The activation comes in the planes of
+// qmm_launch.h (codes / scales / group sums, 16-byte aligned).
+#include "qmm_device.h"
+#include "qmm_launch.h"
+
+namespace qmm {
+
+constexpr int kWavesPerBlock = 4;
+
+// ===========================================================================
+// Q4_K: 144-byte super-blocks are 16-byte aligned, so each lane reads its
+// part straight into registers. Lane = (super-block sb = lane/4 + 16t,
+// 64-value chunk j = lane%4); a wave takes RPW weight rows and applies each
+// lane's unpacked chunk to all NR activation rows.
+// ===========================================================================
+template <int NR, int RPW>
+__global__ __launch_bounds__(256) void mv_q4k_kernel(const uint8_t* __restrict__ W, int64_t n, int nsb,
+                                                     const int8_t* __restrict__ yq, const float* __restrict__ yd,
+                                                     const int16_t* __restrict__ ybs, float* __restrict__ dst,
+                                                     int64_t ldd) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)) * RPW;
+  if (row0 >= n) return;
+  const int j = lane & 3;
+  const int64_t k = (int64_t)nsb * 256;
+  const int64_t rb = (int64_t)nsb * 144;
+  const int sh = 16 * (j & 1);
+  float acc[NR][RPW];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int i = 0; i < RPW; i++) acc[r][i] = 0.0f;
+
+  for (int sb = lane >> 2; sb < nsb; sb += 16) {
+    uint4 hdr[RPW], qa[RPW], qb[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int64_t row = row0 + i < n ? row0 + i : n - 1;  // past the end: re-read, never written
+      const uint8_t* blk = W + row * rb + (int64_t)sb * 144;
+      hdr[i] = *(const uint4*)blk;
+      qa[i] = *(const uint4*)(blk + 16 + 32 * j);
+      qb[i] = *(const uint4*)(blk + 32 + 32 * j);
+    }
+    // per row: d, dmin and the scale/min of sub-blocks 2j, 2j+1
+    float dx[RPW], mx[RPW];
+    int sc0[RPW], sc1[RPW], m0[RPW], m1[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      dx[i] = h2f((uint16_t)(hdr[i].x & 0xFFFF));
+      mx[i] = h2f((uint16_t)(hdr[i].x >> 16));
+      const uint32_t u0 = hdr[i].y, u1 = hdr[i].z, u2 = hdr[i].w;
+      uint32_t scw, mw;
+      if (j < 2) {
+        scw = u0 & 0x3f3f3f3fu;
+        mw = u1 & 0x3f3f3f3fu;
+      } else {
+        scw = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+        mw = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+      }
+      sc0[i] = (scw >> sh) & 0xFF;
+      sc1[i] = (scw >> (sh + 8)) & 0xFF;
+      m0[i] = (mw >> sh) & 0xFF;
+      m1[i] = (mw >> (sh + 8)) & 0xFF;
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const int4* yp = (const int4*)(yq + r * k + (int64_t)sb * 256 + 64 * j);
+      const int4 y0 = yp[0], y1 = yp[1], y2 = yp[2], y3 = yp[3];
+      const int yv[16] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w,
+                          y2.x, y2.y, y2.z, y2.w, y3.x, y3.y, y3.z, y3.w};
+      const float dy = yd[r * nsb + sb];
+      const int2 bb = *(const int2*)(ybs + (r * nsb + sb) * 16 + 4 * j);
+      const int bs0 = (int)(int16_t)(bb.x & 0xFFFF) + (int)(int16_t)((uint32_t)bb.x >> 16);
+      const int bs1 = (int)(int16_t)(bb.y & 0xFFFF) + (int)(int16_t)((uint32_t)bb.y >> 16);
+#pragma unroll
+      for (int i = 0; i < RPW; i++) {
+        const uint32_t w[8] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w, qb[i].x, qb[i].y, qb[i].z, qb[i].w};
+        int slo = 0, shi = 0;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          slo = dot4((int)(w[t] & 0x0F0F0F0Fu), yv[t], slo);
+          shi = dot4((int)((w[t] >> 4) & 0x0F0F0F0Fu), yv[8 + t], shi);
+        }
+        const float main = dx[i] * (float)(sc0[i] * slo + sc1[i] * shi);
+        const float mins = mx[i] * (float)(m0[i] * bs0 + m1[i] * bs1);
+        acc[r][i] += dy * (main - mins);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const float v = wave_sum(acc[r][i]);
+      if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
+    }
+}
+
+// ===========================================================================
+// LDS staging for formats whose blocks are not 16-byte aligned. A wave
+// copies a span of a weight row (4096 values) into its own LDS region with
+// linear 16-byte loads from the 16-byte boundary at or before the span's
+// first byte. Every 16-byte piece read holds at least one byte of the row,
+// and a 16-byte aligned piece never crosses a page, so the over-read at
+// either end stays inside mapped memory.
+// ===========================================================================
+constexpr int kSpanMaxBytes = 4352;                  // 128 Q8_0 blocks, the largest span
+constexpr int kStageBytes = kSpanMaxBytes + 16 + 16; // + alignment slack + over-read
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Copies bytes [start, start+len) of W into lds; returns the LDS offset of `start`.
+__device__ __forceinline__ int stage_span(const uint8_t* __restrict__ W, int64_t start, int len, uint8_t* lds,
+                                          int lane) {
+  const int64_t a0 = start & ~(int64_t)15;
+  const int pieces = (int)((start + len - a0 + 15) >> 4);
+  for (int p = lane; p < pieces; p += 64) *(uint4*)(lds + 16 * p) = *(const uint4*)(W + a0 + 16 * p);
+  return (int)(start - a0);
+}
+
+// 4 bytes from LDS at any byte offset (two aligned dword reads + alignbyte).
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t* lds, int off) {
+  const int a = off & ~3;
+  const uint32_t lo = *(const uint32_t*)(lds + a);
+  const uint32_t hi = *(const uint32_t*)(lds + a + 4);
+  return __builtin_amdgcn_alignbyte(hi, lo, (uint32_t)(off & 3));
+}
+// n consecutive dwords from LDS at any byte offset.
+template <int N>
+__device__ __forceinline__ void lds_words(const uint8_t* lds, int off, uint32_t* out) {
+  const int a = off & ~3;
+  const uint32_t s = (uint32_t)(off & 3);
+  uint32_t w[N + 1];
+#pragma unroll
+  for (int i = 0; i <= N; i++) w[i] = *(const uint32_t*)(lds + a + 4 * i);
+#pragma unroll
+  for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], s);
+}
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t* lds, int off) { return lds_u32(lds, off) & 0xFFFF; }
+
+// 16-entry int8 table lookup of the 4 nibbles in the bytes of n (each < 16).
+__device__ __forceinline__ int32_t lut16(uint32_t n, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  const uint32_t sel = n & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
+  const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
+  const uint32_t m = ((n >> 3) & 0x01010101u) * 0xFFu;
+  return (int32_t)((hi & m) | (lo & ~m));
+}
+
+// ===========================================================================
+// Q6_K from LDS. Lane = (super-block sb = lane/4 within the span, unit u =
+// lane%4: half h = u/2, l0 = 16*(u%2)): the 64 values 128h + l0 + 32t +
+// [0,16), t = 0..3, each group t with its own int8 scale.
+// ===========================================================================
+template <int NR, int RPW>
+__global__ __launch_bounds__(256) void mv_q6k_kernel(const uint8_t* __restrict__ W, int64_t n, int nsb,
+                                                     const int8_t* __restrict__ yq, const float* __restrict__ yd,
+                                                     const int16_t* __restrict__ ybs, float* __restrict__ dst,
+                                                     int64_t ldd) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kWavesPerBlock][RPW][kStageBytes];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t row0 = ((int64_t)blockIdx.x * kWavesPerBlock + wv) * RPW;
+  if (row0 >= n) return;
+  const int64_t k = (int64_t)nsb * 256;
+  const int64_t rb = (int64_t)nsb * 210;
+  const int u = lane & 3, h = u >> 1, l0 = 16 * (u & 1);
+  float acc[NR][RPW];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int i = 0; i < RPW; i++) acc[r][i] = 0.0f;
+
+  for (int s0 = 0; s0 < nsb; s0 += 16) {
+    const int nspan = nsb - s0 < 16 ? nsb - s0 : 16;
+    int off[RPW];
+    wave_lds_sync();  // the previous span's reads are done
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int64_t row = row0 + i < n ? row0 + i : n - 1;
+      off[i] = stage_span(W, row * rb + (int64_t)s0 * 210, nspan * 210, smem[wv][i], lane);
+    }
+    wave_lds_sync();
+    const int sbl = lane >> 2;
+    if (sbl < nspan) {
+      const int sb = s0 + sbl;
+      // weight fields of this unit, per row
+      uint32_t qlA[RPW][4], qlB[RPW][4], qh[RPW][4];
+      int sc[RPW][4];
+      float dx[RPW];
+#pragma unroll
+      for (int i = 0; i < RPW; i++) {
+        const uint8_t* L = smem[wv][i];
+        const int b = off[i] + 210 * sbl;
+        lds_words<4>(L, b + 64 * h + l0, qlA[i]);
+        lds_words<4>(L, b + 64 * h + 32 + l0, qlB[i]);
+        lds_words<4>(L, b + 128 + 32 * h + l0, qh[i]);
+        uint32_t s4[2];
+        lds_words<2>(L, b + 192 + 8 * h, s4);  // scales 8h .. 8h+7
+        const int base = l0 >> 4;               // groups base, base+2, base+4, base+6
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int g = base + 2 * t;
+          sc[i][t] = (int)(int8_t)((s4[g >> 2] >> (8 * (g & 3))) & 0xFF);
+        }
+        dx[i] = h2f((uint16_t)lds_u16(L, b + 208));
+      }
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        const int8_t* yrow = yq + r * k + (int64_t)sb * 256 + 128 * h + l0;
+        int yv[4][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int4 q = *(const int4*)(yrow + 32 * t);
+          yv[t][0] = q.x; yv[t][1] = q.y; yv[t][2] = q.z; yv[t][3] = q.w;
+        }
+        const float dy = yd[r * nsb + sb];
+        const int4 bq = *(const int4*)(ybs + (r * nsb + sb) * 16 + 8 * h);  // bsums 8h .. 8h+7
+        const uint32_t bw[4] = {(uint32_t)bq.x, (uint32_t)bq.y, (uint32_t)bq.z, (uint32_t)bq.w};
+        const int bsh = 16 * (l0 >> 4);
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+          int tot = 0;
+#pragma unroll
+          for (int t = 0; t < 4; t++) {
+            const uint32_t* ql = (t & 1) ? qlB[i] : qlA[i];
+            const int nsh = 4 * (t >> 1);
+            int s = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const uint32_t q6 = ((ql[q] >> nsh) & 0x0F0F0F0Fu) | (((qh[i][q] >> (2 * t)) & 0x03030303u) << 4);
+              s = dot4((int)q6, yv[t][q], s);
+            }
+            const int bs = (int)(int16_t)((bw[t] >> bsh) & 0xFFFF);
+            tot += sc[i][t] * (s - 32 * bs);
+          }
+          acc[r][i] += (dx[i] * dy) * (float)tot;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const float v = wave_sum(acc[r][i]);
+      if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
+    }
+}
+
+// ===========================================================================
+// 32-value formats (Q8_0, MXFP4, IQ4_NL) from LDS. Lane = unit of two
+// blocks (64 values); a span is 128 blocks.
+// ===========================================================================
+template <int FMT>
+struct Fmt32;
+template <>
+struct Fmt32<T_Q8_0> {
+  static constexpr int B = 34;
+  __device__ static void decode(const uint8_t* L, int off, uint32_t q[8], float& d, uint32_t, uint32_t, uint32_t,
+                                uint32_t) {
+    d = h2f((uint16_t)lds_u16(L, off));
+    lds_words<8>(L, off + 2, q);
+  }
+};
+template <>
+struct Fmt32<T_IQ4_NL> {
+  static constexpr int B = 18;
+  __device__ static void decode(const uint8_t* L, int off, uint32_t q[8], float& d, uint32_t t0, uint32_t t1,
+                                uint32_t t2, uint32_t t3) {
+    d = h2f((uint16_t)lds_u16(L, off));
+    uint32_t n[4];
+    lds_words<4>(L, off + 2, n);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      q[i] = (uint32_t)lut16(n[i] & 0x0F0F0F0Fu, t0, t1, t2, t3);
+      q[4 + i] = (uint32_t)lut16((n[i] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
+    }
+  }
+};
+template <>
+struct Fmt32<T_MXFP4> {
+  static constexpr int B = 17;
+  __device__ static void decode(const uint8_t* L, int off, uint32_t q[8], float& d, uint32_t t0, uint32_t t1,
+                                uint32_t t2, uint32_t t3) {
+    d = e8m0_half(lds_u32(L, off) & 0xFF);
+    uint32_t n[4];
+    lds_words<4>(L, off + 1, n);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      q[i] = (uint32_t)lut16(n[i] & 0x0F0F0F0Fu, t0, t1, t2, t3);
+      q[4 + i] = (uint32_t)lut16((n[i] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
+    }
+  }
+};
+
+__device__ __forceinline__ uint32_t pack4(const int8_t* t) {
+  return (uint32_t)(uint8_t)t[0] | ((uint32_t)(uint8_t)t[1] << 8) | ((uint32_t)(uint8_t)t[2] << 16) |
+         ((uint32_t)(uint8_t)t[3] << 24);
+}
+
+template <int FMT, int NR, int RPW>
+__global__ __launch_bounds__(256) void mv_b32_kernel(const uint8_t* __restrict__ W, int64_t n, int nb,
+                                                     const int8_t* __restrict__ yq, const float* __restrict__ yd,
+                                                     float* __restrict__ dst, int64_t ldd) {
+  using F = Fmt32<FMT>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kWavesPerBlock][RPW][kStageBytes];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t row0 = ((int64_t)blockIdx.x * kWavesPerBlock + wv) * RPW;
+  if (row0 >= n) return;
+  const int64_t k = (int64_t)nb * 32;
+  const int64_t rb = (int64_t)nb * F::B;
+  const int8_t* tab = FMT == T_MXFP4 ? kMxfp4Values : kIq4nlValues;
+  const uint32_t t0 = pack4(tab), t1 = pack4(tab + 4), t2 = pack4(tab + 8), t3 = pack4(tab + 12);
+  float acc[NR][RPW];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int i = 0; i < RPW; i++) acc[r][i] = 0.0f;
+
+  for (int b0 = 0; b0 < nb; b0 += 128) {
+    const int nspan = nb - b0 < 128 ? nb - b0 : 128;
+    int off[RPW];
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const int64_t row = row0 + i < n ? row0 + i : n - 1;
+      off[i] = stage_span(W, row * rb + (int64_t)b0 * F::B, nspan * F::B, smem[wv][i], lane);
+    }
+    wave_lds_sync();
+    const int bl = 2 * lane;  // first block of this lane's unit, within the span
+    if (bl < nspan) {
+      const bool two = bl + 1 < nspan;
+      uint32_t q[RPW][2][8];
+      float dx[RPW][2];
+#pragma unroll
+      for (int i = 0; i < RPW; i++) {
+        F::decode(smem[wv][i], off[i] + bl * F::B, q[i][0], dx[i][0], t0, t1, t2, t3);
+        if (two) {
+          F::decode(smem[wv][i], off[i] + (bl + 1) * F::B, q[i][1], dx[i][1], t0, t1, t2, t3);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; t++) q[i][1][t] = 0;
+          dx[i][1] = 0.0f;
+        }
+      }
+      const int64_t gb = b0 + bl;  // global block index within the row
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        const int8_t* yrow = yq + r * k + gb * 32;
+        int yv[2][8];
+        {
+          const int4 a = *(const int4*)yrow;
+          const int4 b = *(const int4*)(yrow + 16);
+          yv[0][0] = a.x; yv[0][1] = a.y; yv[0][2] = a.z; yv[0][3] = a.w;
+          yv[0][4] = b.x; yv[0][5] = b.y; yv[0][6] = b.z; yv[0][7] = b.w;
+        }
+        float dy0 = yd[r * nb + gb], dy1 = 0.0f;
+        if (two) {
+          const int4 a = *(const int4*)(yrow + 32);
+          const int4 b = *(const int4*)(yrow + 48);
+          yv[1][0] = a.x; yv[1][1] = a.y; yv[1][2] = a.z; yv[1][3] = a.w;
+          yv[1][4] = b.x; yv[1][5] = b.y; yv[1][6] = b.z; yv[1][7] = b.w;
+          dy1 = yd[r * nb + gb + 1];
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; t++) yv[1][t] = 0;
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+          int s0 = 0, s1 = 0;
+#pragma unroll
+          for (int t = 0; t < 8; t++) {
+            s0 = dot4((int)q[i][0][t], yv[0][t], s0);
+            s1 = dot4((int)q[i][1][t], yv[1][t], s1);
+          }
+          acc[r][i] += (dx[i][0] * dy0) * (float)s0 + (dx[i][1] * dy1) * (float)s1;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      const float v = wave_sum(acc[r][i]);
+      if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
+    }
+}
+
+// ===========================================================================
+// dispatch
+// ===========================================================================
+int matvec_max_rows() { return 8; }
+
+template <int NR>
+static hipError_t launch_nr(int type, const void* w, int64_t n, int64_t k, const ActPlanes& p, float* dst,
+                            int64_t ldd, hipStream_t st) {
+  const uint8_t* W = (const uint8_t*)w;
+  if (type == T_Q4_K || type == T_Q6_K) {
+    const int nsb = (int)(k / 256);
+    if (type == T_Q4_K) {
+      constexpr int RPW = NR <= 2 ? 4 : 2;
+      const int64_t waves = (n + RPW - 1) / RPW;
+      mv_q4k_kernel<NR, RPW><<<dim3((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock)), 256, 0, st>>>(
+          W, n, nsb, p.codes, p.d, (const int16_t*)p.sums, dst, ldd);
+    } else {
+      constexpr int RPW = NR <= 2 ? 2 : 1;
+      const int64_t waves = (n + RPW - 1) / RPW;
+      mv_q6k_kernel<NR, RPW><<<dim3((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock)), 256, 0, st>>>(
+          W, n, nsb, p.codes, p.d, (const int16_t*)p.sums, dst, ldd);
+    }
+    return hipGetLastError();
+  }
+  const int nb = (int)(k / 32);
+  constexpr int RPW = NR <= 2 ? 2 : 1;
+  const int64_t waves = (n + RPW - 1) / RPW;
+  const dim3 grid((unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock));
+  switch (type) {
+    case T_Q8_0: mv_b32_kernel<T_Q8_0, NR, RPW><<<grid, 256, 0, st>>>(W, n, nb, p.codes, p.d, dst, ldd); break;
+    case T_IQ4_NL: mv_b32_kernel<T_IQ4_NL, NR, RPW><<<grid, 256, 0, st>>>(W, n, nb, p.codes, p.d, dst, ldd); break;
+    case T_MXFP4: mv_b32_kernel<T_MXFP4, NR, RPW><<<grid, 256, 0, st>>>(W, n, nb, p.codes, p.d, dst, ldd); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_matvec(int type, const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
+                         int64_t ldd, hipStream_t st) {
+  switch (rows) {
+    case 1: return launch_nr<1>(type, w, n, k, p, dst, ldd, st);
+    case 2: return launch_nr<2>(type, w, n, k, p, dst, ldd, st);
+    case 3: return launch_nr<3>(type, w, n, k, p, dst, ldd, st);
+    case 4: return launch_nr<4>(type, w, n, k, p, dst, ldd, st);
+    case 5: return launch_nr<5>(type, w, n, k, p, dst, ldd, st);
+    case 6: return launch_nr<6>(type, w, n, k, p, dst, ldd, st);
+    case 7: return launch_nr<7>(type, w, n, k, p, dst, ldd, st);
+    case 8: return launch_nr<8>(type, w, n, k, p, dst, ldd, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace qmm

@@ -1,0 +1,192 @@
+// qmm_api.hip — the C ABI of include/qmm.h: argument checks, the choice of
+// kernel by activation rows (QCudaStorage::fwd's policy,
+// vendor/candle/candle-core/src/quantized/cuda.rs:1653-1680, decided anew
+// for MI355X), status codes, launch counters and host-side fault injection.
+#include <atomic>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/qmm.h"
+#include "qmm_device.h"
+#include "qmm_launch.h"
+
+namespace {
+
+std::atomic<uint64_t> g_matvec_launches{0};
+std::atomic<uint64_t> g_gemm_launches{0};
+std::atomic<bool> g_fail_next{false};
+
+int block_size(int type) {
+  switch (type) {
+    case qmm::T_Q8_0: case qmm::T_IQ4_NL: case qmm::T_MXFP4: return 32;
+    case qmm::T_Q4_K: case qmm::T_Q6_K: return 256;
+    default: return 0;
+  }
+}
+int type_size(int type) {
+  switch (type) {
+    case qmm::T_Q8_0: return 34;
+    case qmm::T_IQ4_NL: return 18;
+    case qmm::T_MXFP4: return 17;
+    case qmm::T_Q4_K: return 144;
+    case qmm::T_Q6_K: return 210;
+    default: return 0;
+  }
+}
+
+// SWARMLLM_Q8K_SCALE=128: candle's Q8_K scale before SwarmLLM's #404 patch,
+// the reference's A/B knob (vendor/candle/candle-core/src/quantized/k_quants.rs:145-152). Read once.
+float q8k_scale() {
+  static const float s = [] {
+    const char* v = std::getenv("SWARMLLM_Q8K_SCALE");
+    return (v && std::strcmp(v, "128") == 0) ? 128.0f : 127.0f;
+  }();
+  return s;
+}
+
+int status_of(hipError_t e) { return e == hipSuccess ? QMM_OK : QMM_DEVICE_ERROR; }
+
+// A launch is judged by the runtime's last error afterwards; an error an
+// earlier, unrelated call left behind is cleared first (mmq_entry.cu:120-122).
+void clear_stale_error() { (void)hipGetLastError(); }
+
+bool shape_ok(int type, int64_t k, int64_t n, int64_t rows) {
+  const int qk = block_size(type);
+  return qk != 0 && k > 0 && k % qk == 0 && n > 0 && rows > 0 && k <= (int64_t)1 << 30 && n <= ((int64_t)1 << 31) - 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qmm_available(void) {
+  static std::mutex mu;
+  static int cached[64];
+  static bool known[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!known[dev]) {
+    hipDeviceProp_t prop;
+    int ok = 0;
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess) ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    (void)hipGetLastError();
+    cached[dev] = ok;
+    known[dev] = true;
+  }
+  return cached[dev];
+}
+
+int qmm_block_size(int type) { return block_size(type); }
+
+size_t qmm_type_bytes(int type, int64_t nelem) {
+  const int qk = block_size(type);
+  if (qk == 0 || nelem < 0 || nelem % qk) return 0;
+  return (size_t)(nelem / qk) * (size_t)type_size(type);
+}
+
+int qmm_act_layout(int type, int64_t rows) {
+  (void)rows;
+  switch (type) {
+    case qmm::T_Q4_K: case qmm::T_Q6_K: return QMM_ACT_Q8K;
+    case qmm::T_Q8_0: case qmm::T_IQ4_NL: case qmm::T_MXFP4: return QMM_ACT_Q8_0;
+    default: return -1;
+  }
+}
+
+size_t qmm_act_bytes(int layout, int64_t k, int64_t rows) {
+  if ((layout != QMM_ACT_Q8K && layout != QMM_ACT_Q8_0) || k <= 0 || rows <= 0) return 0;
+  if (k % (layout == QMM_ACT_Q8K ? 256 : 32)) return 0;
+  return qmm::act_bytes(layout, k, rows);
+}
+
+int qmm_act_planes(int layout, int64_t k, int64_t rows, size_t* codes_off, size_t* scales_off, size_t* sums_off) {
+  if (qmm_act_bytes(layout, k, rows) == 0) return QMM_UNSUPPORTED;
+  const qmm::ActPlanes p = qmm::act_planes(layout, nullptr, k, rows);
+  if (codes_off) *codes_off = (size_t)(uintptr_t)p.codes;
+  if (scales_off) *scales_off = (size_t)(uintptr_t)p.d;
+  if (sums_off) *sums_off = (size_t)(uintptr_t)p.sums;
+  return QMM_OK;
+}
+
+int qmm_quantize_act(const float* x, void* xq, int layout, int64_t k, int64_t rows, int64_t stride, int64_t stream) {
+  if (qmm_act_bytes(layout, k, rows) == 0 || stride < k || x == nullptr || xq == nullptr) return QMM_UNSUPPORTED;
+  clear_stale_error();
+  return status_of(qmm::launch_act_quantize(layout, x, stride, k, rows, xq, q8k_scale(), (hipStream_t)stream));
+}
+
+int qmm_matvec_max_rows(void) { return qmm::matvec_max_rows(); }
+
+int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd, int64_t k, int64_t n, int64_t rows,
+               int64_t stream) {
+  if (!shape_ok(type, k, n, rows) || rows > qmm::matvec_max_rows() || ldd < n || !w || !xq || !dst)
+    return QMM_UNSUPPORTED;
+  const int layout = qmm_act_layout(type, rows);
+  const qmm::ActPlanes p = qmm::act_planes(layout, (void*)xq, k, rows);
+  clear_stale_error();
+  const hipError_t e = qmm::launch_matvec(type, w, n, k, p, rows, dst, ldd, (hipStream_t)stream);
+  if (e == hipSuccess) g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
+  return status_of(e);
+}
+
+int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float* dst, int64_t ldd, void* workspace,
+                size_t workspace_bytes, size_t* need, int64_t k, int64_t n, int64_t rows, int launch, int64_t stream) {
+  if (!shape_ok(type, k, n, rows) || need == nullptr || ldd < n || x_stride < k) return QMM_UNSUPPORTED;
+  const int layout = qmm_act_layout(type, rows);
+  const size_t bytes = qmm::act_bytes(layout, k, rows);
+  *need = bytes;
+  if (!launch) return QMM_OK;
+  if (g_fail_next.exchange(false)) return QMM_NO_ROOM;
+  if (workspace_bytes < bytes || workspace == nullptr) return QMM_WORKSPACE_TOO_SMALL;
+  if (!w || !x || !dst) return QMM_UNSUPPORTED;
+  const hipStream_t st = (hipStream_t)stream;
+  clear_stale_error();
+  hipError_t e = qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st);
+  if (e != hipSuccess) return QMM_DEVICE_ERROR;
+  const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
+  const int64_t step = qmm::matvec_max_rows();
+  for (int64_t r0 = 0; r0 < rows; r0 += step) {
+    const int64_t nr = rows - r0 < step ? rows - r0 : step;
+    e = qmm::launch_matvec(type, w, n, k, qmm::act_rows(layout, p, k, r0), nr, dst + r0 * ldd, ldd, st);
+    if (e != hipSuccess) return QMM_DEVICE_ERROR;
+    g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
+  }
+  return QMM_OK;
+}
+
+int qmm_dequantize(int type, const void* w, void* out, int out_f16, int64_t nelem, int64_t stream) {
+  if (qmm_type_bytes(type, nelem) == 0 || !w || !out) return QMM_UNSUPPORTED;
+  clear_stale_error();
+  return status_of(qmm::launch_dequantize(type, w, out, out_f16, nelem, (hipStream_t)stream));
+}
+
+size_t qmm_quantize_scratch_bytes(int type, int64_t nelem) {
+  if (qmm_type_bytes(type, nelem) == 0) return 0;
+  return qmm::weight_quantize_scratch_bytes(type, nelem);
+}
+
+int qmm_quantize_weights(int type, const float* x, void* w, int64_t nelem, void* scratch, size_t scratch_bytes,
+                         int64_t stream) {
+  if (qmm_type_bytes(type, nelem) == 0 || !x || !w) return QMM_UNSUPPORTED;
+  if (scratch_bytes < qmm::weight_quantize_scratch_bytes(type, nelem)) return QMM_WORKSPACE_TOO_SMALL;
+  clear_stale_error();
+  return status_of(qmm::launch_weight_quantize(type, x, w, nelem, scratch, (hipStream_t)stream));
+}
+
+void qmm_fail_next_launch(void) { g_fail_next.store(true); }
+
+int qmm_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float std, int64_t stream) {
+  if (!out || n < 0) return QMM_UNSUPPORTED;
+  if (n == 0) return QMM_OK;
+  clear_stale_error();
+  return status_of(qmm::launch_fill_normal(out, n, seed, mean, std, (hipStream_t)stream));
+}
+
+uint64_t qmm_matvec_launches(void) { return g_matvec_launches.load(); }
+uint64_t qmm_gemm_launches(void) { return g_gemm_launches.load(); }
+
+}  // extern "C"

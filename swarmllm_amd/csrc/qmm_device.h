@@ -1,0 +1,143 @@
+// qmm_device.h — device-side layouts and helpers shared by the HIP kernels
+// of libqmm (gfx950 / CDNA4, wave64).
+//
+// Block layouts are the GGUF ones (byte-identical to candle's repr(C)
+// structs, vendor/candle/candle-core/src/quantized/k_quants.rs:165-317):
+// weights stay in the bytes a GGUF file holds, so a QTensor's data() is
+// the device buffer as is.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmm {
+
+constexpr int kWave = 64;
+
+// GGUF type ids (vendor/candle/candle-core/src/quantized/mod.rs:319-371).
+enum : int {
+  T_Q8_0 = 8,
+  T_Q4_K = 12,
+  T_Q6_K = 14,
+  T_Q8_K = 15,
+  T_IQ4_NL = 20,
+  T_MXFP4 = 39,
+};
+
+struct blk_q8_0 { uint16_t d; int8_t qs[32]; };                                     // 34 B / 32
+struct blk_q4_k { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; };          // 144 B / 256
+struct blk_q6_k { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; }; // 210 B / 256
+struct blk_q8_k { float d; int8_t qs[256]; int16_t bsums[16]; };                     // 292 B / 256
+struct blk_mxfp4 { uint8_t e; uint8_t qs[16]; };                                     // 17 B / 32
+struct blk_iq4_nl { uint16_t d; uint8_t qs[16]; };                                   // 18 B / 32
+static_assert(sizeof(blk_q8_0) == 34, "q8_0");
+static_assert(sizeof(blk_q4_k) == 144, "q4_k");
+static_assert(sizeof(blk_q6_k) == 210, "q6_k");
+static_assert(sizeof(blk_q8_k) == 292, "q8_k");
+static_assert(sizeof(blk_mxfp4) == 17, "mxfp4");
+static_assert(sizeof(blk_iq4_nl) == 18, "iq4_nl");
+
+// Values of a 4-bit code: k_quants.rs:30-36.
+__device__ __constant__ static const int8_t kIq4nlValues[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                                                1, 13, 25, 38, 53, 69, 89, 113};
+__device__ __constant__ static const int8_t kMxfp4Values[16] = {0, 1, 2, 3, 4, 6, 8, 12,
+                                                                0, -1, -2, -3, -4, -6, -8, -12};
+
+// ---- f16 <-> f32 (IEEE binary16, round to nearest even; f16 denormals kept)
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// f32 -> f16 in integer arithmetic. A plain (_Float16) cast of a product may
+// be folded into a mixed-precision multiply-add with +0, which turns -0 into
+// +0; the conversion here is the IEEE one for every input, signed zeros and
+// subnormal halves included.
+__device__ __forceinline__ uint16_t f2h(float f) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t e8 = (x >> 23) & 0xFFu;
+  const uint32_t m23 = x & 0x7FFFFFu;
+  if (e8 == 0xFFu) return (uint16_t)(sign | 0x7C00u | (m23 ? (0x200u | (m23 >> 13)) : 0u));
+  const int e = (int)e8 - 112;  // biased half exponent
+  if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    const uint32_t m = m23 | 0x800000u;
+    const int shift = 14 - e;
+    uint32_t h = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = ((uint32_t)e << 10) | (m23 >> 13);
+  const uint32_t rem = m23 & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;  // a carry into the exponent is correct
+  return (uint16_t)(sign | h);
+}
+
+// Half an E8M0 scale, exactly: 2^(e-128), subnormal below e = 2 (k_quants.rs:39-54).
+__device__ __forceinline__ float e8m0_half(uint32_t e) {
+  const uint32_t bits = e < 2 ? (0x00200000u << e) : ((e - 1u) << 23);
+  return __builtin_bit_cast(float, bits);
+}
+
+// ---- Rust conversions: truncate toward zero, saturate, NaN -> 0 ----------
+__device__ __forceinline__ int32_t rs_as_i32(float v) {
+  if (v != v) return 0;
+  if (v >= 2147483648.0f) return 2147483647;
+  if (v <= -2147483648.0f) return (-2147483647 - 1);
+  return (int32_t)v;
+}
+__device__ __forceinline__ int32_t rs_as_i8(float v) {
+  if (v != v) return 0;
+  if (v >= 127.0f) return 127;
+  if (v <= -128.0f) return -128;
+  return (int32_t)v;
+}
+__device__ __forceinline__ uint32_t rs_as_u8(float v) {
+  if (v != v) return 0;
+  if (v >= 255.0f) return 255;
+  if (v <= 0.0f) return 0;
+  return (uint32_t)v;
+}
+// f32::max / f32::min: the non-NaN operand wins; between equals the second.
+__device__ __forceinline__ float rs_max(float a, float b) {
+  if (b != b) return a;
+  if (a != a) return b;
+  return a > b ? a : b;
+}
+__device__ __forceinline__ float rs_min(float a, float b) {
+  if (b != b) return a;
+  if (a != a) return b;
+  return a < b ? a : b;
+}
+// nearest_int (k_quants utils.rs:1): round half away from zero, then as i32.
+__device__ __forceinline__ int32_t nearest_int(float v) { return rs_as_i32(roundf(v)); }
+__device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// ---- wave64 reductions ----------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+__device__ __forceinline__ int32_t sum_in_group4(int32_t v) {  // lanes 4g..4g+3
+  v += __shfl_xor(v, 1, kWave);
+  v += __shfl_xor(v, 2, kWave);
+  return v;
+}
+
+// Q4_K 6-bit scale/min of sub-block j (k_quants utils.rs:50-60).
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, int& m) {
+  if (j < 4) {
+    d = q[j] & 63;
+    m = q[j + 4] & 63;
+  } else {
+    d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+    m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+__device__ __forceinline__ int32_t dot4(int32_t a, int32_t b, int32_t c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+}  // namespace qmm

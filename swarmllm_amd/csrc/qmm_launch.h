@@ -1,0 +1,51 @@
+// qmm_launch.h — host-side launchers of libqmm's kernels (internal to the
+// library; the public C ABI is include/qmm.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qmm {
+
+// ---- activation layouts on the device --------------------------------------
+// The codes, scales and sums are bit-for-bit those of candle's BlockQ8K /
+// BlockQ8_0 from_float; only their placement differs: planes, 16-B aligned.
+//   ACT_Q8K (per 256, for Q4_K / Q6_K):
+//     codes  int8  [rows][k]
+//     d      f32   [rows][k/256]
+//     bsums  int16 [rows][k/16]
+//   ACT_Q8_0 (per 32, for Q8_0 / MXFP4 / IQ4_NL, and the MFMA GEMM of every type):
+//     codes  int8  [rows][k]
+//     d      f32   [rows][k/32]   (the f16 scale, widened exactly)
+//     sums   int32 [rows][k/32]   (exact sum of the block's codes)
+enum ActLayout : int { ACT_Q8K = 0, ACT_Q8_0 = 1 };
+
+struct ActPlanes {
+  int8_t* codes;
+  float* d;
+  void* sums;  // int16 (ACT_Q8K) or int32 (ACT_Q8_0)
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Byte size of an activation of `rows` x `k` in `layout`, and its planes.
+size_t act_bytes(int layout, int64_t k, int64_t rows);
+ActPlanes act_planes(int layout, void* base, int64_t k, int64_t rows);
+
+// ---- launchers (return hipSuccess or the launch error) ---------------------
+hipError_t launch_act_quantize(int layout, const float* x, int64_t stride, int64_t k, int64_t rows,
+                               void* out, float q8k_scale, hipStream_t s);
+hipError_t launch_weight_quantize(int type, const float* x, void* w, int64_t nelem, void* scratch,
+                                  hipStream_t s);
+size_t weight_quantize_scratch_bytes(int type, int64_t nelem);
+hipError_t launch_dequantize(int type, const void* w, void* out, int out_f16, int64_t nelem, hipStream_t s);
+// `p` points at the first of `rows` activation rows (planes already offset).
+hipError_t launch_matvec(int type, const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows,
+                         float* dst, int64_t ldd, hipStream_t s);
+// The planes of rows [r0, ...) of an activation laid out for `total_rows`.
+ActPlanes act_rows(int layout, const ActPlanes& p, int64_t k, int64_t r0);
+int matvec_max_rows();
+hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
+
+}  // namespace qmm

@@ -1,0 +1,220 @@
+"""Host-side mirror of candle's quantized tensor API on the MI355X library.
+
+Names, argument meaning and error behaviour follow
+vendor/candle/candle-core/src/quantized/mod.rs (GgmlDType :294-461,
+QTensor :76-1129, QMatMul :1131-1273, matmul_many :746-780): a QTensor
+holds GGUF blocks of an [n, k] weight in device memory; QMatMul.forward(x)
+returns x · Wᵀ with x [..., k] f32 contiguous and the result [..., n].
+
+Device memory and streams come from torch (plumbing only); every product,
+quantization and dequantization runs in libqmm's HIP kernels through the C
+ABI of include/qmm.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from dataclasses import dataclass
+from typing import List, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+
+class GgmlDType(enum.IntEnum):
+    """The GGUF type ids of the covered formats (mod.rs:319-371)."""
+
+    Q8_0 = 8
+    Q4K = 12
+    Q6K = 14
+    Iq4Nl = 20
+    Mxfp4 = 39
+
+    def block_size(self) -> int:
+        return lib().qmm_block_size(int(self))
+
+    def type_size(self) -> int:
+        return {8: 34, 12: 144, 14: 210, 20: 18, 39: 17}[int(self)]
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def fill_normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0, device="cuda") -> torch.Tensor:
+    """n f32 values from N(mean, std), reproducible from seed (on the device)."""
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    check("qmm_fill_normal", lib().qmm_fill_normal(_ptr(out), n, seed, mean, std, _stream()))
+    return out
+
+
+class QTensor:
+    """GGUF blocks of a 2-D weight [n, k] on the device (mod.rs:76)."""
+
+    def __init__(self, data: torch.Tensor, shape: Sequence[int], dtype: GgmlDType):
+        dtype = GgmlDType(dtype)
+        n, k = shape
+        qk = dtype.block_size()
+        if k % qk:
+            raise ValueError(f"quantized tensor must have their last dim divisible by block size {shape} {qk}")
+        want = lib().qmm_type_bytes(int(dtype), n * k)
+        if data.dtype != torch.uint8 or data.numel() != want or not data.is_cuda:
+            raise ValueError(f"QTensor: {data.numel()} device bytes for {shape} {dtype.name} (want {want})")
+        self.data_ = data.contiguous()
+        self.shape = (int(n), int(k))
+        self.dtype = dtype
+
+    @staticmethod
+    def from_data(raw: bytes, shape: Sequence[int], dtype: GgmlDType, device="cuda") -> "QTensor":
+        """Blocks from the bytes a GGUF holds them as (QStorage::from_data, mod.rs:119-163)."""
+        t = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(device)
+        return QTensor(t, shape, dtype)
+
+    @staticmethod
+    def quantize(w: torch.Tensor, dtype: GgmlDType) -> "QTensor":
+        """QTensor::quantize (mod.rs:850-880), on the device, bit-exact to from_float."""
+        dtype = GgmlDType(dtype)
+        if w.dim() != 2:
+            raise ValueError("quantize: a 2-D weight [n, k]")
+        n, k = w.shape
+        if k % dtype.block_size():
+            raise ValueError(f"quantize: last dim {k} not divisible by block size {dtype.block_size()}")
+        w = w.to(device="cuda", dtype=torch.float32).contiguous()
+        nel = n * k
+        out = torch.empty(lib().qmm_type_bytes(int(dtype), nel), dtype=torch.uint8, device=w.device)
+        sb = lib().qmm_quantize_scratch_bytes(int(dtype), nel)
+        scratch = torch.empty(max(sb, 1), dtype=torch.uint8, device=w.device)
+        check("qmm_quantize_weights",
+              lib().qmm_quantize_weights(int(dtype), _ptr(w), _ptr(out), nel, _ptr(scratch), sb, _stream()))
+        return QTensor(out, (n, k), dtype)
+
+    def dequantize(self) -> torch.Tensor:
+        return self._dequant(False)
+
+    def dequantize_f16(self) -> torch.Tensor:
+        return self._dequant(True)
+
+    def _dequant(self, f16: bool) -> torch.Tensor:
+        n, k = self.shape
+        out = torch.empty((n, k), dtype=torch.float16 if f16 else torch.float32, device=self.data_.device)
+        check("qmm_dequantize",
+              lib().qmm_dequantize(int(self.dtype), _ptr(self.data_), _ptr(out), int(f16), n * k, _stream()))
+        return out
+
+    def data(self) -> bytes:
+        """The GGUF bytes (QTensor::data)."""
+        return self.data_.cpu().numpy().tobytes()
+
+    def storage_size_in_bytes(self) -> int:
+        return self.data_.numel()
+
+    def __repr__(self) -> str:
+        return f"QTensor[{list(self.shape)}; {self.dtype.name}]"
+
+
+@dataclass
+class Workspace:
+    """A caller-owned device buffer the products quantize their activation into."""
+
+    buf: torch.Tensor = None
+
+    def get(self, nbytes: int, device) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        return self.buf
+
+
+class QMatMul:
+    """QMatMul::QTensor (mod.rs:1131-1273, Module::forward :1360-1383)."""
+
+    def __init__(self, qtensor: QTensor):
+        self.qtensor = qtensor
+        self._ws = Workspace()
+
+    @staticmethod
+    def from_qtensor(qtensor: QTensor) -> "QMatMul":
+        return QMatMul(qtensor)
+
+    def forward(self, xs: torch.Tensor) -> torch.Tensor:
+        """x [..., k] f32 -> [..., n]; the CustomOp1 shape rules of cpu_fwd (mod.rs:1280-1333)."""
+        n, k = self.qtensor.shape
+        if xs.dim() < 1 or xs.shape[-1] != k:
+            raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with {self.qtensor.shape}")
+        if xs.dtype != torch.float32:
+            raise ValueError("Expected f32")
+        if not xs.is_contiguous():
+            raise ValueError(f"input tensor is not contiguous {tuple(xs.shape)}")
+        rows = xs.numel() // k
+        out = torch.empty((*xs.shape[:-1], n), dtype=torch.float32, device=xs.device)
+        if rows == 0:
+            return out
+        need = ctypes.c_size_t(0)
+        L = lib()
+        t = int(self.qtensor.dtype)
+        st = _stream()
+        check("qmm_forward", L.qmm_forward(t, _ptr(self.qtensor.data_), _ptr(xs), k, _ptr(out), n, None, 0,
+                                           ctypes.byref(need), k, n, rows, 0, st))
+        ws = self._ws.get(need.value, xs.device)
+        check("qmm_forward", L.qmm_forward(t, _ptr(self.qtensor.data_), _ptr(xs), k, _ptr(out), n, _ptr(ws),
+                                           ws.numel(), ctypes.byref(need), k, n, rows, 1, st))
+        return out
+
+    __call__ = forward
+
+    @staticmethod
+    def forward_shared(xs: torch.Tensor, ws: Sequence["QMatMul"]) -> List[torch.Tensor]:
+        """Several weights against ONE activation, quantized once where their
+        activation layouts agree (mod.rs:1221-1263)."""
+        if len(ws) <= 1:
+            return [w.forward(xs) for w in ws]
+        k = ws[0].qtensor.shape[1]
+        if any(w.qtensor.shape[1] != k for w in ws) or xs.shape[-1] != k or not xs.is_contiguous():
+            return [w.forward(xs) for w in ws]
+        rows = xs.numel() // k
+        L = lib()
+        layouts = {L.qmm_act_layout(int(w.qtensor.dtype), rows) for w in ws}
+        if len(layouts) != 1 or rows > L.qmm_matvec_max_rows():
+            return [w.forward(xs) for w in ws]
+        layout = layouts.pop()
+        st = _stream()
+        xq = torch.empty(L.qmm_act_bytes(layout, k, rows), dtype=torch.uint8, device=xs.device)
+        check("qmm_quantize_act", L.qmm_quantize_act(_ptr(xs), _ptr(xq), layout, k, rows, k, st))
+        outs = []
+        for w in ws:
+            n = w.qtensor.shape[0]
+            out = torch.empty((*xs.shape[:-1], n), dtype=torch.float32, device=xs.device)
+            check("qmm_matvec", L.qmm_matvec(int(w.qtensor.dtype), _ptr(w.qtensor.data_), _ptr(xq), _ptr(out), n,
+                                             k, n, rows, st))
+            outs.append(out)
+        return outs
+
+
+def quantize_act(x: torch.Tensor, layout: int) -> torch.Tensor:
+    """The activation rows quantized on the device (qmm_quantize_act); the raw buffer."""
+    x = x.contiguous()
+    k = x.shape[-1]
+    rows = x.numel() // k
+    L = lib()
+    out = torch.zeros(L.qmm_act_bytes(layout, k, rows), dtype=torch.uint8, device=x.device)
+    check("qmm_quantize_act", L.qmm_quantize_act(_ptr(x), _ptr(out), layout, k, rows, k, _stream()))
+    return out
+
+
+def act_planes(buf: torch.Tensor, layout: int, k: int, rows: int):
+    """(codes int8 [rows, k], scales f32, sums) views of an activation buffer."""
+    co, so, uo = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+    check("qmm_act_planes", lib().qmm_act_planes(layout, k, rows, ctypes.byref(co), ctypes.byref(so), ctypes.byref(uo)))
+    per_scale = 256 if layout == _lib.ACT_Q8K else 32
+    codes = buf[co.value: co.value + rows * k].view(torch.int8).reshape(rows, k)
+    scales = buf[so.value: so.value + rows * (k // per_scale) * 4].view(torch.float32).reshape(rows, -1)
+    if layout == _lib.ACT_Q8K:
+        sums = buf[uo.value: uo.value + rows * (k // 16) * 2].view(torch.int16).reshape(rows, -1)
+    else:
+        sums = buf[uo.value: uo.value + rows * (k // 32) * 4].view(torch.int32).reshape(rows, -1)
+    return codes, scales, sums
