@@ -1,0 +1,333 @@
+#!/usr/bin/env python3
+"""bench.py — SwarmLLM's quantized matmul path on one MI355X (gfx950).
+
+One step = one Llama-3-8B-shaped decode layer's weight products at M = 1
+q/o 4096x4096, k/v 1024x4096 and gate/up
+14336x4096 in Q4_K, down 4096x14336 in Q6_K, each activation quantized once
+and shared where the reference shares it (q/k/v, gate/up: QMatMul::
+forward_shared, vendor/candle/candle-core/src/quantized/mod.rs:1221-1263).
+The launches go through libqmm's C ABI; a step is captured once as a HIP
+graph and replayed. Weights are N(0, 0.02) quantized on the device (bit-exact
+to the reference's from_float); activations N(0, 1). Several copies of the
+layer (>= 1 GiB together) are rotated so the 256 MB last-level cache cannot
+serve the weights: every step streams its weights from HBM.
+
+value = algorithmic bytes of the layer (weights + f32 inputs + f32 outputs,
+138,149,888 B) per second, whole job, inputs resident in HBM.
+roofline = the dominant kernel (the Q4_K matvec of the 14336x4096 gate
+projection) timed live on its own stream with HIP events, against 8 TB/s.
+cpu_baseline = the CPU restatement of candle's path (oracle/, the reference's
+k_quants::matmul with its AVX2 kernels) on this host's cores, on the same
+layer's bytes.
+
+Prints ONE JSON line. --gpus N > 1 exits: this build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+Q4K, Q6K = 12, 14
+ACT_Q8K = 0
+# (name, type, n, k): the C2 layer
+LAYER = [("q", Q4K, 4096, 4096), ("k", Q4K, 1024, 4096), ("v", Q4K, 1024, 4096), ("o", Q4K, 4096, 4096),
+         ("gate", Q4K, 14336, 4096), ("up", Q4K, 14336, 4096), ("down", Q6K, 4096, 14336)]
+# products sharing one quantized activation, in launch order
+GROUPS = [("attn_in", 4096, ["q", "k", "v"]), ("attn_out", 4096, ["o"]), ("ffn_in", 4096, ["gate", "up"]),
+          ("ffn_mid", 14336, ["down"])]
+CONFIG_SEED = 2
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def type_bytes(t: int, n: int, k: int) -> int:
+    return n * (k // 256) * (144 if t == Q4K else 210)
+
+
+def layer_bytes() -> dict:
+    w = sum(type_bytes(t, n, k) for _, t, n, k in LAYER)
+    xin = sum(4 * k for _, _, _, k in LAYER)
+    out = sum(4 * n for _, _, n, _ in LAYER)
+    return {"weights": w, "inputs": xin, "outputs": out, "total": w + xin + out}
+
+
+class Layer:
+    """Device buffers of one C2 layer copy plus the shared activations."""
+
+    def __init__(self, copy: int, acts: dict):
+        import torch
+
+        from swarmllm_amd import GgmlDType, QTensor, fill_normal
+
+        self.w = {}
+        for p, (name, t, n, k) in enumerate(LAYER):
+            seed = (CONFIG_SEED << 40) | (copy << 8) | p
+            wf = fill_normal(n * k, seed=seed, std=0.02).reshape(n, k)
+            self.w[name] = QTensor.quantize(wf, GgmlDType(t))
+            del wf
+        torch.cuda.synchronize()
+        self.acts = acts
+
+
+def make_acts():
+    import torch
+
+    from swarmllm_amd import fill_normal
+    from swarmllm_amd._lib import lib
+
+    L = lib()
+    acts = {}
+    for i, (g, k, _) in enumerate(GROUPS):
+        x = fill_normal(k, seed=(CONFIG_SEED << 40) | (0xA0 + i)).reshape(1, k)
+        xq = torch.empty(L.qmm_act_bytes(ACT_Q8K, k, 1), dtype=torch.uint8, device="cuda")
+        acts[g] = (x, xq)
+    outs = {name: torch.empty((1, n), dtype=torch.float32, device="cuda") for name, _, n, _ in LAYER}
+    return acts, outs
+
+
+def enqueue_step(layer: Layer, outs: dict, stream: int) -> None:
+    """The layer's launches: per group one activation quantization, then its matvecs."""
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    shape = {name: (t, n, k) for name, t, n, k in LAYER}
+    for g, k, names in GROUPS:
+        x, xq = layer.acts[g]
+        check("qmm_quantize_act", L.qmm_quantize_act(x.data_ptr(), xq.data_ptr(), ACT_Q8K, k, 1, k, stream))
+        for name in names:
+            t, n, _ = shape[name]
+            check("qmm_matvec", L.qmm_matvec(t, layer.w[name].data_.data_ptr(), xq.data_ptr(),
+                                             outs[name].data_ptr(), n, k, n, 1, stream))
+
+
+def capture(fn, stream):
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            fn(stream.cuda_stream)
+    torch.cuda.synchronize()
+    return g
+
+
+class Replayer:
+    """Runs exactly `steps` steps as replays of graphs over the layer copies."""
+
+    def __init__(self, layers, outs, stream):
+        self.layers, self.outs, self.stream = layers, outs, stream
+        self.graphs = {}
+
+    def graph(self, count: int):
+        if count not in self.graphs:
+            def fn(s, count=count):
+                for c in range(count):
+                    enqueue_step(self.layers[c], self.outs, s)
+            self.graphs[count] = capture(fn, self.stream)
+        return self.graphs[count]
+
+    def run(self, steps: int) -> None:
+        C = len(self.layers)
+        full, rem = divmod(steps, C)
+        g = self.graph(C) if full else None
+        for _ in range(full):
+            g.replay()
+        if rem:
+            self.graph(rem).replay()
+
+
+def time_gpu(fn, stream) -> float:
+    """Milliseconds of fn() on `stream`, between HIP events recorded on it."""
+    import torch
+
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b)
+
+
+def dominant_kernel(layers, outs, stream, reps: int) -> dict:
+    """The gate projection's Q4_K matvec alone, back to back over the copies
+    (activation already quantized), in one graph: its average launch."""
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    x, xq = layers[0].acts["ffn_in"]
+    n, k = 14336, 4096
+    s = stream.cuda_stream
+    check("qmm_quantize_act", L.qmm_quantize_act(x.data_ptr(), xq.data_ptr(), ACT_Q8K, k, 1, k, s))
+    per_graph = 4 * len(layers)
+
+    def fn(st):
+        for i in range(per_graph):
+            lay = layers[i % len(layers)]
+            check("qmm_matvec", L.qmm_matvec(Q4K, lay.w["gate"].data_.data_ptr(), xq.data_ptr(),
+                                             outs["gate"].data_ptr(), n, k, n, 1, st))
+
+    g = capture(fn, stream)
+    for _ in range(3):
+        g.replay()
+    ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+    launches = reps * per_graph
+    us = ms * 1e3 / launches
+    alg = 14336 * 16 * 144 + 4 * 4096 + 4 * 14336
+    gbs = alg / (us * 1e-6) / 1e9
+    return {"kernel": "mv_q4k_kernel<1,4> (Q4_K matvec, M=1, 14336x4096)", "us": us, "launches": launches,
+            "alg_bytes": alg, "gbs": gbs}
+
+
+def cpu_baseline(layers, budget_s: float) -> dict:
+    """The oracle (CPU restatement of candle's k_quants::matmul + AVX2 dots) on
+    the same layers' bytes, rotating over the copies as the GPU does (so the
+    weights come from DRAM, not the host's last-level cache), min over trials
+    of one full rotation, on this host's cores."""
+    import numpy as np
+
+    from oracle import qref
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    wbs = [{name: np.frombuffer(lay.w[name].data(), np.uint8) for name, _, _, _ in LAYER} for lay in layers]
+    xs = {g: layers[0].acts[g][0].cpu().numpy() for g, _, _ in GROUPS}
+    shape = {name: (t, n, k) for name, t, n, k in LAYER}
+
+    def one_layer(wb):
+        for g, _, names in GROUPS:
+            for name in names:
+                t, n, _ = shape[name]
+                qref.matmul(t, xs[g], wb[name], n, threads=threads)
+
+    def rotation():
+        for wb in wbs:
+            one_layer(wb)
+
+    rotation()  # warm
+    best, t_end, trials = float("inf"), time.perf_counter() + budget_s, 0
+    while trials < 3 or (time.perf_counter() < t_end and trials < 100):
+        t0 = time.perf_counter()
+        rotation()
+        best = min(best, (time.perf_counter() - t0) / len(wbs))
+        trials += 1
+    alg = layer_bytes()["total"]
+    return {"value": round(alg / best / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"C2 decode layer at M=1 (7 products, 138.1 MB of Q4_K/Q6_K weights) rotated over "
+                      f"{len(wbs)} copies, oracle/ restatement of candle k_quants::matmul with its AVX2 vec_dot "
+                      f"kernels, {threads} threads, min of {trials} rotations: {best * 1e3:.3f} ms/layer",
+            "cpu": cpu_name(), "logical_cpus": os.cpu_count()}
+
+
+def cpu_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--copies", type=int, default=8, help="layer copies rotated (8 x 138 MB)")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs its path on ONE GPU; --gpus {args.gpus} (WORLD_SIZE {world}) is not "
+              "supported. The path shards by weight rows with no exchange (see the sharding design); run with "
+              "--gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from swarmllm_amd._lib import lib
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    L = lib()
+    if L.qmm_available() != 1:
+        print("bench.py: libqmm kernels do not run on this device (gfx950 required)", file=sys.stderr)
+        return 1
+    props = torch.cuda.get_device_properties(0)
+    log(f"device {props.name} ({getattr(props, 'gcnArchName', '?')}), {props.multi_processor_count} CUs")
+
+    stream = torch.cuda.Stream()  # default priority
+    acts, outs = make_acts()
+    t0 = time.perf_counter()
+    layers = [Layer(c, acts) for c in range(args.copies)]
+    lb = layer_bytes()
+    log(f"{args.copies} layer copies quantized on the device in {time.perf_counter() - t0:.1f} s "
+        f"({args.copies * lb['weights'] / 2**30:.2f} GiB of weights)")
+
+    rep = Replayer(layers, outs, stream)
+    with torch.cuda.stream(stream):
+        rep.run(args.warmup)
+    torch.cuda.synchronize()
+    log(f"warmup {args.warmup} steps done")
+
+    wall0 = time.perf_counter()
+    ms = time_gpu(lambda: rep.run(args.steps), stream)
+    wall = time.perf_counter() - wall0
+    ms_per_step = ms / args.steps
+    value = lb["total"] / (ms_per_step * 1e-3) / 1e9
+    log(f"timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step (wall {wall * 1e3 / args.steps:.2f} us/step)")
+
+    dk = dominant_kernel(layers, outs, stream, args.kernel_reps)
+    log(f"dominant kernel: {dk['us']:.3f} us/launch, {dk['gbs']:.1f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(layers, args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['cpu']})")
+
+    line = {
+        "metric": "Q4_K matvec HBM GB/s (% of 8 TB/s) at M=1; prefill int8 MFMA TOPS at M=512",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: weights N(0,0.02) quantized on device (bit-exact from_float), activations N(0,1)",
+        "config": {"workload": "C2: Llama-3-8B decode layer, 7 products at M=1 (q/k/v/o/gate/up Q4_K, down Q6_K)",
+                   "rows": 1, "layer_bytes": lb["total"], "weight_copies": args.copies,
+                   "percent_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(dk["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": dk["kernel"], "us_per_launch": round(dk["us"], 4),
+                     "alg_bytes_per_launch": dk["alg_bytes"]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
