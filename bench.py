@@ -90,25 +90,36 @@ def make_acts():
     acts = {}
     for i, (g, k, _) in enumerate(GROUPS):
         x = fill_normal(k, seed=(CONFIG_SEED << 40) | (0xA0 + i)).reshape(1, k)
-        xq = torch.empty(L.qmm_act_bytes(ACT_Q8K, k, 1), dtype=torch.uint8, device="cuda")
-        acts[g] = (x, xq)
+        ws = torch.empty(L.qmm_act_bytes(ACT_Q8K, k, 1), dtype=torch.uint8, device="cuda")
+        acts[g] = (x, ws)
     outs = {name: torch.empty((1, n), dtype=torch.float32, device="cuda") for name, _, n, _ in LAYER}
     return acts, outs
 
 
 def enqueue_step(layer: Layer, outs: dict, stream: int) -> None:
-    """The layer's launches: per group one activation quantization, then its matvecs."""
+    """The layer's products: per group of weights sharing an activation one
+    qmm_forward_shared (QMatMul::forward_shared), or qmm_forward for one."""
     from swarmllm_amd._lib import check, lib
 
     L = lib()
     shape = {name: (t, n, k) for name, t, n, k in LAYER}
+    need = ctypes.c_size_t(0)
     for g, k, names in GROUPS:
-        x, xq = layer.acts[g]
-        check("qmm_quantize_act", L.qmm_quantize_act(x.data_ptr(), xq.data_ptr(), ACT_Q8K, k, 1, k, stream))
-        for name in names:
-            t, n, _ = shape[name]
-            check("qmm_matvec", L.qmm_matvec(t, layer.w[name].data_.data_ptr(), xq.data_ptr(),
-                                             outs[name].data_ptr(), n, k, n, 1, stream))
+        x, ws = layer.acts[g]
+        t = shape[names[0]][0]
+        if len(names) == 1:
+            name = names[0]
+            _, n, _ = shape[name]
+            check("qmm_forward", L.qmm_forward(t, layer.w[name].data_.data_ptr(), x.data_ptr(), k,
+                                               outs[name].data_ptr(), n, ws.data_ptr(), ws.numel(),
+                                               ctypes.byref(need), k, n, 1, 1, stream))
+            continue
+        cnt = len(names)
+        wp = (ctypes.c_void_p * cnt)(*[layer.w[nm].data_.data_ptr() for nm in names])
+        ns = (ctypes.c_int64 * cnt)(*[shape[nm][1] for nm in names])
+        dp = (ctypes.c_void_p * cnt)(*[outs[nm].data_ptr() for nm in names])
+        check("qmm_forward_shared", L.qmm_forward_shared(t, cnt, wp, ns, dp, ns, x.data_ptr(), k, ws.data_ptr(),
+                                                         ws.numel(), ctypes.byref(need), k, 1, 1, stream))
 
 
 def capture(fn, stream):
@@ -163,22 +174,26 @@ def time_gpu(fn, stream) -> float:
 
 
 def dominant_kernel(layers, outs, stream, reps: int) -> dict:
-    """The gate projection's Q4_K matvec alone, back to back over the copies
-    (activation already quantized), in one graph: its average launch."""
+    """The step's dominant launch, the gate+up products (two Q4_K 14336x4096
+    weights sharing one activation: one streaming launch quantizing the
+    activation in LDS), back to back over the copies in one graph: its
+    average launch, timed with HIP events on the stream it runs on."""
     from swarmllm_amd._lib import check, lib
 
     L = lib()
-    x, xq = layers[0].acts["ffn_in"]
+    x, ws = layers[0].acts["ffn_in"]
     n, k = 14336, 4096
-    s = stream.cuda_stream
-    check("qmm_quantize_act", L.qmm_quantize_act(x.data_ptr(), xq.data_ptr(), ACT_Q8K, k, 1, k, s))
     per_graph = 4 * len(layers)
+    need = ctypes.c_size_t(0)
+    ns = (ctypes.c_int64 * 2)(n, n)
+    dp = (ctypes.c_void_p * 2)(outs["gate"].data_ptr(), outs["up"].data_ptr())
 
     def fn(st):
         for i in range(per_graph):
             lay = layers[i % len(layers)]
-            check("qmm_matvec", L.qmm_matvec(Q4K, lay.w["gate"].data_.data_ptr(), xq.data_ptr(),
-                                             outs["gate"].data_ptr(), n, k, n, 1, st))
+            wp = (ctypes.c_void_p * 2)(lay.w["gate"].data_.data_ptr(), lay.w["up"].data_.data_ptr())
+            check("qmm_forward_shared", L.qmm_forward_shared(Q4K, 2, wp, ns, dp, ns, x.data_ptr(), k, ws.data_ptr(),
+                                                             ws.numel(), ctypes.byref(need), k, 1, 1, st))
 
     g = capture(fn, stream)
     for _ in range(3):
@@ -186,10 +201,10 @@ def dominant_kernel(layers, outs, stream, reps: int) -> dict:
     ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
     launches = reps * per_graph
     us = ms * 1e3 / launches
-    alg = 14336 * 16 * 144 + 4 * 4096 + 4 * 14336
+    alg = 2 * 14336 * 16 * 144 + 4 * 4096 + 2 * 4 * 14336
     gbs = alg / (us * 1e-6) / 1e9
-    return {"kernel": "mv_q4k_kernel<1,4> (Q4_K matvec, M=1, 14336x4096)", "us": us, "launches": launches,
-            "alg_bytes": alg, "gbs": gbs}
+    return {"kernel": "mv_q4k_stream_kernel<1,1,FUSED,16,PF> (gate+up: two Q4_K 14336x4096, M=1, one launch)",
+            "us": us, "launches": launches, "alg_bytes": alg, "gbs": gbs}
 
 
 def cpu_baseline(layers, budget_s: float) -> dict:

@@ -109,6 +109,21 @@ int qmm_forward(int type, const void *w, const float *x, int64_t x_stride, float
                 void *workspace, size_t workspace_bytes, size_t *need, int64_t k, int64_t n, int64_t rows,
                 int launch, int64_t stream);
 
+/* dst[i] = x · W[i]ᵀ for `count` weights of one type and the same k that
+ * share the activation x (rows x k f32, `x_stride` floats apart): the
+ * activation is quantized once for all of them. Weight i has n[i] rows and
+ * writes dst[i] with leading dimension ldd[i]. For Q4_K at 1-2 rows the
+ * products run as one launch per 4 weights, each quantizing the activation
+ * in LDS (workspace unused); otherwise the activation is quantized once into
+ * the workspace and each weight's product reads it. Plan (launch == 0) and
+ * launch as qmm_forward. Replaces QMatMul::forward_shared with the CUDA
+ * arm's shared activation (quantized/mod.rs:1221-1263,
+ * quantized/cuda.rs:622-720). */
+int qmm_forward_shared(int type, int count, const void *const *w, const int64_t *n, float *const *dst,
+                       const int64_t *ldd, const float *x, int64_t x_stride, void *workspace,
+                       size_t workspace_bytes, size_t *need, int64_t k, int64_t rows, int launch,
+                       int64_t stream);
+
 /* Dequantize `nelem` values of weight type `type` into f32 (out_f16 == 0)
  * or IEEE f16 (out_f16 != 0; each value is f16 of the f32 one).
  * Replaces QCudaStorage::dequantize / dequantize_f16

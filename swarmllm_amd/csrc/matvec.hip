@@ -34,7 +34,6 @@ __global__ __launch_bounds__(256) void mv_q4k_kernel(const uint8_t* __restrict__
   const int j = lane & 3;
   const int64_t k = (int64_t)nsb * 256;
   const int64_t rb = (int64_t)nsb * 144;
-  const int sh = 16 * (j & 1);
   float acc[NR][RPW];
 #pragma unroll
   for (int r = 0; r < NR; r++)
@@ -51,57 +50,28 @@ __global__ __launch_bounds__(256) void mv_q4k_kernel(const uint8_t* __restrict__
       qa[i] = *(const uint4*)(blk + 16 + 32 * j);
       qb[i] = *(const uint4*)(blk + 32 + 32 * j);
     }
-    // per row: d, dmin and the scale/min of sub-blocks 2j, 2j+1
-    float dx[RPW], mx[RPW];
-    int sc0[RPW], sc1[RPW], m0[RPW], m1[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      dx[i] = h2f((uint16_t)(hdr[i].x & 0xFFFF));
-      mx[i] = h2f((uint16_t)(hdr[i].x >> 16));
-      const uint32_t u0 = hdr[i].y, u1 = hdr[i].z, u2 = hdr[i].w;
-      uint32_t scw, mw;
-      if (j < 2) {
-        scw = u0 & 0x3f3f3f3fu;
-        mw = u1 & 0x3f3f3f3fu;
-      } else {
-        scw = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
-        mw = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
-      }
-      sc0[i] = (scw >> sh) & 0xFF;
-      sc1[i] = (scw >> (sh + 8)) & 0xFF;
-      m0[i] = (mw >> sh) & 0xFF;
-      m1[i] = (mw >> (sh + 8)) & 0xFF;
-    }
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       const int4* yp = (const int4*)(yq + r * k + (int64_t)sb * 256 + 64 * j);
-      const int4 y0 = yp[0], y1 = yp[1], y2 = yp[2], y3 = yp[3];
-      const int yv[16] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w,
-                          y2.x, y2.y, y2.z, y2.w, y3.x, y3.y, y3.z, y3.w};
+      int yv[16];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int4 v = yp[q];
+        yv[4 * q] = v.x; yv[4 * q + 1] = v.y; yv[4 * q + 2] = v.z; yv[4 * q + 3] = v.w;
+      }
       const float dy = yd[r * nsb + sb];
       const int2 bb = *(const int2*)(ybs + (r * nsb + sb) * 16 + 4 * j);
-      const int bs0 = (int)(int16_t)(bb.x & 0xFFFF) + (int)(int16_t)((uint32_t)bb.x >> 16);
-      const int bs1 = (int)(int16_t)(bb.y & 0xFFFF) + (int)(int16_t)((uint32_t)bb.y >> 16);
+      const int p0 = (int)(int16_t)(bb.x & 0xFFFF) + (int)(int16_t)((uint32_t)bb.x >> 16);
+      const int p1 = (int)(int16_t)(bb.y & 0xFFFF) + (int)(int16_t)((uint32_t)bb.y >> 16);
 #pragma unroll
-      for (int i = 0; i < RPW; i++) {
-        const uint32_t w[8] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w, qb[i].x, qb[i].y, qb[i].z, qb[i].w};
-        int slo = 0, shi = 0;
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-          slo = dot4((int)(w[t] & 0x0F0F0F0Fu), yv[t], slo);
-          shi = dot4((int)((w[t] >> 4) & 0x0F0F0F0Fu), yv[8 + t], shi);
-        }
-        const float main = dx[i] * (float)(sc0[i] * slo + sc1[i] * shi);
-        const float mins = mx[i] * (float)(m0[i] * bs0 + m1[i] * bs1);
-        acc[r][i] += dy * (main - mins);
-      }
+      for (int i = 0; i < RPW; i++) acc[r][i] = q4k_unit(hdr[i], qa[i], qb[i], yv, dy, p0, p1, j, acc[r][i]);
     }
   }
 #pragma unroll
   for (int r = 0; r < NR; r++)
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
-      const float v = wave_sum(acc[r][i]);
+      const float v = wave_sum_dpp(acc[r][i]);
       if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
     }
 }

@@ -1,0 +1,326 @@
+// mv_q4k.hip — Q4_K decode matvec (1-2 activation rows) for gfx950.
+//
+// Arithmetic: candle's Q4_K x Q8_K vec_dot
+// (vendor/candle/candle-core/src/quantized/k_quants.rs:2031-2111):
+//   per super-block  d*dy * sum_j sc_j * sum_{32} q*y  -  dmin*dy * sum_j m_j * (bsum_2j + bsum_2j+1)
+// with every inner sum an exact int32 (v_dot4_i32_i8) and f32 scaling.
+//
+// Shape of the work: a streaming kernel. Each wave walks weight rows
+// gw, gw + W, gw + 2W, ... (gw its index among the W waves of the grid) and
+// (with PF) keeps the next row's loads in flight while it computes one, so
+// the VALU work of a row runs under the transfer of the next instead of
+// piling up after the last byte lands (a kernel that loads everything first
+// and computes after spends that compute as a tail: ~1.7 us per SIMD for a
+// 33 MB Q4_K matrix at 4 cycles per wave64 instruction).
+//
+// Lane L of a wave owns the 64-value unit (super-block sb = L/4 + 16t,
+// chunk j = L%4: sub-blocks 2j, 2j+1) of every row, so its slice of the
+// activation is the same for every row and lives in registers: the
+// workgroup quantizes the f32 activation into LDS once (FUSED; the codes,
+// scales and group sums of BlockQ8K::from_float bit for bit, through the
+// q8k_block_group16 the standalone quantizer runs) or copies pre-quantized
+// planes there, and each lane then takes its slice. Per row a lane loads the
+// 16-byte header and its 32 code bytes of each of its super-blocks.
+//
+// One launch may cover up to kMaxTargets weights of the same k that share
+// the activation (QMatMul::forward_shared, quantized/mod.rs:1221-1263): the
+// rows of the targets are numbered one after another.
+#include "qmm_device.h"
+#include "qmm_launch.h"
+
+namespace qmm {
+
+namespace {
+
+
+struct Lds {
+  int8_t* codes;  // [NR][k]
+  float* dy;      // [NR][nsb]
+  int32_t* mp;    // [NR][nsb][8]: code sums of each 32-value sub-block (bsum_2j + bsum_2j+1)
+};
+
+__host__ __device__ inline size_t lds_layout(int nr, int nsb, size_t* off_dy, size_t* off_mp) {
+  const size_t k = (size_t)nsb * 256;
+  const size_t a = (size_t)nr * k;
+  const size_t b = (a + (size_t)nr * nsb * 4 + 15) / 16 * 16;
+  *off_dy = a;
+  *off_mp = b;
+  return b + (size_t)nr * nsb * 32;
+}
+
+// The activation part of LDS: FUSED quantizes the f32 rows, else copies
+// pre-quantized planes. A pass of a wave covers four Q8_K blocks, one per
+// group of 16 lanes (lane gl of a group holds values 16gl..16gl+15 of its
+// block); pass p of wave w covers blocks 4(p*kWaves + w) .. +3 of the
+// NR x nsb blocks. The loads of the first kPasses passes are issued before
+// the weight loads (ActBatch::load) so that waiting for them does not mean
+// waiting for HBM; further passes load and store one after another.
+constexpr int kPasses = 2;
+
+template <int NR, bool FUSED, int kWaves>
+struct ActBatch {
+  uint4 v[kPasses][4];  // FUSED: 16 f32 values; else [0] = 16 codes, [1].x = d bits, [1].y = sum of the 16
+
+  __device__ __forceinline__ static int block_of(int pass, int wv) {
+    return (pass * kWaves + wv) * 4 + ((threadIdx.x & 63) >> 4);
+  }
+
+  __device__ __forceinline__ static void load_pass(uint4 (&v)[4], int b, int nsb, const float* __restrict__ x,
+                                                   int64_t xstride, const int8_t* __restrict__ yq,
+                                                   const float* __restrict__ yd, const int16_t* __restrict__ ybs) {
+    const int gl = threadIdx.x & 15;
+    if (b >= NR * nsb) return;
+    const int r = b / nsb, sb = b - r * nsb;
+    if (FUSED) {
+      // rows 16-byte aligned (the launcher checks x and xstride)
+      const uint4* xp = (const uint4*)(x + r * xstride + sb * 256 + 16 * gl);
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = xp[i];
+    } else {
+      const int k = nsb * 256;
+      v[0] = *(const uint4*)(yq + (int64_t)r * k + sb * 256 + 16 * gl);
+      v[1].x = __float_as_uint(yd[r * nsb + sb]);
+      v[1].y = (uint32_t)(int32_t)ybs[(r * nsb + sb) * 16 + gl];
+    }
+  }
+
+  __device__ __forceinline__ void load(int nsb, const float* x, int64_t xstride, const int8_t* yq, const float* yd,
+                                       const int16_t* ybs) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int p = 0; p < kPasses; p++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[p][i] = make_uint4(0, 0, 0, 0);
+      if ((p * kWaves + wv) * 4 < NR * nsb) load_pass(v[p], block_of(p, wv), nsb, x, xstride, yq, yd, ybs);
+    }
+  }
+
+  // every lane of the wave calls (the quantizer's shuffles span the groups)
+  __device__ __forceinline__ static void store_pass(const Lds& s, const uint4 (&v)[4], int b, int nsb, float qmax) {
+    const int gl = threadIdx.x & 15;
+    uint32_t c[4];
+    int32_t sum16;
+    float d;
+    if (FUSED) {
+      float f[16];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        f[4 * i] = __uint_as_float(v[i].x); f[4 * i + 1] = __uint_as_float(v[i].y);
+        f[4 * i + 2] = __uint_as_float(v[i].z); f[4 * i + 3] = __uint_as_float(v[i].w);
+      }
+      q8k_block_group16(f, gl, qmax, c, sum16, d);
+    } else {
+      c[0] = v[0].x; c[1] = v[0].y; c[2] = v[0].z; c[3] = v[0].w;
+      d = __uint_as_float(v[1].x);
+      sum16 = (int32_t)v[1].y;
+    }
+    // sums of 16 -> sums of each 32-value sub-block (lanes 2j, 2j+1 of the group)
+    const int32_t pair = sum16 + __shfl_xor(sum16, 1, kWave);
+    if (b >= NR * nsb) return;
+    const int k = nsb * 256;
+    const int r = b / nsb, sb = b - r * nsb;
+    *(uint4*)(s.codes + r * k + sb * 256 + 16 * gl) = make_uint4(c[0], c[1], c[2], c[3]);
+    if ((gl & 1) == 0) s.mp[(r * nsb + sb) * 8 + (gl >> 1)] = pair;
+    if (gl == 0) s.dy[r * nsb + sb] = d;
+  }
+
+  __device__ __forceinline__ void store(const Lds& s, int nsb, const float* x, int64_t xstride, const int8_t* yq,
+                                        const float* yd, const int16_t* ybs, float qmax) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int p = 0; p < kPasses; p++)
+      if ((p * kWaves + wv) * 4 < NR * nsb) store_pass(s, v[p], block_of(p, wv), nsb, qmax);
+    for (int p = kPasses; (p * kWaves + wv) * 4 < NR * nsb; p++) {
+      uint4 t[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+      load_pass(t, block_of(p, wv), nsb, x, xstride, yq, yd, ybs);
+      store_pass(s, t, block_of(p, wv), nsb, qmax);
+    }
+  }
+};
+
+// A row's bytes for one lane: per super-block t, the header and the 32 code bytes of chunk j.
+template <int T>
+struct RowRegs {
+  uint4 h[T], qa[T], qb[T];
+};
+
+template <int T>
+__device__ __forceinline__ void load_row(RowRegs<T>& rr, const uint8_t* __restrict__ row, int nsb, int lane) {
+  const int j = lane & 3, sbl = lane >> 2;
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const int sb = sbl + 16 * t;
+    if (sb < nsb) {
+      const uint8_t* blk = row + sb * 144;
+      rr.h[t] = *(const uint4*)blk;
+      rr.qa[t] = *(const uint4*)(blk + 16 + 32 * j);
+      rr.qb[t] = *(const uint4*)(blk + 32 + 32 * j);
+    } else {
+      rr.h[t] = rr.qa[t] = rr.qb[t] = make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+// A lane's slice of one activation row: the 64 codes of its unit per
+// super-block t, dy, and the code sums of sub-blocks 2j, 2j+1.
+template <int T>
+struct ActRegs {
+  int y[T][16];
+  float dy[T];
+  int32_t p0[T], p1[T];
+};
+
+template <int NR, int T, bool FUSED, int kWaves, bool PF>
+__global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
+                                                            int64_t xstride, const int8_t* __restrict__ yq,
+                                                            const float* __restrict__ yd,
+                                                            const int16_t* __restrict__ ybs, float qmax) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  size_t o_dy, o_mp;
+  lds_layout(NR, nsb, &o_dy, &o_mp);
+  Lds s;
+  s.codes = (int8_t*)smem;
+  s.dy = (float*)(smem + o_dy);
+  s.mp = (int32_t*)(smem + o_mp);
+
+  // the wave index is uniform: rows, targets and pointers stay scalar
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 3, sbl = lane >> 2;
+  const int k = nsb * 256;
+  const int64_t rowbytes = (int64_t)nsb * 144;
+  const int64_t n_total = tg.row_end[tg.count - 1];
+  const int64_t W = (int64_t)gridDim.x * kWaves;
+  const int64_t gw = (int64_t)blockIdx.x * kWaves + wv;
+
+  auto row_ptr = [&](int64_t R, float*& out, int64_t& ldd) -> const uint8_t* {
+    int t = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxTargets - 1; i++)
+      if (i < tg.count - 1 && R >= tg.row_end[i]) t = i + 1;
+    const int64_t lrow = R - (t ? tg.row_end[t - 1] : 0);
+    out = tg.dst[t] + lrow;
+    ldd = tg.ldd[t];
+    return (const uint8_t*)tg.w[t] + lrow * rowbytes;
+  };
+
+  // 1. activation loads, then the first row's weight loads
+  ActBatch<NR, FUSED, kWaves> act;
+  act.load(nsb, x, xstride, yq, yd, ybs);
+  RowRegs<T> cur;
+  float* out = nullptr;
+  int64_t ldd = 0;
+  if (gw < n_total) load_row<T>(cur, row_ptr(gw, out, ldd), nsb, lane);
+
+  // 2. the activation into LDS, then each lane's slice into registers
+  act.store(s, nsb, x, xstride, yq, yd, ybs, qmax);
+  __syncthreads();
+  ActRegs<T> a[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const int sb = sbl + 16 * t;
+      if (sb < nsb) {
+        const int4* yp = (const int4*)(s.codes + r * k + sb * 256 + 64 * j);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int4 v = yp[q];
+          a[r].y[t][4 * q] = v.x; a[r].y[t][4 * q + 1] = v.y; a[r].y[t][4 * q + 2] = v.z; a[r].y[t][4 * q + 3] = v.w;
+        }
+        a[r].dy[t] = s.dy[r * nsb + sb];
+        a[r].p0[t] = s.mp[(r * nsb + sb) * 8 + 2 * j];
+        a[r].p1[t] = s.mp[(r * nsb + sb) * 8 + 2 * j + 1];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 16; q++) a[r].y[t][q] = 0;
+        a[r].dy[t] = 0.0f;
+        a[r].p0[t] = a[r].p1[t] = 0;
+      }
+    }
+
+  // 3. stream the rows
+  for (int64_t R = gw; R < n_total; R += W) {
+    // PF: the next row's loads go out before this row's compute
+    RowRegs<T> nxt;
+    float* nout = nullptr;
+    int64_t nldd = 0;
+    if (PF && R + W < n_total) load_row<T>(nxt, row_ptr(R + W, nout, nldd), nsb, lane);
+
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int r = 0; r < NR; r++)
+        acc[r] = q4k_unit(cur.h[t], cur.qa[t], cur.qb[t], a[r].y[t], a[r].dy[t], a[r].p0[t], a[r].p1[t], j, acc[r]);
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const float v = wave_sum_dpp(acc[r]);
+      if (lane == 0) out[r * ldd] = v;
+    }
+    if (PF) {
+      cur = nxt;
+      out = nout;
+      ldd = nldd;
+    } else if (R + W < n_total) {
+      load_row<T>(cur, row_ptr(R + W, out, ldd), nsb, lane);
+    }
+  }
+}
+
+template <int NR, int T, int WPG, bool PF>
+hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
+                         float qmax, int64_t waves, hipStream_t st) {
+  size_t a, b;
+  const size_t lds = lds_layout(NR, nsb, &a, &b);
+  const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
+  if (pre)
+    mv_q4k_stream_kernel<NR, T, false, WPG, PF><<<grid, 64 * WPG, lds, st>>>(t, nsb, nullptr, 0, pre->codes, pre->d,
+                                                                          (const int16_t*)pre->sums, qmax);
+  else
+    mv_q4k_stream_kernel<NR, T, true, WPG, PF><<<grid, 64 * WPG, lds, st>>>(t, nsb, x, xstride, nullptr, nullptr,
+                                                                         nullptr, qmax);
+  return hipGetLastError();
+}
+
+template <int NR, int T>
+hipError_t launch_shape(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
+                        float qmax, const MvShape& sh, hipStream_t st) {
+  if (sh.wpg == 16)
+    return sh.prefetch ? launch_stream<NR, T, 16, true>(t, nsb, x, xstride, pre, qmax, sh.waves, st)
+                       : launch_stream<NR, T, 16, false>(t, nsb, x, xstride, pre, qmax, sh.waves, st);
+  return sh.prefetch ? launch_stream<NR, T, 4, true>(t, nsb, x, xstride, pre, qmax, sh.waves, st)
+                     : launch_stream<NR, T, 4, false>(t, nsb, x, xstride, pre, qmax, sh.waves, st);
+}
+
+}  // namespace
+
+bool mv_q4k_rows_supported(int64_t k, int64_t rows) {
+  return rows >= 1 && rows <= 2 && k % 256 == 0 && k >= 256 && k <= (rows == 1 ? 16384 : 8192);
+}
+
+bool mv_q4k_rows_fusable(const float* x, int64_t xstride) {
+  return ((uintptr_t)x & 15) == 0 && xstride % 4 == 0;
+}
+
+// Waves in the grid: each wave streams about `per_wave` weight rows.
+int64_t mv_q4k_rows_waves(int64_t n_total, int per_wave) {
+  const int64_t w = (n_total + per_wave - 1) / per_wave;
+  return (w + 15) / 16 * 16;
+}
+
+hipError_t launch_mv_q4k_rows(const MvTargets& t, int64_t k, int64_t rows, const float* x, int64_t xstride,
+                              const ActPlanes* pre, float qmax, const MvShape& sh, hipStream_t st) {
+  const int nsb = (int)(k / 256);
+  const int T = (nsb + 15) / 16;
+  if (rows == 1) {
+    if (T <= 1) return launch_shape<1, 1>(t, nsb, x, xstride, pre, qmax, sh, st);
+    if (T <= 2) return launch_shape<1, 2>(t, nsb, x, xstride, pre, qmax, sh, st);
+    return launch_shape<1, 4>(t, nsb, x, xstride, pre, qmax, sh, st);
+  }
+  if (T <= 1) return launch_shape<2, 1>(t, nsb, x, xstride, pre, qmax, sh, st);
+  return launch_shape<2, 2>(t, nsb, x, xstride, pre, qmax, sh, st);
+}
+
+}  // namespace qmm

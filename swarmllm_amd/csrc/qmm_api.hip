@@ -56,6 +56,55 @@ bool shape_ok(int type, int64_t k, int64_t n, int64_t rows) {
   return qk != 0 && k > 0 && k % qk == 0 && n > 0 && rows > 0 && k <= (int64_t)1 << 30 && n <= ((int64_t)1 << 31) - 1;
 }
 
+// Compute units of the current device (256 on an MI355X), read once per device.
+int cu_count() {
+  static std::mutex mu;
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cached[dev]) {
+    hipDeviceProp_t prop;
+    cached[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0
+                      ? prop.multiProcessorCount
+                      : 256;
+    (void)hipGetLastError();
+  }
+  return cached[dev];
+}
+
+// Launch shape of the streaming Q4_K kernel for n_total weight rows: 16-wave
+// workgroups, up to 32 waves per CU, about 1.5 rows per wave where the rows
+// are few; the next row is prefetched when a wave has 3 or more rows.
+qmm::MvShape q4k_shape(int64_t n_total) {
+  const int64_t cap = (int64_t)cu_count() * 32;
+  int64_t waves = n_total * 2 / 3;
+  if (waves < 1024) waves = 1024;
+  if (waves > cap) waves = cap;
+  waves = (waves + 15) / 16 * 16;
+  return qmm::MvShape{waves, 16, n_total >= 3 * waves};
+}
+
+// One streaming launch over up to kMaxTargets weights (Q4_K, 1-2 rows).
+hipError_t launch_q4k_targets(int count, const void* const* w, const int64_t* n, float* const* dst,
+                              const int64_t* ldd, int64_t k, int64_t rows, const float* x, int64_t x_stride,
+                              const qmm::ActPlanes* pre, hipStream_t st) {
+  qmm::MvTargets t{};
+  int64_t end = 0;
+  for (int i = 0; i < count; i++) {
+    t.w[i] = w[i];
+    t.dst[i] = dst[i];
+    t.ldd[i] = ldd[i];
+    end += n[i];
+    t.row_end[i] = end;
+  }
+  t.count = count;
+  return qmm::launch_mv_q4k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), q4k_shape(end), st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -128,7 +177,11 @@ int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd,
   const int layout = qmm_act_layout(type, rows);
   const qmm::ActPlanes p = qmm::act_planes(layout, (void*)xq, k, rows);
   clear_stale_error();
-  const hipError_t e = qmm::launch_matvec(type, w, n, k, p, rows, dst, ldd, (hipStream_t)stream);
+  hipError_t e;
+  if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, rows))
+    e = launch_q4k_targets(1, &w, &n, &dst, &ldd, k, rows, nullptr, 0, &p, (hipStream_t)stream);
+  else
+    e = qmm::launch_matvec(type, w, n, k, p, rows, dst, ldd, (hipStream_t)stream);
   if (e == hipSuccess) g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
   return status_of(e);
 }
@@ -145,15 +198,78 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   if (!w || !x || !dst) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
+  if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
+    // the activation is quantized inside the product's own launch
+    const hipError_t e = launch_q4k_targets(1, &w, &n, &dst, &ldd, k, rows, x, x_stride, nullptr, st);
+    if (e != hipSuccess) return QMM_DEVICE_ERROR;
+    g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
+    return QMM_OK;
+  }
   hipError_t e = qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st);
   if (e != hipSuccess) return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
   const int64_t step = qmm::matvec_max_rows();
   for (int64_t r0 = 0; r0 < rows; r0 += step) {
     const int64_t nr = rows - r0 < step ? rows - r0 : step;
-    e = qmm::launch_matvec(type, w, n, k, qmm::act_rows(layout, p, k, r0), nr, dst + r0 * ldd, ldd, st);
+    const qmm::ActPlanes pr = qmm::act_rows(layout, p, k, r0);
+    if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, nr)) {
+      float* d = dst + r0 * ldd;
+      e = launch_q4k_targets(1, &w, &n, &d, &ldd, k, nr, nullptr, 0, &pr, st);
+    } else {
+      e = qmm::launch_matvec(type, w, n, k, pr, nr, dst + r0 * ldd, ldd, st);
+    }
     if (e != hipSuccess) return QMM_DEVICE_ERROR;
     g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
+  }
+  return QMM_OK;
+}
+
+int qmm_forward_shared(int type, int count, const void* const* w, const int64_t* n, float* const* dst,
+                       const int64_t* ldd, const float* x, int64_t x_stride, void* workspace, size_t workspace_bytes,
+                       size_t* need, int64_t k, int64_t rows, int launch, int64_t stream) {
+  if (count < 1 || !w || !n || !dst || !ldd || need == nullptr || x_stride < k) return QMM_UNSUPPORTED;
+  for (int i = 0; i < count; i++)
+    if (!shape_ok(type, k, n[i], rows) || ldd[i] < n[i]) return QMM_UNSUPPORTED;
+  const int layout = qmm_act_layout(type, rows);
+  const size_t bytes = qmm::act_bytes(layout, k, rows);
+  *need = bytes;
+  if (!launch) return QMM_OK;
+  if (g_fail_next.exchange(false)) return QMM_NO_ROOM;
+  if (!x) return QMM_UNSUPPORTED;
+  for (int i = 0; i < count; i++)
+    if (!w[i] || !dst[i]) return QMM_UNSUPPORTED;
+  const hipStream_t st = (hipStream_t)stream;
+  clear_stale_error();
+  if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
+    // one launch per kMaxTargets weights, each quantizing the activation in LDS
+    for (int i0 = 0; i0 < count; i0 += qmm::kMaxTargets) {
+      const int c = count - i0 < qmm::kMaxTargets ? count - i0 : qmm::kMaxTargets;
+      if (launch_q4k_targets(c, w + i0, n + i0, dst + i0, ldd + i0, k, rows, x, x_stride, nullptr, st) != hipSuccess)
+        return QMM_DEVICE_ERROR;
+      g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
+    }
+    return QMM_OK;
+  }
+  // otherwise: the activation quantized once into the workspace, then each product
+  if (workspace_bytes < bytes || workspace == nullptr) return QMM_WORKSPACE_TOO_SMALL;
+  if (qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st) != hipSuccess)
+    return QMM_DEVICE_ERROR;
+  const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
+  const int64_t step = qmm::matvec_max_rows();
+  for (int i = 0; i < count; i++) {
+    for (int64_t r0 = 0; r0 < rows; r0 += step) {
+      const int64_t nr = rows - r0 < step ? rows - r0 : step;
+      const qmm::ActPlanes pr = qmm::act_rows(layout, p, k, r0);
+      hipError_t e;
+      if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, nr)) {
+        float* d = dst[i] + r0 * ldd[i];
+        e = launch_q4k_targets(1, w + i, n + i, &d, ldd + i, k, nr, nullptr, 0, &pr, st);
+      } else {
+        e = qmm::launch_matvec(type, w[i], n[i], k, pr, nr, dst[i] + r0 * ldd[i], ldd[i], st);
+      }
+      if (e != hipSuccess) return QMM_DEVICE_ERROR;
+      g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
+    }
   }
   return QMM_OK;
 }

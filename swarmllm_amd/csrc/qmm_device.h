@@ -114,15 +114,72 @@ __device__ __forceinline__ int32_t nearest_int(float v) { return rs_as_i32(round
 __device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 // ---- wave64 reductions ----------------------------------------------------
+// Sum over the 64 lanes: DPP within rows of 16, then the four row sums, in a
+// fixed order (every decode kernel of a format reduces with this one, so a
+// row's result does not depend on which kernel or batch width computed it).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));   // quad 1,0,3,2
+  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));   // quad 2,3,0,1
+  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));  // half mirror
+  v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // mirror
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return __fadd_rn(__fadd_rn(a, b), __fadd_rn(c, d));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
   return v;
 }
-__device__ __forceinline__ int32_t sum_in_group4(int32_t v) {  // lanes 4g..4g+3
-  v += __shfl_xor(v, 1, kWave);
-  v += __shfl_xor(v, 2, kWave);
-  return v;
+
+// ---- activation quantizer -------------------------------------------------
+// Q8_K (BlockQ8K::from_float, k_quants.rs:2882-2927) of one 256-value block
+// held by a group of 16 lanes (gl = lane within the group, 0..15), lane gl
+// holding values 16gl..16gl+15 in v[0..15]. The block's scale value is the
+// signed value of the FIRST element of largest |x| (strict <), found in one
+// 4-step reduction as the maximum of the key
+// (|x| bits, 0xFFFF - index, sign): |x| orders as its bits (NaN never
+// qualifies, as `amax < |x|` is false for it), the lower index wins a tie,
+// and the sign rides along. Returns the lane's 16 codes packed in c[0..3],
+// their sum (the reference's bsums entry gl) and d. All 64 lanes must call.
+__device__ __forceinline__ void q8k_block_group16(const float v[16], int gl, float qmax, uint32_t c[4],
+                                                  int32_t& sum16, float& d) {
+#pragma clang fp contract(off)
+  float amax = 0.0f;
+  int first = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const float a = fabsf(v[i]);
+    if (amax < a) { amax = a; first = i; }
+  }
+  uint32_t hi = __float_as_uint(amax);
+  uint32_t lo = amax != 0.0f
+                    ? ((uint32_t)(0xFFFF - (16 * gl + first)) << 1) | (__float_as_uint(v[first]) >> 31)
+                    : 0u;
+#pragma unroll
+  for (int m = 1; m <= 8; m <<= 1) {
+    const uint32_t ohi = (uint32_t)__shfl_xor((int)hi, m, kWave);
+    const uint32_t olo = (uint32_t)__shfl_xor((int)lo, m, kWave);
+    if (ohi > hi || (ohi == hi && olo > lo)) { hi = ohi; lo = olo; }
+  }
+  amax = __uint_as_float(hi);
+  sum16 = 0;
+  d = 0.0f;
+  c[0] = c[1] = c[2] = c[3] = 0u;
+  if (amax != 0.0f) {
+    const float mx = (lo & 1u) ? -amax : amax;
+    const float iscale = -qmax / mx;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int q = rs_as_i8(rs_min(roundf(iscale * v[i]), 127.0f));
+      c[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
+      sum16 += q;
+    }
+    d = 1.0f / iscale;
+  }
 }
 
 // Q4_K 6-bit scale/min of sub-block j (k_quants utils.rs:50-60).
@@ -138,6 +195,36 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& d, in
 
 __device__ __forceinline__ int32_t dot4(int32_t a, int32_t b, int32_t c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// One 64-value unit of a Q4_K x Q8_K product (k_quants.rs:2031-2111): chunk
+// j (sub-blocks 2j, 2j+1) of a super-block with header h (d, dmin, scales)
+// and code bytes qa, qb (qs[32j .. 32j+31]), against the activation's 64
+// codes y (values 64j .. 64j+63 of the block), its d (dy) and the code sums
+// of the two sub-blocks (p0, p1). Adds dy*(d*sum_sc - dmin*sum_m) to acc with
+// every f32 operation rounded explicitly, so each decode kernel that calls it
+// gets the same bits for a unit.
+__device__ __forceinline__ float q4k_unit(uint4 h, uint4 qa, uint4 qb, const int y[16], float dy, int32_t p0,
+                                          int32_t p1, int j, float acc) {
+  const int sh = 16 * (j & 1);
+  const uint32_t u0 = h.y, u1 = h.z, u2 = h.w;
+  const uint32_t scw = j < 2 ? (u0 & 0x3f3f3f3fu) : ((u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4));
+  const uint32_t mw = j < 2 ? (u1 & 0x3f3f3f3fu) : (((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4));
+  const int sc0 = (int)((scw >> sh) & 0xFF), sc1 = (int)((scw >> (sh + 8)) & 0xFF);
+  const int m0 = (int)((mw >> sh) & 0xFF), m1 = (int)((mw >> (sh + 8)) & 0xFF);
+  const float dx = h2f((uint16_t)(h.x & 0xFFFF));
+  const float mx = h2f((uint16_t)(h.x >> 16));
+  const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+  int slo = 0, shi = 0;
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    slo = dot4((int)(w[q] & 0x0F0F0F0Fu), y[q], slo);
+    shi = dot4((int)((w[q] >> 4) & 0x0F0F0F0Fu), y[8 + q], shi);
+  }
+  // |slo|, |shi| <= 16*15*127 and |p| <= 32*127: 24-bit products are exact
+  const float main = __fmul_rn(dx, (float)(__mul24(sc0, slo) + __mul24(sc1, shi)));
+  const float mins = __fmul_rn(mx, (float)(__mul24(m0, p0) + __mul24(m1, p1)));
+  return __fmaf_rn(dy, __fsub_rn(main, mins), acc);
 }
 
 }  // namespace qmm

@@ -46,6 +46,35 @@ hipError_t launch_matvec(int type, const void* w, int64_t n, int64_t k, const Ac
 // The planes of rows [r0, ...) of an activation laid out for `total_rows`.
 ActPlanes act_rows(int layout, const ActPlanes& p, int64_t k, int64_t r0);
 int matvec_max_rows();
+
+// ---- weights sharing one activation (QMatMul::forward_shared) -------------
+// Up to kMaxTargets weights of the same type and k, whose rows one launch
+// numbers one after another: target t holds rows [row_end[t-1], row_end[t]).
+constexpr int kMaxTargets = 4;
+struct MvTargets {
+  const void* w[kMaxTargets];
+  float* dst[kMaxTargets];
+  int64_t ldd[kMaxTargets];
+  int64_t row_end[kMaxTargets];
+  int count;
+};
+
+// Q4_K decode matvec over 1-2 activation rows, streaming: `waves` waves
+// each walk about n_total/waves weight rows with the next row's loads in
+// flight. Quantizes the f32 activation in LDS (pre == nullptr; rows 16-byte
+// aligned, see mv_q4k_rows_fusable) or reads pre-quantized Q8_K planes.
+bool mv_q4k_rows_supported(int64_t k, int64_t rows);
+bool mv_q4k_rows_fusable(const float* x, int64_t xstride);
+// Launch shape: waves in the grid, waves per workgroup (4 or 16), and
+// whether a wave prefetches its next row before computing the current one.
+struct MvShape {
+  int64_t waves;
+  int wpg;
+  bool prefetch;
+};
+int64_t mv_q4k_rows_waves(int64_t n_total, int per_wave);
+hipError_t launch_mv_q4k_rows(const MvTargets& t, int64_t k, int64_t rows, const float* x, int64_t xstride,
+                              const ActPlanes* pre, float qmax, const MvShape& sh, hipStream_t s);
 hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
 
 }  // namespace qmm

@@ -62,58 +62,41 @@ ActPlanes act_rows(int layout, const ActPlanes& p, int64_t k, int64_t r0) {
 }
 
 // ===========================================================================
-// Q8_K activation (per 256): one wave per block, 4 values per lane.
+// Q8_K activation (per 256): 16 lanes per block (16 values per lane), four
+// blocks per wave, through q8k_block_group16 (the routine the fused decode
+// kernels run in LDS).
 // ===========================================================================
 template <bool kVec>
 __global__ __launch_bounds__(256) void act_q8k_kernel(const float* __restrict__ x, int64_t stride, int64_t k,
                                                       int64_t rows, int8_t* __restrict__ codes,
                                                       float* __restrict__ dout, int16_t* __restrict__ bsout,
                                                       float qmax) {
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, gl = lane & 15;
   const int64_t nbk = k / 256;
-  const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (blk >= rows * nbk) return;  // whole wave
-  const int64_t r = blk / nbk, b = blk - r * nbk;
-  const float* xp = x + r * stride + b * 256 + 4 * lane;
-  float v[4];
+  const int64_t blk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  const bool valid = blk < rows * nbk;  // every lane takes part in the shuffles
+  const int64_t bb = valid ? blk : 0;
+  const int64_t r = bb / nbk, b = bb - r * nbk;
+  const float* xp = x + r * stride + b * 256 + 16 * gl;
+  float v[16];
   if (kVec) {
-    const float4 t = *(const float4*)xp;
-    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = xp[i];
-  }
-  // the first element with the largest |x| (strict <): its signed value
-  float amax = 0.0f, mx = 0.0f;
-  int idx = 0x7fffffff;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float a = fabsf(v[i]);
-    if (amax < a) { amax = a; mx = v[i]; idx = 4 * lane + i; }
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float oa = __shfl_xor(amax, m, kWave);
-    const float om = __shfl_xor(mx, m, kWave);
-    const int oi = __shfl_xor(idx, m, kWave);
-    if (oa > amax || (oa == amax && oi < idx)) { amax = oa; mx = om; idx = oi; }
-  }
-  int32_t packed = 0, gsum = 0;
-  float d = 0.0f;
-  if (amax != 0.0f) {
-    const float iscale = -qmax / mx;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int q = rs_as_i8(rs_min(roundf(iscale * v[i]), 127.0f));
-      packed |= (q & 0xFF) << (8 * i);
-      gsum += q;
+      const float4 t = ((const float4*)xp)[i];
+      v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
     }
-    d = 1.0f / iscale;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = xp[i];
   }
-  gsum = sum_in_group4(gsum);
-  ((int32_t*)(codes + r * k + b * 256))[lane] = packed;
-  if (lane == 0) dout[r * nbk + b] = d;
-  if ((lane & 3) == 0) bsout[r * (k / 16) + b * 16 + (lane >> 2)] = (int16_t)gsum;
+  uint32_t c[4];
+  int32_t sum16;
+  float d;
+  q8k_block_group16(v, gl, qmax, c, sum16, d);
+  if (!valid) return;
+  *(uint4*)(codes + r * k + b * 256 + 16 * gl) = make_uint4(c[0], c[1], c[2], c[3]);
+  bsout[r * (k / 16) + b * 16 + gl] = (int16_t)sum16;
+  if (gl == 0) dout[r * nbk + b] = d;
 }
 
 // ===========================================================================
@@ -179,7 +162,7 @@ hipError_t launch_act_quantize(int layout, const float* x, int64_t stride, int64
   const bool vec = ((uintptr_t)x % 16 == 0) && (stride % 4 == 0);
   if (layout == ACT_Q8K) {
     const int64_t blocks = rows * (k / 256);
-    const dim3 grid((unsigned)((blocks + 3) / 4));
+    const dim3 grid((unsigned)((blocks + 15) / 16));
     if (vec)
       act_q8k_kernel<true><<<grid, 256, 0, st>>>(x, stride, k, rows, p.codes, p.d, (int16_t*)p.sums, q8k_scale);
     else

@@ -169,29 +169,42 @@ class QMatMul:
 
     @staticmethod
     def forward_shared(xs: torch.Tensor, ws: Sequence["QMatMul"]) -> List[torch.Tensor]:
-        """Several weights against ONE activation, quantized once where their
-        activation layouts agree (mod.rs:1221-1263)."""
+        """Several weights against ONE activation, quantized once for all of
+        them (mod.rs:1221-1263): one qmm_forward_shared call per group of
+        weights of the same type; a single weight is a plain forward."""
         if len(ws) <= 1:
             return [w.forward(xs) for w in ws]
         k = ws[0].qtensor.shape[1]
-        if any(w.qtensor.shape[1] != k for w in ws) or xs.shape[-1] != k or not xs.is_contiguous():
-            return [w.forward(xs) for w in ws]
+        if any(w.qtensor.shape[1] != k for w in ws):
+            raise ValueError("forward_shared: every weight must have the activation's k")
+        if xs.dim() < 1 or xs.shape[-1] != k:
+            raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with k={k}")
+        if xs.dtype != torch.float32:
+            raise ValueError("Expected f32")
+        if not xs.is_contiguous():
+            raise ValueError(f"input tensor is not contiguous {tuple(xs.shape)}")
         rows = xs.numel() // k
+        outs = [torch.empty((*xs.shape[:-1], w.qtensor.shape[0]), dtype=torch.float32, device=xs.device)
+                for w in ws]
+        if rows == 0:
+            return outs
         L = lib()
-        layouts = {L.qmm_act_layout(int(w.qtensor.dtype), rows) for w in ws}
-        if len(layouts) != 1 or rows > L.qmm_matvec_max_rows():
-            return [w.forward(xs) for w in ws]
-        layout = layouts.pop()
         st = _stream()
-        xq = torch.empty(L.qmm_act_bytes(layout, k, rows), dtype=torch.uint8, device=xs.device)
-        check("qmm_quantize_act", L.qmm_quantize_act(_ptr(xs), _ptr(xq), layout, k, rows, k, st))
-        outs = []
-        for w in ws:
-            n = w.qtensor.shape[0]
-            out = torch.empty((*xs.shape[:-1], n), dtype=torch.float32, device=xs.device)
-            check("qmm_matvec", L.qmm_matvec(int(w.qtensor.dtype), _ptr(w.qtensor.data_), _ptr(xq), _ptr(out), n,
-                                             k, n, rows, st))
-            outs.append(out)
+        by_type = {}
+        for i, w in enumerate(ws):
+            by_type.setdefault(int(w.qtensor.dtype), []).append(i)
+        for t, idx in by_type.items():
+            cnt = len(idx)
+            wp = (ctypes.c_void_p * cnt)(*[ws[i].qtensor.data_.data_ptr() for i in idx])
+            ns = (ctypes.c_int64 * cnt)(*[ws[i].qtensor.shape[0] for i in idx])
+            dp = (ctypes.c_void_p * cnt)(*[outs[i].data_ptr() for i in idx])
+            ld = (ctypes.c_int64 * cnt)(*[ws[i].qtensor.shape[0] for i in idx])
+            need = ctypes.c_size_t(0)
+            check("qmm_forward_shared", L.qmm_forward_shared(t, cnt, wp, ns, dp, ld, _ptr(xs), k, None, 0,
+                                                             ctypes.byref(need), k, rows, 0, st))
+            buf = ws[idx[0]]._ws.get(need.value, xs.device)
+            check("qmm_forward_shared", L.qmm_forward_shared(t, cnt, wp, ns, dp, ld, _ptr(xs), k, _ptr(buf),
+                                                             buf.numel(), ctypes.byref(need), k, rows, 1, st))
         return outs
 
 

@@ -220,14 +220,64 @@ def test_forward_shape_rules_and_batch_invariance():
         mm.forward(x.transpose(0, 1))
 
 
-def test_forward_shared_equals_forward():
-    k = 1024
-    rng = np.random.default_rng(9)
-    mats = [QMatMul(qtensor_from_oracle(qref.Q4_K, weights(rng, n, k))[0]) for n in (96, 32, 32)]
-    x = upload(rng.standard_normal((3, k)).astype(np.float32))
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows", [1, 2, 3])
+def test_forward_shared_equals_forward(name, rows):
+    """forward_shared (qmm_forward_shared) returns what each weight's own
+    forward returns, bit for bit: more weights than one launch takes (6 > 4),
+    ragged row counts, odd ones."""
+    qtype = TYPES[name]
+    k = 1024 if qtype in (12, 14) else 2880
+    rng = np.random.default_rng(9 + rows)
+    mats = [QMatMul(qtensor_from_oracle(qtype, weights(rng, n, k))[0]) for n in (96, 32, 33, 1, 160, 7)]
+    x = upload(rng.standard_normal((rows, k)).astype(np.float32))
     shared = QMatMul.forward_shared(x, mats)
     for m, y in zip(mats, shared):
         assert torch.equal(y, m.forward(x))
+
+
+@pytest.mark.parametrize("k", [256, 1024, 4096, 8192, 14336, 16384])
+@pytest.mark.parametrize("rows", [1, 2])
+def test_q4k_in_kernel_quantization_matches_standalone(k, rows):
+    """The decode kernel quantizing its activation in LDS gives the same bits
+    as the same kernel reading the standalone quantizer's planes (which are
+    bit-exact to BlockQ8K::from_float): the in-kernel quantization is that
+    quantization. Also within tolerance of the oracle."""
+    if rows == 2 and k > 8192:
+        pytest.skip("two rows stream up to k = 8192")
+    n = 300
+    rng = np.random.default_rng(k + rows)
+    w = weights(rng, n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[0, :256] = special_rows(256)[3]  # ties in |x| of both signs
+    qt, wq = qtensor_from_oracle(qref.Q4_K, w)
+    xt = upload(x)
+    fused = QMatMul(qt).forward(xt)
+    L = lib()
+    xq = quantize_act(xt, _lib.ACT_Q8K)
+    pre = torch.empty((rows, n), dtype=torch.float32, device=DEV)
+    st = L.qmm_matvec(qref.Q4_K, qt.data_.data_ptr(), xq.data_ptr(), pre.data_ptr(), n, k, n, rows,
+                      torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    assert torch.equal(fused, pre)
+    want = qref.matmul(qref.Q4_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q4_K, wq, n * k).reshape(n, k)
+    assert normalised_error(fused.cpu().numpy(), want, wdeq, x) <= TOL_MATVEC
+
+
+def test_q4k_unaligned_activation_takes_the_quantize_then_product_path():
+    """An activation that is not 16-byte aligned goes through the standalone
+    quantizer and the same product kernel: the same bits as aligned."""
+    k, n = 1024, 64
+    rng = np.random.default_rng(11)
+    qt, _ = qtensor_from_oracle(qref.Q4_K, weights(rng, n, k))
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    base = upload(np.concatenate([np.zeros(1, np.float32), x.ravel()]))
+    xs = base[1:].reshape(1, k)  # 4 bytes past the allocation's alignment
+    assert xs.data_ptr() % 16 == 4
+    y_unaligned = QMatMul(qt).forward(xs)
+    y_aligned = QMatMul(qt).forward(upload(x))
+    assert torch.equal(y_unaligned, y_aligned)
 
 
 def test_full_size_decode_gate_projection():
