@@ -10,8 +10,7 @@
 //
 // Weights are read in GGUF bytes. The activation comes in the planes of
 // qmm_launch.h (codes / scales / group sums, 16-byte aligned).
-#include "qmm_device.h"
-#include "qmm_launch.h"
+#include "mv_common.h"
 
 namespace qmm {
 
@@ -75,52 +74,6 @@ __global__ __launch_bounds__(256) void mv_q4k_kernel(const uint8_t* __restrict__
       if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
     }
 }
-
-// ===========================================================================
-// LDS staging for formats whose blocks are not 16-byte aligned. A wave
-// copies a span of a weight row (4096 values) into its own LDS region with
-// linear 16-byte loads from the 16-byte boundary at or before the span's
-// first byte. Every 16-byte piece read holds at least one byte of the row,
-// and a 16-byte aligned piece never crosses a page, so the over-read at
-// either end stays inside mapped memory.
-// ===========================================================================
-constexpr int kSpanMaxBytes = 4352;                  // 128 Q8_0 blocks, the largest span
-constexpr int kStageBytes = kSpanMaxBytes + 16 + 16; // + alignment slack + over-read
-
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Copies bytes [start, start+len) of W into lds; returns the LDS offset of `start`.
-__device__ __forceinline__ int stage_span(const uint8_t* __restrict__ W, int64_t start, int len, uint8_t* lds,
-                                          int lane) {
-  const int64_t a0 = start & ~(int64_t)15;
-  const int pieces = (int)((start + len - a0 + 15) >> 4);
-  for (int p = lane; p < pieces; p += 64) *(uint4*)(lds + 16 * p) = *(const uint4*)(W + a0 + 16 * p);
-  return (int)(start - a0);
-}
-
-// 4 bytes from LDS at any byte offset (two aligned dword reads + alignbyte).
-__device__ __forceinline__ uint32_t lds_u32(const uint8_t* lds, int off) {
-  const int a = off & ~3;
-  const uint32_t lo = *(const uint32_t*)(lds + a);
-  const uint32_t hi = *(const uint32_t*)(lds + a + 4);
-  return __builtin_amdgcn_alignbyte(hi, lo, (uint32_t)(off & 3));
-}
-// n consecutive dwords from LDS at any byte offset.
-template <int N>
-__device__ __forceinline__ void lds_words(const uint8_t* lds, int off, uint32_t* out) {
-  const int a = off & ~3;
-  const uint32_t s = (uint32_t)(off & 3);
-  uint32_t w[N + 1];
-#pragma unroll
-  for (int i = 0; i <= N; i++) w[i] = *(const uint32_t*)(lds + a + 4 * i);
-#pragma unroll
-  for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], s);
-}
-__device__ __forceinline__ uint32_t lds_u16(const uint8_t* lds, int off) { return lds_u32(lds, off) & 0xFFFF; }
 
 // 16-entry int8 table lookup of the 4 nibbles in the bytes of n (each < 16).
 __device__ __forceinline__ int32_t lut16(uint32_t n, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
@@ -202,24 +155,11 @@ __global__ __launch_bounds__(256) void mv_q6k_kernel(const uint8_t* __restrict__
         const int4 bq = *(const int4*)(ybs + (r * nsb + sb) * 16 + 8 * h);  // bsums 8h .. 8h+7
         const uint32_t bw[4] = {(uint32_t)bq.x, (uint32_t)bq.y, (uint32_t)bq.z, (uint32_t)bq.w};
         const int bsh = 16 * (l0 >> 4);
+        int bs[4];
 #pragma unroll
-        for (int i = 0; i < RPW; i++) {
-          int tot = 0;
+        for (int t = 0; t < 4; t++) bs[t] = (int)(int16_t)((bw[t] >> bsh) & 0xFFFF);
 #pragma unroll
-          for (int t = 0; t < 4; t++) {
-            const uint32_t* ql = (t & 1) ? qlB[i] : qlA[i];
-            const int nsh = 4 * (t >> 1);
-            int s = 0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-              const uint32_t q6 = ((ql[q] >> nsh) & 0x0F0F0F0Fu) | (((qh[i][q] >> (2 * t)) & 0x03030303u) << 4);
-              s = dot4((int)q6, yv[t][q], s);
-            }
-            const int bs = (int)(int16_t)((bw[t] >> bsh) & 0xFFFF);
-            tot += sc[i][t] * (s - 32 * bs);
-          }
-          acc[r][i] += (dx[i] * dy) * (float)tot;
-        }
+        for (int i = 0; i < RPW; i++) acc[r][i] = q6k_unit(qlA[i], qlB[i], qh[i], sc[i], dx[i], yv, dy, bs, acc[r][i]);
       }
     }
   }
@@ -227,7 +167,7 @@ __global__ __launch_bounds__(256) void mv_q6k_kernel(const uint8_t* __restrict__
   for (int r = 0; r < NR; r++)
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
-      const float v = wave_sum(acc[r][i]);
+      const float v = wave_sum_dpp(acc[r][i]);
       if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
     }
 }

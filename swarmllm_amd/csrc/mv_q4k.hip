@@ -25,118 +25,12 @@
 // One launch may cover up to kMaxTargets weights of the same k that share
 // the activation (QMatMul::forward_shared, quantized/mod.rs:1221-1263): the
 // rows of the targets are numbered one after another.
-#include "qmm_device.h"
-#include "qmm_launch.h"
+#include "mv_common.h"
 
 namespace qmm {
 
 namespace {
 
-
-struct Lds {
-  int8_t* codes;  // [NR][k]
-  float* dy;      // [NR][nsb]
-  int32_t* mp;    // [NR][nsb][8]: code sums of each 32-value sub-block (bsum_2j + bsum_2j+1)
-};
-
-__host__ __device__ inline size_t lds_layout(int nr, int nsb, size_t* off_dy, size_t* off_mp) {
-  const size_t k = (size_t)nsb * 256;
-  const size_t a = (size_t)nr * k;
-  const size_t b = (a + (size_t)nr * nsb * 4 + 15) / 16 * 16;
-  *off_dy = a;
-  *off_mp = b;
-  return b + (size_t)nr * nsb * 32;
-}
-
-// The activation part of LDS: FUSED quantizes the f32 rows, else copies
-// pre-quantized planes. A pass of a wave covers four Q8_K blocks, one per
-// group of 16 lanes (lane gl of a group holds values 16gl..16gl+15 of its
-// block); pass p of wave w covers blocks 4(p*kWaves + w) .. +3 of the
-// NR x nsb blocks. The loads of the first kPasses passes are issued before
-// the weight loads (ActBatch::load) so that waiting for them does not mean
-// waiting for HBM; further passes load and store one after another.
-constexpr int kPasses = 2;
-
-template <int NR, bool FUSED, int kWaves>
-struct ActBatch {
-  uint4 v[kPasses][4];  // FUSED: 16 f32 values; else [0] = 16 codes, [1].x = d bits, [1].y = sum of the 16
-
-  __device__ __forceinline__ static int block_of(int pass, int wv) {
-    return (pass * kWaves + wv) * 4 + ((threadIdx.x & 63) >> 4);
-  }
-
-  __device__ __forceinline__ static void load_pass(uint4 (&v)[4], int b, int nsb, const float* __restrict__ x,
-                                                   int64_t xstride, const int8_t* __restrict__ yq,
-                                                   const float* __restrict__ yd, const int16_t* __restrict__ ybs) {
-    const int gl = threadIdx.x & 15;
-    if (b >= NR * nsb) return;
-    const int r = b / nsb, sb = b - r * nsb;
-    if (FUSED) {
-      // rows 16-byte aligned (the launcher checks x and xstride)
-      const uint4* xp = (const uint4*)(x + r * xstride + sb * 256 + 16 * gl);
-#pragma unroll
-      for (int i = 0; i < 4; i++) v[i] = xp[i];
-    } else {
-      const int k = nsb * 256;
-      v[0] = *(const uint4*)(yq + (int64_t)r * k + sb * 256 + 16 * gl);
-      v[1].x = __float_as_uint(yd[r * nsb + sb]);
-      v[1].y = (uint32_t)(int32_t)ybs[(r * nsb + sb) * 16 + gl];
-    }
-  }
-
-  __device__ __forceinline__ void load(int nsb, const float* x, int64_t xstride, const int8_t* yq, const float* yd,
-                                       const int16_t* ybs) {
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-    for (int p = 0; p < kPasses; p++) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) v[p][i] = make_uint4(0, 0, 0, 0);
-      if ((p * kWaves + wv) * 4 < NR * nsb) load_pass(v[p], block_of(p, wv), nsb, x, xstride, yq, yd, ybs);
-    }
-  }
-
-  // every lane of the wave calls (the quantizer's shuffles span the groups)
-  __device__ __forceinline__ static void store_pass(const Lds& s, const uint4 (&v)[4], int b, int nsb, float qmax) {
-    const int gl = threadIdx.x & 15;
-    uint32_t c[4];
-    int32_t sum16;
-    float d;
-    if (FUSED) {
-      float f[16];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        f[4 * i] = __uint_as_float(v[i].x); f[4 * i + 1] = __uint_as_float(v[i].y);
-        f[4 * i + 2] = __uint_as_float(v[i].z); f[4 * i + 3] = __uint_as_float(v[i].w);
-      }
-      q8k_block_group16(f, gl, qmax, c, sum16, d);
-    } else {
-      c[0] = v[0].x; c[1] = v[0].y; c[2] = v[0].z; c[3] = v[0].w;
-      d = __uint_as_float(v[1].x);
-      sum16 = (int32_t)v[1].y;
-    }
-    // sums of 16 -> sums of each 32-value sub-block (lanes 2j, 2j+1 of the group)
-    const int32_t pair = sum16 + __shfl_xor(sum16, 1, kWave);
-    if (b >= NR * nsb) return;
-    const int k = nsb * 256;
-    const int r = b / nsb, sb = b - r * nsb;
-    *(uint4*)(s.codes + r * k + sb * 256 + 16 * gl) = make_uint4(c[0], c[1], c[2], c[3]);
-    if ((gl & 1) == 0) s.mp[(r * nsb + sb) * 8 + (gl >> 1)] = pair;
-    if (gl == 0) s.dy[r * nsb + sb] = d;
-  }
-
-  __device__ __forceinline__ void store(const Lds& s, int nsb, const float* x, int64_t xstride, const int8_t* yq,
-                                        const float* yd, const int16_t* ybs, float qmax) {
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-    for (int p = 0; p < kPasses; p++)
-      if ((p * kWaves + wv) * 4 < NR * nsb) store_pass(s, v[p], block_of(p, wv), nsb, qmax);
-    for (int p = kPasses; (p * kWaves + wv) * 4 < NR * nsb; p++) {
-      uint4 t[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-      load_pass(t, block_of(p, wv), nsb, x, xstride, yq, yd, ybs);
-      store_pass(s, t, block_of(p, wv), nsb, qmax);
-    }
-  }
-};
 
 // A row's bytes for one lane: per super-block t, the header and the 32 code bytes of chunk j.
 template <int T>
@@ -176,12 +70,7 @@ __global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg
                                                             const float* __restrict__ yd,
                                                             const int16_t* __restrict__ ybs, float qmax) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  size_t o_dy, o_mp;
-  lds_layout(NR, nsb, &o_dy, &o_mp);
-  Lds s;
-  s.codes = (int8_t*)smem;
-  s.dy = (float*)(smem + o_dy);
-  s.mp = (int32_t*)(smem + o_mp);
+  const ActLds s = act_lds(smem, NR, nsb);
 
   // the wave index is uniform: rows, targets and pointers stay scalar
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -228,8 +117,9 @@ __global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg
           a[r].y[t][4 * q] = v.x; a[r].y[t][4 * q + 1] = v.y; a[r].y[t][4 * q + 2] = v.z; a[r].y[t][4 * q + 3] = v.w;
         }
         a[r].dy[t] = s.dy[r * nsb + sb];
-        a[r].p0[t] = s.mp[(r * nsb + sb) * 8 + 2 * j];
-        a[r].p1[t] = s.mp[(r * nsb + sb) * 8 + 2 * j + 1];
+        const int32_t* g = s.s16 + (r * nsb + sb) * 16 + 4 * j;  // sub-blocks 2j, 2j+1 = groups 4j .. 4j+3
+        a[r].p0[t] = g[0] + g[1];
+        a[r].p1[t] = g[2] + g[3];
       } else {
 #pragma unroll
         for (int q = 0; q < 16; q++) a[r].y[t][q] = 0;
@@ -272,8 +162,7 @@ __global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg
 template <int NR, int T, int WPG, bool PF>
 hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
                          float qmax, int64_t waves, hipStream_t st) {
-  size_t a, b;
-  const size_t lds = lds_layout(NR, nsb, &a, &b);
+  const size_t lds = act_lds_bytes(NR, nsb);
   const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
   if (pre)
     mv_q4k_stream_kernel<NR, T, false, WPG, PF><<<grid, 64 * WPG, lds, st>>>(t, nsb, nullptr, 0, pre->codes, pre->d,

@@ -76,22 +76,34 @@ int cu_count() {
   return cached[dev];
 }
 
-// Launch shape of the streaming Q4_K kernel for n_total weight rows: 16-wave
-// workgroups, up to 32 waves per CU, about 1.5 rows per wave where the rows
-// are few; the next row is prefetched when a wave has 3 or more rows.
-qmm::MvShape q4k_shape(int64_t n_total) {
+// The streaming decode kernels (Q4_K, Q6_K at 1-2 activation rows).
+bool stream_supported(int type, int64_t k, int64_t rows) {
+  if (type == qmm::T_Q4_K) return qmm::mv_q4k_rows_supported(k, rows);
+  if (type == qmm::T_Q6_K) return qmm::mv_q6k_rows_supported(k, rows);
+  return false;
+}
+
+// Launch shape for n_total weight rows: up to 32 waves per CU, about 1.5
+// rows per wave where the rows are few, the next row prefetched when a wave
+// has 3 or more; 16-wave workgroups (one activation fill per 16 waves), or
+// fewer waves per group where a Q6_K group's LDS would pass 64 KiB.
+qmm::MvShape stream_shape(int type, int64_t k, int64_t rows, int64_t n_total) {
   const int64_t cap = (int64_t)cu_count() * 32;
   int64_t waves = n_total * 2 / 3;
   if (waves < 1024) waves = 1024;
   if (waves > cap) waves = cap;
   waves = (waves + 15) / 16 * 16;
-  return qmm::MvShape{waves, 16, n_total >= 3 * waves};
+  int wpg = 16;
+  if (type == qmm::T_Q6_K)
+    while (wpg > 4 && qmm::mv_q6k_rows_lds(k, rows, wpg) > 65536) wpg /= 2;
+  const int64_t units = type == qmm::T_Q6_K ? n_total * ((k / 256 + 15) / 16) : n_total;
+  return qmm::MvShape{waves, wpg, units >= 3 * waves};
 }
 
-// One streaming launch over up to kMaxTargets weights (Q4_K, 1-2 rows).
-hipError_t launch_q4k_targets(int count, const void* const* w, const int64_t* n, float* const* dst,
-                              const int64_t* ldd, int64_t k, int64_t rows, const float* x, int64_t x_stride,
-                              const qmm::ActPlanes* pre, hipStream_t st) {
+// One streaming launch over up to kMaxTargets weights.
+hipError_t launch_stream_targets(int type, int count, const void* const* w, const int64_t* n, float* const* dst,
+                                 const int64_t* ldd, int64_t k, int64_t rows, const float* x, int64_t x_stride,
+                                 const qmm::ActPlanes* pre, hipStream_t st) {
   qmm::MvTargets t{};
   int64_t end = 0;
   for (int i = 0; i < count; i++) {
@@ -102,7 +114,9 @@ hipError_t launch_q4k_targets(int count, const void* const* w, const int64_t* n,
     t.row_end[i] = end;
   }
   t.count = count;
-  return qmm::launch_mv_q4k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), q4k_shape(end), st);
+  const qmm::MvShape sh = stream_shape(type, k, rows, end);
+  if (type == qmm::T_Q6_K) return qmm::launch_mv_q6k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), sh, st);
+  return qmm::launch_mv_q4k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), sh, st);
 }
 
 }  // namespace
@@ -178,8 +192,8 @@ int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd,
   const qmm::ActPlanes p = qmm::act_planes(layout, (void*)xq, k, rows);
   clear_stale_error();
   hipError_t e;
-  if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, rows))
-    e = launch_q4k_targets(1, &w, &n, &dst, &ldd, k, rows, nullptr, 0, &p, (hipStream_t)stream);
+  if (stream_supported(type, k, rows))
+    e = launch_stream_targets(type, 1, &w, &n, &dst, &ldd, k, rows, nullptr, 0, &p, (hipStream_t)stream);
   else
     e = qmm::launch_matvec(type, w, n, k, p, rows, dst, ldd, (hipStream_t)stream);
   if (e == hipSuccess) g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
@@ -198,9 +212,9 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   if (!w || !x || !dst) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
-  if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
+  if (stream_supported(type, k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
     // the activation is quantized inside the product's own launch
-    const hipError_t e = launch_q4k_targets(1, &w, &n, &dst, &ldd, k, rows, x, x_stride, nullptr, st);
+    const hipError_t e = launch_stream_targets(type, 1, &w, &n, &dst, &ldd, k, rows, x, x_stride, nullptr, st);
     if (e != hipSuccess) return QMM_DEVICE_ERROR;
     g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
@@ -212,9 +226,9 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   for (int64_t r0 = 0; r0 < rows; r0 += step) {
     const int64_t nr = rows - r0 < step ? rows - r0 : step;
     const qmm::ActPlanes pr = qmm::act_rows(layout, p, k, r0);
-    if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, nr)) {
+    if (stream_supported(type, k, nr)) {
       float* d = dst + r0 * ldd;
-      e = launch_q4k_targets(1, &w, &n, &d, &ldd, k, nr, nullptr, 0, &pr, st);
+      e = launch_stream_targets(type, 1, &w, &n, &d, &ldd, k, nr, nullptr, 0, &pr, st);
     } else {
       e = qmm::launch_matvec(type, w, n, k, pr, nr, dst + r0 * ldd, ldd, st);
     }
@@ -240,11 +254,12 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
     if (!w[i] || !dst[i]) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
-  if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
+  if (stream_supported(type, k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
     // one launch per kMaxTargets weights, each quantizing the activation in LDS
     for (int i0 = 0; i0 < count; i0 += qmm::kMaxTargets) {
       const int c = count - i0 < qmm::kMaxTargets ? count - i0 : qmm::kMaxTargets;
-      if (launch_q4k_targets(c, w + i0, n + i0, dst + i0, ldd + i0, k, rows, x, x_stride, nullptr, st) != hipSuccess)
+      if (launch_stream_targets(type, c, w + i0, n + i0, dst + i0, ldd + i0, k, rows, x, x_stride, nullptr, st) !=
+          hipSuccess)
         return QMM_DEVICE_ERROR;
       g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
     }
@@ -261,9 +276,9 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
       const int64_t nr = rows - r0 < step ? rows - r0 : step;
       const qmm::ActPlanes pr = qmm::act_rows(layout, p, k, r0);
       hipError_t e;
-      if (type == qmm::T_Q4_K && qmm::mv_q4k_rows_supported(k, nr)) {
+      if (stream_supported(type, k, nr)) {
         float* d = dst[i] + r0 * ldd[i];
-        e = launch_q4k_targets(1, w + i, n + i, &d, ldd + i, k, nr, nullptr, 0, &pr, st);
+        e = launch_stream_targets(type, 1, w + i, n + i, &d, ldd + i, k, nr, nullptr, 0, &pr, st);
       } else {
         e = qmm::launch_matvec(type, w[i], n[i], k, pr, nr, dst[i] + r0 * ldd[i], ldd[i], st);
       }

@@ -227,4 +227,32 @@ __device__ __forceinline__ float q4k_unit(uint4 h, uint4 qa, uint4 qb, const int
   return __fmaf_rn(dy, __fsub_rn(main, mins), acc);
 }
 
+// One 64-value unit of a Q6_K x Q8_K product (k_quants.rs:2598-2655): half
+// h of a super-block, values 128h + 32t + l0 + [0,16) for t = 0..3 (l0 = 0
+// or 16). qlA = ql[64h + l0 ..], qlB = ql[64h + 32 + l0 ..], qh = qh[32h + l0 ..]
+// (16 bytes each, as 4 words), sc[t] = scales[8h + l0/16 + 2t], dx = d;
+// y[t] = the activation codes of group t, bs[t] their sum, dy the
+// activation block's d. Adds (dx*dy) * sum_t sc_t * sum (q-32)*y to acc with
+// every f32 operation rounded explicitly, so each decode kernel that calls it
+// gets the same bits for a unit.
+__device__ __forceinline__ float q6k_unit(const uint32_t qlA[4], const uint32_t qlB[4], const uint32_t qh[4],
+                                          const int sc[4], float dx, const int y[4][4], float dy, const int bs[4],
+                                          float acc) {
+  int tot = 0;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const uint32_t* ql = (t & 1) ? qlB : qlA;
+    const int nsh = 4 * (t >> 1);
+    int s = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t q6 = ((ql[q] >> nsh) & 0x0F0F0F0Fu) | (((qh[q] >> (2 * t)) & 0x03030303u) << 4);
+      s = dot4((int)q6, y[t][q], s);
+    }
+    // |s - 32*bs| <= 16*63*127 + 32*16*127 < 2^23: a 24-bit product is exact
+    tot += __mul24(sc[t], s - 32 * bs[t]);
+  }
+  return __fmaf_rn(__fmul_rn(dx, dy), (float)tot, acc);
+}
+
 }  // namespace qmm

@@ -202,9 +202,9 @@ def test_forward_beyond_the_matvec_rows(name, rows):
     assert normalised_error(y, want, wdeq, x) <= TOL_MATVEC
 
 
-def test_forward_shape_rules_and_batch_invariance():
-    """cpu_fwd's shape rules (mod.rs:1280-1333); a row's result does not depend
-    on the rows beside it (quantized_tests.rs:223-258)."""
+def test_forward_shape_rules():
+    """cpu_fwd's shape rules (mod.rs:1280-1333): leading dims kept, k checked,
+    contiguity required."""
     k, n = 512, 40
     rng = np.random.default_rng(8)
     qt, _ = qtensor_from_oracle(qref.Q4_K, weights(rng, n, k))
@@ -212,12 +212,28 @@ def test_forward_shape_rules_and_batch_invariance():
     x = upload(rng.standard_normal((2, 3, k)).astype(np.float32))
     y = mm.forward(x)
     assert tuple(y.shape) == (2, 3, n)
-    y1 = mm.forward(x[1, 2:3].contiguous())
-    assert torch.equal(y1[0], y[1, 2])
     with pytest.raises(ValueError):
         mm.forward(upload(np.zeros((1, k + 32), np.float32)))
     with pytest.raises(ValueError):
         mm.forward(x.transpose(0, 1))
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_batch_invariance(name):
+    """A row's result does not depend on the rows beside it, for every batch
+    width up to 8 (the reference's qmm_batch, quantized_tests.rs:223-258,
+    which asserts exact equality within its one-to-eight-row kernel), and
+    beyond 8 rows too (the chunks of 8 run the same per-row arithmetic)."""
+    qtype = TYPES[name]
+    k, n = (4096, 70) if qtype in (12, 14) else (2880, 70)
+    rng = np.random.default_rng(80 + qtype)
+    qt, _ = qtensor_from_oracle(qtype, weights(rng, n, k))
+    mm = QMatMul(qt)
+    xs = upload(rng.standard_normal((12, k)).astype(np.float32))
+    alone = mm.forward(xs[:1].contiguous())
+    for rows in (2, 3, 4, 5, 6, 7, 8, 9, 12):
+        y = mm.forward(xs[:rows].contiguous())
+        assert torch.equal(y[0], alone[0]), rows
 
 
 @pytest.mark.parametrize("name", list(TYPES))
