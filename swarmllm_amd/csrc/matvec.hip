@@ -102,13 +102,21 @@ __global__ __launch_bounds__(256) void mv_q6k_kernel(const uint8_t* __restrict__
   const int64_t k = (int64_t)nsb * 256;
   const int64_t rb = (int64_t)nsb * 210;
   const int u = lane & 3, h = u >> 1, l0 = 16 * (u & 1);
-  float acc[NR][RPW];
+  // per span of 16 super-blocks: one partial sum per (activation row, weight
+  // row), the partials added in span order (the arithmetic of the streaming
+  // kernel, which gives each span to its own wave)
+  float tot[NR][RPW];
 #pragma unroll
   for (int r = 0; r < NR; r++)
 #pragma unroll
-    for (int i = 0; i < RPW; i++) acc[r][i] = 0.0f;
+    for (int i = 0; i < RPW; i++) tot[r][i] = 0.0f;
 
   for (int s0 = 0; s0 < nsb; s0 += 16) {
+    float acc[NR][RPW];
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+      for (int i = 0; i < RPW; i++) acc[r][i] = 0.0f;
     const int nspan = nsb - s0 < 16 ? nsb - s0 : 16;
     int off[RPW];
     wave_lds_sync();  // the previous span's reads are done
@@ -162,14 +170,19 @@ __global__ __launch_bounds__(256) void mv_q6k_kernel(const uint8_t* __restrict__
         for (int i = 0; i < RPW; i++) acc[r][i] = q6k_unit(qlA[i], qlB[i], qh[i], sc[i], dx[i], yv, dy, bs, acc[r][i]);
       }
     }
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+      for (int i = 0; i < RPW; i++) {
+        const float p = wave_sum_dpp(acc[r][i]);
+        tot[r][i] = s0 == 0 ? p : __fadd_rn(tot[r][i], p);
+      }
   }
 #pragma unroll
   for (int r = 0; r < NR; r++)
 #pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      const float v = wave_sum_dpp(acc[r][i]);
-      if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
-    }
+    for (int i = 0; i < RPW; i++)
+      if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = tot[r][i];
 }
 
 // ===========================================================================

@@ -10,11 +10,10 @@
 // consecutive 16-byte pieces per instruction) into its own LDS buffer and
 // computes from there, one 64-value unit per lane (super-block sbl = L/4 of
 // the span, unit u = L%4: half h = u/2, l0 = 16*(u%2)), through the same
-// q6k_unit the multi-row kernel runs. Work items are (row, span); a wave
-// walks rows gw, gw + W, ... and their spans in order, and (PF) keeps the
-// next item's loads in flight in registers while it computes the current
-// one. The workgroup quantizes the f32 activation into LDS once (FUSED) or
-// copies pre-quantized planes there.
+// q6k_unit the multi-row kernel runs, and (PF) keeps its next span's loads in
+// flight in registers while it computes the current one. The workgroup
+// quantizes the f32 activation into LDS once (FUSED) or copies pre-quantized
+// planes there.
 //
 // One launch may cover up to kMaxTargets weights of the same k sharing the
 // activation (QMatMul::forward_shared, quantized/mod.rs:1221-1263).
@@ -26,9 +25,11 @@ namespace {
 
 constexpr int kSpanSb = 16;                            // super-blocks per span
 constexpr int kSpanBytes = kSpanSb * 210;              // 3360
-constexpr int kSpanPieces = (kSpanBytes + 15) / 16 + 1; // 16-byte pieces, start not aligned
+constexpr int kSpanPieces = (kSpanBytes + 15) / 16 + 1; // 16-byte pieces, start not aligned: 211
 constexpr int kPiecesPerLane = (kSpanPieces + 63) / 64; // 4
-constexpr int kSpanBuf = kPiecesPerLane * 64 * 16;     // LDS bytes per wave (>= pieces + alignbyte over-read)
+// LDS bytes per wave: the pieces, and the 8 bytes past the last that the
+// dword reads of lds_words may touch
+constexpr int kSpanBuf = kSpanPieces * 16 + 16;
 
 struct Span {
   uint4 p[kPiecesPerLane];
@@ -41,8 +42,11 @@ struct Span {
 // holds at least one byte of the span, and an aligned piece never crosses a
 // page, so the bytes read beyond the span stay in mapped memory.
 __device__ __forceinline__ void load_span(Span& sp, const uint8_t* __restrict__ p, int len, int lane) {
-  const uint8_t* a0 = (const uint8_t*)((uintptr_t)p & ~(uintptr_t)15);
-  sp.off = (int)(p - a0);
+  // rounded down by pointer arithmetic: the compiler keeps these global
+  // loads (an integer round trip would make them flat loads, which every LDS
+  // wait also waits for)
+  sp.off = (int)((uintptr_t)p & 15);
+  const uint8_t* a0 = p - sp.off;
   sp.len = len;
   const int pieces = (int)((sp.off + len * 210 + 15) >> 4);
 #pragma unroll
@@ -52,6 +56,14 @@ __device__ __forceinline__ void load_span(Span& sp, const uint8_t* __restrict__ 
   }
 }
 
+// Work: the spans of a row go to different waves of one workgroup. With
+// nspan spans per row, a workgroup of kWaves waves takes G = kWaves / nspan
+// rows at a time: wave wv works span wv % nspan of row-slot wv / nspan. Each
+// wave reduces its span's partial sum (wave_sum_dpp) into LDS; after the
+// workgroup barrier the span-0 wave of each row-slot adds the partials in
+// span order and writes the row. Row-slots walk the rows
+// (blockIdx.x + i * gridDim.x) * G + g, every wave of the grid the same
+// number of iterations (a wave without a row still meets the barriers).
 template <int NR, bool FUSED, int kWaves, bool PF>
 __global__ __launch_bounds__(64 * kWaves) void mv_q6k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
                                                                     int64_t xstride, const int8_t* __restrict__ yq,
@@ -60,145 +72,173 @@ __global__ __launch_bounds__(64 * kWaves) void mv_q6k_stream_kernel(MvTargets tg
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const ActLds s = act_lds(smem, NR, nsb);
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* buf = smem + (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + (size_t)wv * kSpanBuf;
+  uint8_t* const part_base = smem + (act_lds_bytes(NR, nsb) + 15) / 16 * 16;  // [2][kWaves][NR] floats
+  uint8_t* buf = part_base + 2 * kWaves * NR * 4 + (size_t)wv * kSpanBuf;
+  float* const part = (float*)part_base;
   const int k = nsb * 256;
   const int64_t rowbytes = (int64_t)nsb * 210;
   const int64_t n_total = tg.row_end[tg.count - 1];
-  const int64_t W = (int64_t)gridDim.x * kWaves;
-  const int64_t gw = (int64_t)blockIdx.x * kWaves + wv;
   const int nspan = (nsb + kSpanSb - 1) / kSpanSb;
-  const int64_t my_rows = gw < n_total ? (n_total - gw + W - 1) / W : 0;
-  const int64_t items = my_rows * nspan;
+  const int G = kWaves / nspan;  // rows per workgroup iteration
+  const int g = wv / nspan, span = wv - g * nspan;
+  const bool active = g < G;
+  const int s0 = span * kSpanSb;
+  const int len = nsb - s0 < kSpanSb ? nsb - s0 : kSpanSb;
+  const int64_t rows_per_iter = (int64_t)gridDim.x * G;
+  const int64_t iters = (n_total + rows_per_iter - 1) / rows_per_iter;
 
+  auto row_of = [&](int64_t i) -> int64_t { return ((int64_t)blockIdx.x + i * gridDim.x) * G + g; };
   auto row_ptr = [&](int64_t R, float*& out, int64_t& ldd) -> const uint8_t* {
     int t = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxTargets - 1; i++)
-      if (i < tg.count - 1 && R >= tg.row_end[i]) t = i + 1;
+    for (int q = 0; q < kMaxTargets - 1; q++)
+      if (q < tg.count - 1 && R >= tg.row_end[q]) t = q + 1;
     const int64_t lrow = R - (t ? tg.row_end[t - 1] : 0);
     out = tg.dst[t] + lrow;
     ldd = tg.ldd[t];
     return (const uint8_t*)tg.w[t] + lrow * rowbytes;
   };
-  auto load_item = [&](Span& sp, int64_t it, float*& out, int64_t& ldd) {
-    const int64_t R = gw + (it / nspan) * W;
-    const int s0 = (int)(it % nspan) * kSpanSb;
-    const uint8_t* row = row_ptr(R, out, ldd);
-    load_span(sp, row + (int64_t)s0 * 210, nsb - s0 < kSpanSb ? nsb - s0 : kSpanSb, lane);
-  };
 
-  // 1. activation loads, then the first item's weight loads
+  // 1. activation loads, then the first span's weight loads
   ActBatch<NR, FUSED, kWaves> act;
   act.load(nsb, x, xstride, yq, yd, ybs);
   Span cur;
   float* out = nullptr;
   int64_t ldd = 0;
-  if (items > 0) load_item(cur, 0, out, ldd);
+  if (active && row_of(0) < n_total) load_span(cur, row_ptr(row_of(0), out, ldd) + (int64_t)s0 * 210, len, lane);
 
   // 2. the activation into LDS
   act.store(s, nsb, x, xstride, yq, yd, ybs, qmax);
   __syncthreads();
 
-  // 3. stream the items
+  // 3. stream the rows
   const int sbl = lane >> 2, u = lane & 3, h = u >> 1, l0 = 16 * (u & 1);
-  float acc[NR];
-#pragma unroll
-  for (int r = 0; r < NR; r++) acc[r] = 0.0f;
-  for (int64_t it = 0; it < items; it++) {
-    const int span = (int)(it % nspan);
-    // the span into this wave's LDS buffer
-    wave_lds_sync();  // the previous item's reads are done
-#pragma unroll
-    for (int c = 0; c < kPiecesPerLane; c++) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
-    wave_lds_sync();
-    const int off = cur.off, len = cur.len;
+  for (int64_t i = 0; i < iters; i++) {
+    const int64_t R = row_of(i);
+    const bool have = active && R < n_total;
     float* cout = out;
     const int64_t cldd = ldd;
-
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) acc[r] = 0.0f;
     Span nxt;
-    if (PF && it + 1 < items) load_item(nxt, it + 1, out, ldd);
-
-    if (sbl < len) {
-      const int b = off + 210 * sbl;
-      uint32_t qlA[4], qlB[4], qh[4], s4[2];
-      lds_words<4>(buf, b + 64 * h + l0, qlA);
-      lds_words<4>(buf, b + 64 * h + 32 + l0, qlB);
-      lds_words<4>(buf, b + 128 + 32 * h + l0, qh);
-      lds_words<2>(buf, b + 192 + 8 * h, s4);  // scales 8h .. 8h+7
-      int sc[4];
+    if (have) {
+      // the span into this wave's LDS buffer
+      wave_lds_sync();  // the previous span's reads are done
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const int g = (l0 >> 4) + 2 * t;
-        sc[t] = (int)(int8_t)((s4[g >> 2] >> (8 * (g & 3))) & 0xFF);
-      }
-      const float dx = h2f((uint16_t)lds_u16(buf, b + 208));
-      const int sb = span * kSpanSb + sbl;
-#pragma unroll
-      for (int r = 0; r < NR; r++) {
-        const int8_t* yrow = s.codes + r * k + sb * 256 + 128 * h + l0;
-        int yv[4][4], bs[4];
+      for (int c = 0; c < kPiecesPerLane; c++)
+        if (lane + 64 * c < kSpanPieces) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
+      wave_lds_sync();
+      const int off = cur.off;
+      if (PF && row_of(i + 1) < n_total)
+        load_span(nxt, row_ptr(row_of(i + 1), out, ldd) + (int64_t)s0 * 210, len, lane);
+      if (sbl < len) {
+        const int b = off + 210 * sbl;
+        uint32_t qlA[4], qlB[4], qh[4], s4[2];
+        lds_words<4>(buf, b + 64 * h + l0, qlA);
+        lds_words<4>(buf, b + 64 * h + 32 + l0, qlB);
+        lds_words<4>(buf, b + 128 + 32 * h + l0, qh);
+        lds_words<2>(buf, b + 192 + 8 * h, s4);  // scales 8h .. 8h+7
+        int sc[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-          const int4 q = *(const int4*)(yrow + 32 * t);
-          yv[t][0] = q.x; yv[t][1] = q.y; yv[t][2] = q.z; yv[t][3] = q.w;
-          bs[t] = s.s16[(r * nsb + sb) * 16 + 8 * h + 2 * t + (l0 >> 4)];
+          const int gg = (l0 >> 4) + 2 * t;
+          sc[t] = (int)(int8_t)((s4[gg >> 2] >> (8 * (gg & 3))) & 0xFF);
         }
-        acc[r] = q6k_unit(qlA, qlB, qh, sc, dx, yv, s.dy[r * nsb + sb], bs, acc[r]);
+        const float dx = h2f((uint16_t)lds_u16(buf, b + 208));
+        const int sb = s0 + sbl;
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+          const int8_t* yrow = s.codes + r * k + sb * 256 + 128 * h + l0;
+          int yv[4][4], bs[4];
+#pragma unroll
+          for (int t = 0; t < 4; t++) {
+            const int4 q = *(const int4*)(yrow + 32 * t);
+            yv[t][0] = q.x; yv[t][1] = q.y; yv[t][2] = q.z; yv[t][3] = q.w;
+            bs[t] = s.s16[(r * nsb + sb) * 16 + 8 * h + 2 * t + (l0 >> 4)];
+          }
+          acc[r] = q6k_unit(qlA, qlB, qh, sc, dx, yv, s.dy[r * nsb + sb], bs, acc[r]);
+        }
       }
     }
-    if (span == nspan - 1) {
+    // partial sums of the spans, added in span order
+    float* slot = part + (i & 1) * kWaves * NR;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const float v = wave_sum_dpp(acc[r]);
+      if (lane == 0) slot[wv * NR + r] = v;
+    }
+    __syncthreads();
+    if (have && span == 0 && lane == 0) {
 #pragma unroll
       for (int r = 0; r < NR; r++) {
-        const float v = wave_sum_dpp(acc[r]);
-        if (lane == 0) cout[r * cldd] = v;
-        acc[r] = 0.0f;
+        float tot = slot[(g * nspan) * NR + r];
+        for (int q = 1; q < nspan; q++) tot = __fadd_rn(tot, slot[(g * nspan + q) * NR + r]);
+        cout[r * cldd] = tot;
       }
     }
     if (PF) {
       cur = nxt;
-    } else if (it + 1 < items) {
-      load_item(cur, it + 1, out, ldd);
+    } else if (active && row_of(i + 1) < n_total) {
+      load_span(cur, row_ptr(row_of(i + 1), out, ldd) + (int64_t)s0 * 210, len, lane);
     }
   }
 }
 
 template <int NR, int WPG, bool PF>
+size_t stream_lds(int nsb) {
+  return (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + 2 * WPG * NR * 4 + (size_t)WPG * kSpanBuf;
+}
+
+template <int NR, int WPG, bool PF>
 hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
                          float qmax, int64_t waves, hipStream_t st) {
-  const size_t lds = (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + (size_t)WPG * kSpanBuf;
+  const size_t lds = stream_lds<NR, WPG, PF>(nsb);
   const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
-  if (pre)
-    mv_q6k_stream_kernel<NR, false, WPG, PF><<<grid, 64 * WPG, lds, st>>>(t, nsb, nullptr, 0, pre->codes, pre->d,
-                                                                       (const int16_t*)pre->sums, qmax);
-  else
-    mv_q6k_stream_kernel<NR, true, WPG, PF><<<grid, 64 * WPG, lds, st>>>(t, nsb, x, xstride, nullptr, nullptr,
-                                                                      nullptr, qmax);
+  // dynamic LDS past 64 KiB needs the kernel's limit raised (to the 160 KiB
+  // of a CU), once per kernel
+  static bool raised[2] = {false, false};
+  if (pre) {
+    auto* kfn = &mv_q6k_stream_kernel<NR, false, WPG, PF>;
+    if (!raised[0]) {
+      if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+        return hipErrorInvalidValue;
+      raised[0] = true;
+    }
+    kfn<<<grid, 64 * WPG, lds, st>>>(t, nsb, nullptr, 0, pre->codes, pre->d, (const int16_t*)pre->sums, qmax);
+  } else {
+    auto* kfn = &mv_q6k_stream_kernel<NR, true, WPG, PF>;
+    if (!raised[1]) {
+      if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+        return hipErrorInvalidValue;
+      raised[1] = true;
+    }
+    kfn<<<grid, 64 * WPG, lds, st>>>(t, nsb, x, xstride, nullptr, nullptr, nullptr, qmax);
+  }
   return hipGetLastError();
 }
 
 template <int NR>
 hipError_t launch_shape(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
                         float qmax, const MvShape& sh, hipStream_t st) {
-  if (sh.wpg == 16)
-    return sh.prefetch ? launch_stream<NR, 16, true>(t, nsb, x, xstride, pre, qmax, sh.waves, st)
-                       : launch_stream<NR, 16, false>(t, nsb, x, xstride, pre, qmax, sh.waves, st);
-  if (sh.wpg == 8)
-    return sh.prefetch ? launch_stream<NR, 8, true>(t, nsb, x, xstride, pre, qmax, sh.waves, st)
-                       : launch_stream<NR, 8, false>(t, nsb, x, xstride, pre, qmax, sh.waves, st);
-  return sh.prefetch ? launch_stream<NR, 4, true>(t, nsb, x, xstride, pre, qmax, sh.waves, st)
-                     : launch_stream<NR, 4, false>(t, nsb, x, xstride, pre, qmax, sh.waves, st);
+  return sh.prefetch ? launch_stream<NR, 16, true>(t, nsb, x, xstride, pre, qmax, sh.waves, st)
+                     : launch_stream<NR, 16, false>(t, nsb, x, xstride, pre, qmax, sh.waves, st);
 }
 
 }  // namespace
 
-// LDS: the activation (NR x k codes + scales + sums) and one span buffer per
-// wave must fit the 160 KiB of a CU with a 16-wave workgroup.
+// LDS: the activation (rows x k codes + scales + sums) and one span buffer
+// per wave of a 16-wave workgroup, within a CU's 160 KiB; a row's spans must
+// fit the 16 waves.
 bool mv_q6k_rows_supported(int64_t k, int64_t rows) {
-  return rows >= 1 && rows <= 2 && k % 256 == 0 && k >= 256 && k * rows <= 32768;
+  return rows >= 1 && rows <= 2 && k % 256 == 0 && k >= 256 && k <= 16 * kSpanSb * 256 && k * rows <= 32768;
 }
 
+int mv_q6k_rows_per_group(int64_t k) { return 16 / (int)((k / 256 + kSpanSb - 1) / kSpanSb); }
+
 size_t mv_q6k_rows_lds(int64_t k, int64_t rows, int wpg) {
-  return (act_lds_bytes((int)rows, (int)(k / 256)) + 15) / 16 * 16 + (size_t)wpg * kSpanBuf;
+  const int nsb = (int)(k / 256);
+  return (act_lds_bytes((int)rows, nsb) + 15) / 16 * 16 + 2 * (size_t)wpg * rows * 4 + (size_t)wpg * kSpanBuf;
 }
 
 hipError_t launch_mv_q6k_rows(const MvTargets& t, int64_t k, int64_t rows, const float* x, int64_t xstride,

@@ -83,21 +83,29 @@ bool stream_supported(int type, int64_t k, int64_t rows) {
   return false;
 }
 
-// Launch shape for n_total weight rows: up to 32 waves per CU, about 1.5
-// rows per wave where the rows are few, the next row prefetched when a wave
-// has 3 or more; 16-wave workgroups (one activation fill per 16 waves), or
-// fewer waves per group where a Q6_K group's LDS would pass 64 KiB.
+// Launch shape for n_total weight rows. Q4_K: up to 32 waves per CU, about
+// 1.5 rows per wave where the rows are few, 16-wave workgroups (one
+// activation fill per 16 waves). Q6_K: 16-wave workgroups taking
+// mv_q6k_rows_per_group rows at a time, one workgroup per CU at most (each
+// workgroup fills the activation once, and further groups per CU cost more
+// in fills than they give in bytes in flight), the next span prefetched when
+// a workgroup has 2 or more rounds. Q4_K prefetches when a wave has 3 or
+// more rows.
 qmm::MvShape stream_shape(int type, int64_t k, int64_t rows, int64_t n_total) {
-  const int64_t cap = (int64_t)cu_count() * 32;
+  (void)rows;
+  const int64_t cus = cu_count();
+  if (type == qmm::T_Q6_K) {
+    const int64_t G = qmm::mv_q6k_rows_per_group(k);
+    int64_t groups = (n_total + G - 1) / G;
+    if (groups > cus) groups = cus;
+    const int64_t iters = (n_total + groups * G - 1) / (groups * G);
+    return qmm::MvShape{groups * 16, 16, iters >= 2};
+  }
   int64_t waves = n_total * 2 / 3;
   if (waves < 1024) waves = 1024;
-  if (waves > cap) waves = cap;
+  if (waves > cus * 32) waves = cus * 32;
   waves = (waves + 15) / 16 * 16;
-  int wpg = 16;
-  if (type == qmm::T_Q6_K)
-    while (wpg > 4 && qmm::mv_q6k_rows_lds(k, rows, wpg) > 65536) wpg /= 2;
-  const int64_t units = type == qmm::T_Q6_K ? n_total * ((k / 256 + 15) / 16) : n_total;
-  return qmm::MvShape{waves, wpg, units >= 3 * waves};
+  return qmm::MvShape{waves, 16, n_total >= 3 * waves};
 }
 
 // One streaming launch over up to kMaxTargets weights.
