@@ -230,6 +230,12 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   hipError_t e = qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st);
   if (e != hipSuccess) return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
+  if (type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && ((uintptr_t)w & 15) == 0) {
+    // prefill: the int8 matrix-core GEMM
+    if (qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
+    g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+    return QMM_OK;
+  }
   const int64_t step = qmm::matvec_max_rows();
   for (int64_t r0 = 0; r0 < rows; r0 += step) {
     const int64_t nr = rows - r0 < step ? rows - r0 : step;
@@ -280,6 +286,11 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
   const int64_t step = qmm::matvec_max_rows();
   for (int i = 0; i < count; i++) {
+    if (type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && ((uintptr_t)w[i] & 15) == 0) {
+      if (qmm::launch_gemm_q4k(w[i], n[i], k, p, rows, dst[i], ldd[i], st) != hipSuccess) return QMM_DEVICE_ERROR;
+      g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+      continue;
+    }
     for (int64_t r0 = 0; r0 < rows; r0 += step) {
       const int64_t nr = rows - r0 < step ? rows - r0 : step;
       const qmm::ActPlanes pr = qmm::act_rows(layout, p, k, r0);

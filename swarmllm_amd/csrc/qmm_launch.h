@@ -87,4 +87,11 @@ hipError_t launch_mv_q4k_rows(const MvTargets& t, int64_t k, int64_t rows, const
                               const ActPlanes* pre, float qmax, const MvShape& sh, hipStream_t s);
 hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
 
+// ---- prefill GEMM on the int8 matrix cores --------------------------------
+// dst = x · Wᵀ for a Q4_K weight from the Q8_K activation planes of `rows`
+// rows (qmm_quantize_act ACT_Q8K); used from gemm_q4k_min_rows() rows up.
+int gemm_q4k_min_rows();
+hipError_t launch_gemm_q4k(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
+                           int64_t ldd, hipStream_t s);
+
 }  // namespace qmm

@@ -1,0 +1,117 @@
+"""The prefill GEMM (int8 matrix cores) against the CPU oracle, through the
+C ABI: qmm_forward at 9 rows and more runs it for Q4_K weights.
+
+Tolerance (for the MFMA GEMM): max
+|y_gpu - y_cpu| / (||w_j|| * ||x_r||) <= 2e-3. The GEMM multiplies the same
+integers as the reference (Q8_K activation, exact int32 super-block sums);
+its one approximation is the min term, whose operands dy*S_j and
+-dmin*m_j enter its f16 MFMA rounded to f16 (2^-11 relative). An emulation
+of exactly that arithmetic in numpy lands within 1e-9 of the GPU on these
+cases (5e-8 against the oracle with the min term exact, 1.4e-4 with it in
+f16), so the tests also assert a bound of 5e-4 that a lost or wrong term
+would break.
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import TOL_GEMM, normalised_error, weights
+from oracle import qref
+from swarmllm_amd import GgmlDType, QMatMul, QTensor
+from swarmllm_amd._lib import lib
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TIGHT = 5e-4  # the f16 rounding of the min term's operands, with room
+
+
+def upload(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def q4k(w: np.ndarray):
+    wq = qref.from_float(qref.Q4_K, w)
+    return QTensor.from_data(wq.tobytes(), w.shape, GgmlDType.Q4K, device=DEV), wq
+
+
+def activations(rng, rows: int, k: int, outliers: bool = False) -> np.ndarray:
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    if outliers:  # BASELINE C3: 1% of channels scaled x20 in every row
+        ch = rng.permutation(k)[: max(1, k // 100)]
+        x[:, ch] *= np.float32(20.0)
+    return x
+
+
+GEMM_SHAPES = [  # (k, n, rows): tails in M and N, one and many super-blocks
+    (256, 128, 9), (256, 7, 9), (1024, 200, 16), (4096, 300, 33), (2560, 96, 64),
+    (4096, 1000, 130), (14336, 136, 40), (512, 384, 257),
+]
+
+
+@pytest.mark.parametrize("k,n,rows", GEMM_SHAPES)
+def test_q4k_gemm_parity(k, n, rows):
+    rng = np.random.default_rng(zlib.crc32(f"gemm-{k}-{n}-{rows}".encode()))
+    w = weights(rng, n, k)
+    x = activations(rng, rows, k, outliers=True)
+    qt, wq = q4k(w)
+    L = lib()
+    before = L.qmm_gemm_launches()
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert L.qmm_gemm_launches() == before + 1, "the MFMA GEMM did not run"
+    want = qref.matmul(qref.Q4_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q4_K, wq, n * k).reshape(n, k)
+    err = normalised_error(y, want, wdeq, x)
+    assert err <= TOL_GEMM, f"k={k} n={n} rows={rows}: {err}"
+    assert err <= TIGHT, f"k={k} n={n} rows={rows}: {err}"
+
+
+def test_q4k_gemm_c3_gate_full_size():
+    """BASELINE C3's gate projection: Q4_K 14336 x 4096 at M = 512, activations
+    with 1% outlier channels x20; the weight quantized on the device."""
+    from swarmllm_amd import fill_normal
+
+    n, k, rows = 14336, 4096, 512
+    w = fill_normal(n * k, seed=3 << 40, std=0.02).reshape(n, k)
+    qt = QTensor.quantize(w, GgmlDType.Q4K)
+    del w
+    rng = np.random.default_rng(3)
+    x = activations(rng, rows, k, outliers=True)
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    wq = np.frombuffer(qt.data(), np.uint8)
+    want = qref.matmul(qref.Q4_K, x, wq, n)
+    wdeq = qt.dequantize().cpu().numpy()
+    err = normalised_error(y, want, wdeq, x)
+    assert err <= TOL_GEMM
+    assert err <= TIGHT, err
+
+
+def test_q4k_gemm_rows_are_independent_and_close_to_the_decode_kernel():
+    """Within one GEMM call a row's result does not depend on its place in the
+    batch (the reference's qmm_batch: identical rows, identical outputs), and
+    across the switch from the decode kernel (<= 8 rows) to the GEMM the
+    results differ by the GEMM's f16 min term only (the reference allows a
+    deviation at its own kernel switch, quantized_tests.rs:244-251)."""
+    k, n = 4096, 300
+    rng = np.random.default_rng(12)
+    qt, _ = q4k(weights(rng, n, k))
+    mm = QMatMul(qt)
+    x6 = rng.standard_normal((6, k)).astype(np.float32)
+    x12 = upload(np.concatenate([x6, x6]))
+    y12 = mm.forward(x12)
+    assert torch.equal(y12[:6], y12[6:])
+    y6 = mm.forward(upload(x6))
+    wdeq = qt.dequantize().cpu().numpy()
+    assert normalised_error(y12[:6].cpu().numpy(), y6.cpu().numpy(), wdeq, x6) <= TIGHT
+
+
+def test_q4k_gemm_through_forward_shared():
+    k = 1024
+    rng = np.random.default_rng(13)
+    mats = [QMatMul(q4k(weights(rng, n, k))[0]) for n in (64, 200, 33)]
+    x = upload(rng.standard_normal((20, k)).astype(np.float32))
+    shared = QMatMul.forward_shared(x, mats)
+    for m, y in zip(mats, shared):
+        assert torch.equal(y, m.forward(x))
