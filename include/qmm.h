@@ -98,6 +98,15 @@ int qmm_matvec_max_rows(void);
 int qmm_matvec(int type, const void *w, const void *xq, float *dst, int64_t ldd, int64_t k, int64_t n,
                int64_t rows, int64_t stream);
 
+/* dst = x · Wᵀ for any rows >= 1 from an activation already quantized in
+ * qmm_act_layout(type, rows) (qmm_quantize_act): the decode kernels up to
+ * qmm_matvec_max_rows() rows, the int8 matrix-core GEMM from 9 rows for
+ * Q4_K. Nothing is allocated. Replaces swarm_mmq_matmul's launch step
+ * (mmq_entry.cu:162-203), which multiplies the activation swarm_mmq_quantize
+ * produced. */
+int qmm_matmul(int type, const void *w, const void *xq, float *dst, int64_t ldd, int64_t k, int64_t n,
+               int64_t rows, int64_t stream);
+
 /* dst = x · Wᵀ for any rows, from an f32 activation: quantizes it into the
  * workspace and picks the kernel by rows (the QCudaStorage::fwd policy,
  * quantized/cuda.rs:1653-1680). With launch == 0 nothing is enqueued and

@@ -34,6 +34,7 @@ SIGNATURES = {
     "qmm_quantize_act": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64]),
     "qmm_matvec_max_rows": (_I, []),
     "qmm_matvec": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64]),
+    "qmm_matmul": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64]),
     "qmm_forward": (_I, [_I, _P, _P, _I64, _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64, _I64, _I64, _I, _I64]),
     "qmm_forward_shared": (_I, [_I, _I, ctypes.POINTER(_P), ctypes.POINTER(_I64), ctypes.POINTER(_P),
                                 ctypes.POINTER(_I64), _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64, _I64, _I, _I64]),

@@ -20,11 +20,14 @@
 // term, a K = 8 product of f16(dy_m * S_mj) and f16(-dmin_n * m_nj), runs as one
 // f16 MFMA accumulating into the same f32 tile.
 //
-// Tiles: a workgroup of 4 waves computes 128 x 128 outputs (2 x 2 waves of
-// 64 x 64, each 2 x 2 MFMA 32x32x32 tiles), stepping K by 64 (one 64-value
-// chunk of a super-block per step) through double-buffered LDS: activation
-// codes, and the two weight halves sl*q and sh*q, each [row][64] padded to
-// 80 bytes. Rows past M or N are zero-filled and never stored.
+// Tiles: a workgroup of 8 waves computes 128 x 128 outputs (2 x 4 waves of
+// 64 x 32, each 2 x 1 MFMA 32x32x32 tiles; two waves per SIMD, so one's
+// scaling work runs beside the other's matrix work), stepping K by one
+// super-block:
+// its activation codes and the two weight halves sl*q and sh*q go to LDS
+// ([row][256] padded to 272 bytes), and the next super-block's bytes load
+// into registers while this one is multiplied (~3000 cycles of work between
+// a load and its use). Rows past M or N are zero-filled and never stored.
 #include "qmm_device.h"
 #include "qmm_launch.h"
 
@@ -38,18 +41,18 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128, BN = 128, KSTEP = 64, LDK = 80;
-constexpr int kThreads = 256;
+constexpr int BM = 128, BN = 128, LDK = 256 + 16;  // one super-block of K per step, rows padded
+constexpr int kWavesM = 2, kWavesN = 4;             // waves of 64 x 32 outputs
+constexpr int kThreads = 64 * kWavesM * kWavesN;    // 512
 
 struct __attribute__((aligned(16))) Smem {
-  int8_t a[2][BM][LDK];
-  int8_t blo[2][BN][LDK];
-  int8_t bhi[2][BN][LDK];
-  // per super-block, double-buffered by super-block parity
-  _Float16 amin[2][BM][8];  // f16(dy_m * S_mj)
-  _Float16 bmin[2][BN][8];  // f16(-dmin_n * m_nj)
-  float dy[2][BM];
-  float dw[2][BN];
+  int8_t a[BM][LDK];
+  int8_t blo[BN][LDK];
+  int8_t bhi[BN][LDK];
+  _Float16 amin[BM][8];  // f16(dy_m * S_mj)
+  _Float16 bmin[BN][8];  // f16(-dmin_n * m_nj)
+  float dy[BM];
+  float dw[BN];
 };
 
 // sl | sl << 16 for the packed multiply
@@ -61,12 +64,12 @@ __device__ __forceinline__ uint32_t pkmul(uint32_t a, uint32_t s2) {
   return __builtin_bit_cast(uint32_t, x * y);
 }
 
-// What a thread carries from global memory for one K-step.
+// What a thread carries from global memory for one super-block. Rows past M
+// or N are read as the last row (valid memory); their outputs are never stored.
 struct StepRegs {
-  uint4 a[2];   // activation codes: pieces tid and tid + 256 of the BM x 64 tile
-  uint4 q;      // Q4_K codes: 16 bytes of chunk j of weight row tid/2, half tid%2
-  // once per super-block (j == 0)
-  uint4 hdr;    // the weight row's super-block header
+  uint4 a[4];   // activation codes: pieces tid + 512 i of the BM x 256 tile (16 per row)
+  uint4 hdr;    // header of weight row tid/4
+  uint4 q[2];   // its code bytes 32*(tid%4) .. +31 (chunk tid%4)
   float dy;     // activation row tid's scale (tid < BM)
   uint4 bs0, bs1;  // its 16 bsums (int16)
 };
@@ -78,203 +81,164 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_kernel(const uint8_t* __
                                                                 float* __restrict__ dst, int64_t ldd) {
   __shared__ Smem sm;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wv = tid >> 6;
-  const int wm = wv >> 1, wn = wv & 1;  // this wave's 64 x 64 block of the tile
+  const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv / kWavesN, wn = wv % kWavesN;  // this wave's 64 x 32 block of the tile
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
   const int64_t K = (int64_t)nsb * 256;
   const int64_t rowbytes = (int64_t)nsb * 144;
-  const int steps = nsb * 4;
 
-  // the weight row and half this thread dequantises
-  const int bn = tid >> 1, bh = tid & 1;
-  const bool bvalid = n0 + bn < N;
-  const uint8_t* wrow = W + (n0 + (bvalid ? bn : 0)) * rowbytes;
-  // the activation pieces this thread copies: rows (tid + 256 i) / 4, 16-byte piece % 4
-  auto load_step = [&](StepRegs& r, int t) {
-    const int sb = t >> 2, j = t & 3;
+  // the weight row and chunk this thread dequantises
+  const int bn = tid >> 2, bj = tid & 3;
+  const int64_t wr = n0 + bn < N ? n0 + bn : N - 1;
+  const uint8_t* wrow = W + wr * rowbytes;
+  const int64_t ar = m0 + tid < M ? m0 + tid : M - 1;  // activation row of the scale loads (tid < BM)
+  const int8_t* arow[4];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int p = tid + kThreads * i;
-      const int row = p >> 2, c = p & 3;
-      r.a[i] = m0 + row < M ? *(const uint4*)(yq + (m0 + row) * K + (int64_t)sb * 256 + 64 * j + 16 * c)
-                            : make_uint4(0, 0, 0, 0);
-    }
-    r.q = bvalid ? *(const uint4*)(wrow + (int64_t)sb * 144 + 16 + 32 * j + 16 * bh) : make_uint4(0, 0, 0, 0);
-    if (j == 0) {
-      r.hdr = bvalid ? *(const uint4*)(wrow + (int64_t)sb * 144) : make_uint4(0, 0, 0, 0);
-      if (tid < BM) {
-        const bool av = m0 + tid < M;
-        r.dy = av ? yd[(m0 + tid) * nsb + sb] : 0.0f;
-        const uint4* bp = (const uint4*)(ybs + (m0 + (av ? tid : 0)) * (K / 16) + (int64_t)sb * 16);
-        r.bs0 = av ? bp[0] : make_uint4(0, 0, 0, 0);
-        r.bs1 = av ? bp[1] : make_uint4(0, 0, 0, 0);
-      }
+  for (int i = 0; i < 4; i++) {
+    const int p = tid + kThreads * i;
+    const int64_t r = m0 + (p >> 4) < M ? m0 + (p >> 4) : M - 1;
+    arow[i] = yq + r * K + 16 * (p & 15);
+  }
+
+  auto load_sb = [&](StepRegs& r, int sb) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.a[i] = *(const uint4*)(arow[i] + (int64_t)sb * 256);
+    const uint8_t* blk = wrow + (int64_t)sb * 144;
+    r.hdr = *(const uint4*)blk;
+    r.q[0] = *(const uint4*)(blk + 16 + 32 * bj);
+    r.q[1] = *(const uint4*)(blk + 32 + 32 * bj);
+    if (tid < BM) {
+      r.dy = yd[ar * nsb + sb];
+      const uint4* bp = (const uint4*)(ybs + ar * (K / 16) + (int64_t)sb * 16);
+      r.bs0 = bp[0];
+      r.bs1 = bp[1];
     }
   };
 
-  // scales of the current super-block for this thread's weight row (from the header)
-  uint32_t sl2[8], sh2[8];
-  auto store_step = [&](const StepRegs& r, int t) {
-    const int buf = t & 1, sb = t >> 2, j = t & 3, sbuf = sb & 1;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int p = tid + kThreads * i;
-      *(uint4*)&sm.a[buf][p >> 2][16 * (p & 3)] = r.a[i];
-    }
-    if (j == 0) {
-      // 6-bit scales and mins of the 8 sub-blocks (get_scale_min_k4, utils.rs:50-60)
-      const uint32_t u0 = r.hdr.y, u1 = r.hdr.z, u2 = r.hdr.w;
-      const uint32_t s03 = u0 & 0x3f3f3f3fu, m03 = u1 & 0x3f3f3f3fu;
-      const uint32_t s47 = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
-      const uint32_t m47 = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const uint32_t sc = ((q < 4 ? s03 : s47) >> (8 * (q & 3))) & 0xFF;
-        sl2[q] = dup16(sc & 7);
-        sh2[q] = dup16(sc >> 3);
-      }
-      if (bh == 0) {
-        const float d = h2f((uint16_t)(r.hdr.x & 0xFFFF)), dmin = h2f((uint16_t)(r.hdr.x >> 16));
-        h8 bm;
-#pragma unroll
-        for (int q = 0; q < 8; q++) bm[q] = (_Float16)(-dmin * (float)(((q < 4 ? m03 : m47) >> (8 * (q & 3))) & 0xFF));
-        *(h8*)&sm.bmin[sbuf][bn][0] = bm;
-        sm.dw[sbuf][bn] = d;
-      }
-      if (tid < BM) {
-        const uint32_t w[8] = {r.bs0.x, r.bs0.y, r.bs0.z, r.bs0.w, r.bs1.x, r.bs1.y, r.bs1.z, r.bs1.w};
-        h8 am;
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-          // S_q = bsum_2q + bsum_2q+1 (the two int16 of word q)
-          const int s = (int)(int16_t)(w[q] & 0xFFFF) + (int)(int16_t)(w[q] >> 16);
-          am[q] = (_Float16)(r.dy * (float)s);
-        }
-        *(h8*)&sm.amin[sbuf][tid][0] = am;
-        sm.dy[sbuf][tid] = r.dy;
-      }
-    }
-    // weight codes: 16 bytes = values l0..l0+15 of sub-blocks 2j (low nibbles)
-    // and 2j+1 (high nibbles), l0 = 16*bh; k within the step: l0 + b and 32 + l0 + b
-    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-    uint32_t lo_a[4], hi_a[4], lo_b[4], hi_b[4];
+  auto store_sb = [&](const StepRegs& r) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t a = qw[i] & 0x0F0F0F0Fu, b = (qw[i] >> 4) & 0x0F0F0F0Fu;
-      lo_a[i] = pkmul(a, sl2[2 * j]);
-      hi_a[i] = pkmul(a, sh2[2 * j]);
-      lo_b[i] = pkmul(b, sl2[2 * j + 1]);
-      hi_b[i] = pkmul(b, sh2[2 * j + 1]);
+      const int p = tid + kThreads * i;
+      *(uint4*)&sm.a[p >> 4][16 * (p & 15)] = r.a[i];
     }
-    const int l0 = 16 * bh;
-    *(uint4*)&sm.blo[buf][bn][l0] = make_uint4(lo_a[0], lo_a[1], lo_a[2], lo_a[3]);
-    *(uint4*)&sm.bhi[buf][bn][l0] = make_uint4(hi_a[0], hi_a[1], hi_a[2], hi_a[3]);
-    *(uint4*)&sm.blo[buf][bn][32 + l0] = make_uint4(lo_b[0], lo_b[1], lo_b[2], lo_b[3]);
-    *(uint4*)&sm.bhi[buf][bn][32 + l0] = make_uint4(hi_b[0], hi_b[1], hi_b[2], hi_b[3]);
+    // 6-bit scales and mins of the 8 sub-blocks (get_scale_min_k4, utils.rs:50-60)
+    const uint32_t u0 = r.hdr.y, u1 = r.hdr.z, u2 = r.hdr.w;
+    const uint32_t s03 = u0 & 0x3f3f3f3fu, m03 = u1 & 0x3f3f3f3fu;
+    const uint32_t s47 = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+    const uint32_t m47 = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+    if (bj == 0) {
+      const float d = h2f((uint16_t)(r.hdr.x & 0xFFFF)), dmin = h2f((uint16_t)(r.hdr.x >> 16));
+      h8 bm;
+#pragma unroll
+      for (int q = 0; q < 8; q++) bm[q] = (_Float16)(-dmin * (float)(((q < 4 ? m03 : m47) >> (8 * (q & 3))) & 0xFF));
+      *(h8*)&sm.bmin[bn][0] = bm;
+      sm.dw[bn] = d;
+    }
+    if (tid < BM) {
+      const uint32_t w[8] = {r.bs0.x, r.bs0.y, r.bs0.z, r.bs0.w, r.bs1.x, r.bs1.y, r.bs1.z, r.bs1.w};
+      h8 am;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        // S_q = bsum_2q + bsum_2q+1 (the two int16 of word q)
+        const int sv = (int)(int16_t)(w[q] & 0xFFFF) + (int)(int16_t)(w[q] >> 16);
+        am[q] = (_Float16)(r.dy * (float)sv);
+      }
+      *(h8*)&sm.amin[tid][0] = am;
+      sm.dy[tid] = r.dy;
+    }
+    // chunk j = bj: code bytes 32j + 16i (i = 0, 1 -> offset l0 = 16i); low
+    // nibbles are values 64j + l0 + b (sub-block 2j), high 64j + 32 + l0 + b
+    const int j = bj;
+    const uint32_t sw = j < 2 ? s03 : s47;
+    const uint32_t sca = (sw >> (16 * (j & 1))) & 0xFF, scb = (sw >> (16 * (j & 1) + 8)) & 0xFF;
+    const uint32_t sla = dup16(sca & 7), sha = dup16(sca >> 3), slb = dup16(scb & 7), shb = dup16(scb >> 3);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int l0 = 16 * i;
+      const uint32_t qw[4] = {r.q[i].x, r.q[i].y, r.q[i].z, r.q[i].w};
+      uint32_t lo_a[4], hi_a[4], lo_b[4], hi_b[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t a = qw[e] & 0x0F0F0F0Fu, b = (qw[e] >> 4) & 0x0F0F0F0Fu;
+        lo_a[e] = pkmul(a, sla);
+        hi_a[e] = pkmul(a, sha);
+        lo_b[e] = pkmul(b, slb);
+        hi_b[e] = pkmul(b, shb);
+      }
+      *(uint4*)&sm.blo[bn][64 * j + l0] = make_uint4(lo_a[0], lo_a[1], lo_a[2], lo_a[3]);
+      *(uint4*)&sm.bhi[bn][64 * j + l0] = make_uint4(hi_a[0], hi_a[1], hi_a[2], hi_a[3]);
+      *(uint4*)&sm.blo[bn][64 * j + 32 + l0] = make_uint4(lo_b[0], lo_b[1], lo_b[2], lo_b[3]);
+      *(uint4*)&sm.bhi[bn][64 * j + 32 + l0] = make_uint4(hi_b[0], hi_b[1], hi_b[2], hi_b[3]);
+    }
   };
 
-  // accumulators: per super-block int32 halves, and the f32 result
-  i16v clo[2][2], chi[2][2];
-  f16v acc[2][2];
+  f16v acc[2];
 #pragma unroll
   for (int a = 0; a < 2; a++)
 #pragma unroll
-    for (int b = 0; b < 2; b++) {
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        clo[a][b][i] = 0;
-        chi[a][b][i] = 0;
-        acc[a][b][i] = 0.0f;
-      }
-    }
+    for (int i = 0; i < 16; i++) acc[a][i] = 0.0f;
 
   StepRegs regs;
-  load_step(regs, 0);
-  store_step(regs, 0);
-  __syncthreads();
-
+  load_sb(regs, 0);
   const int r32 = lane & 31, kh = 16 * (lane >> 5);
-  for (int t = 0; t < steps; t++) {
-    const int buf = t & 1;
-    if (t + 1 < steps) load_step(regs, t + 1);
-    // two 32-value K-chunks of the step
-#pragma unroll
-    for (int kc = 0; kc < 2; kc++) {
-      i4v af[2], bl[2], bhv[2];
-#pragma unroll
-      for (int tm = 0; tm < 2; tm++)
-        af[tm] = *(const i4v*)&sm.a[buf][64 * wm + 32 * tm + r32][32 * kc + kh];
-#pragma unroll
-      for (int tn = 0; tn < 2; tn++) {
-        bl[tn] = *(const i4v*)&sm.blo[buf][64 * wn + 32 * tn + r32][32 * kc + kh];
-        bhv[tn] = *(const i4v*)&sm.bhi[buf][64 * wn + 32 * tn + r32][32 * kc + kh];
-      }
-#pragma unroll
-      for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-        for (int tn = 0; tn < 2; tn++) {
-          clo[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[tm], bl[tn], clo[tm][tn], 0, 0, 0);
-          chi[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[tm], bhv[tn], chi[tm][tn], 0, 0, 0);
-        }
-    }
-    if ((t & 3) == 3) {
-      // end of a super-block: scale into the f32 result, then the min term
-      const int sbuf = (t >> 2) & 1;
-#pragma unroll
-      for (int tn = 0; tn < 2; tn++) {
-        const float dwn = sm.dw[sbuf][64 * wn + 32 * tn + r32];
-#pragma unroll
-        for (int tm = 0; tm < 2; tm++) {
-#pragma unroll
-          for (int g = 0; g < 4; g++) {
-            const float4 dy4 = *(const float4*)&sm.dy[sbuf][64 * wm + 32 * tm + 8 * g + 4 * (lane >> 5)];
-            const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              const int i = 4 * g + e;
-              const int tot = (chi[tm][tn][i] << 3) + clo[tm][tn][i];
-              acc[tm][tn][i] = __builtin_fmaf(dyv[e] * dwn, (float)tot, acc[tm][tn][i]);
-              clo[tm][tn][i] = 0;
-              chi[tm][tn][i] = 0;
-            }
-          }
-        }
-      }
-      h8 amf[2], bmf[2];
-      const h8 z = {};
-#pragma unroll
-      for (int tm = 0; tm < 2; tm++)
-        amf[tm] = lane < 32 ? *(const h8*)&sm.amin[sbuf][64 * wm + 32 * tm + r32][0] : z;
-#pragma unroll
-      for (int tn = 0; tn < 2; tn++)
-        bmf[tn] = lane < 32 ? *(const h8*)&sm.bmin[sbuf][64 * wn + 32 * tn + r32][0] : z;
-#pragma unroll
-      for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-        for (int tn = 0; tn < 2; tn++)
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(amf[tm], bmf[tn], acc[tm][tn], 0, 0, 0);
-    }
-    if (t + 1 < steps) {
-      // buffer (t+1)&1 was last read in step t-1, which every wave finished
-      // before the barrier that ended it
-      store_step(regs, t + 1);
-    }
+  const int nrow = 32 * wn + r32;  // this lane's weight row (output column) in the tile
+  for (int sb = 0; sb < nsb; sb++) {
+    // every wave is done with the previous super-block's LDS
+    if (sb > 0) __syncthreads();
+    store_sb(regs);
     __syncthreads();
+    // the next super-block's bytes travel while this one is multiplied
+    if (sb + 1 < nsb) load_sb(regs, sb + 1);
+
+    i16v clo[2], chi[2];
+#pragma unroll
+    for (int kc = 0; kc < 8; kc++) {
+      const i4v bl = *(const i4v*)&sm.blo[nrow][32 * kc + kh];
+      const i4v bhv = *(const i4v*)&sm.bhi[nrow][32 * kc + kh];
+#pragma unroll
+      for (int tm = 0; tm < 2; tm++) {
+        const i4v af = *(const i4v*)&sm.a[64 * wm + 32 * tm + r32][32 * kc + kh];
+        const i16v zero = {};
+        clo[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bl, kc ? clo[tm] : zero, 0, 0, 0);
+        chi[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bhv, kc ? chi[tm] : zero, 0, 0, 0);
+      }
+    }
+    // scale the super-block's integers into the f32 result, then the min term
+    const float dwn = sm.dw[nrow];
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const float4 dy4 = *(const float4*)&sm.dy[64 * wm + 32 * tm + 8 * g + 4 * (lane >> 5)];
+        const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int i = 4 * g + e;
+          const int tot = (chi[tm][i] << 3) + clo[tm][i];
+          acc[tm][i] = __builtin_fmaf(dyv[e] * dwn, (float)tot, acc[tm][i]);
+        }
+      }
+    }
+    const h8 z = {};
+    const h8 bmf = lane < 32 ? *(const h8*)&sm.bmin[nrow][0] : z;
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++) {
+      const h8 amf = lane < 32 ? *(const h8*)&sm.amin[64 * wm + 32 * tm + r32][0] : z;
+      acc[tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(amf, bmf, acc[tm], 0, 0, 0);
+    }
   }
 
   // store
+  const int64_t col = n0 + nrow;
+  if (col < N) {
 #pragma unroll
-  for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-    for (int tn = 0; tn < 2; tn++) {
-      const int64_t col = n0 + 64 * wn + 32 * tn + r32;
-      if (col >= N) continue;
+    for (int tm = 0; tm < 2; tm++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const int64_t row = m0 + 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < M) dst[row * ldd + col] = acc[tm][tn][i];
+        if (row < M) dst[row * ldd + col] = acc[tm][i];
       }
-    }
+  }
 }
 
 }  // namespace

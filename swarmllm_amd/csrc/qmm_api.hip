@@ -208,6 +208,32 @@ int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd,
   return status_of(e);
 }
 
+int qmm_matmul(int type, const void* w, const void* xq, float* dst, int64_t ldd, int64_t k, int64_t n, int64_t rows,
+               int64_t stream) {
+  if (!shape_ok(type, k, n, rows) || ldd < n || !w || !xq || !dst) return QMM_UNSUPPORTED;
+  const int layout = qmm_act_layout(type, rows);
+  const qmm::ActPlanes p = qmm::act_planes(layout, (void*)xq, k, rows);
+  const hipStream_t st = (hipStream_t)stream;
+  clear_stale_error();
+  if (type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && ((uintptr_t)w & 15) == 0) {
+    if (qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
+    g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+    return QMM_OK;
+  }
+  const int64_t step = qmm::matvec_max_rows();
+  for (int64_t r0 = 0; r0 < rows; r0 += step) {
+    const int64_t nr = rows - r0 < step ? rows - r0 : step;
+    const qmm::ActPlanes pr = qmm::act_rows(layout, p, k, r0);
+    float* d = dst + r0 * ldd;
+    const hipError_t e = stream_supported(type, k, nr)
+                             ? launch_stream_targets(type, 1, &w, &n, &d, &ldd, k, nr, nullptr, 0, &pr, st)
+                             : qmm::launch_matvec(type, w, n, k, pr, nr, d, ldd, st);
+    if (e != hipSuccess) return QMM_DEVICE_ERROR;
+    g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
+  }
+  return QMM_OK;
+}
+
 int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float* dst, int64_t ldd, void* workspace,
                 size_t workspace_bytes, size_t* need, int64_t k, int64_t n, int64_t rows, int launch, int64_t stream) {
   if (!shape_ok(type, k, n, rows) || need == nullptr || ldd < n || x_stride < k) return QMM_UNSUPPORTED;

@@ -115,3 +115,22 @@ def test_q4k_gemm_through_forward_shared():
     shared = QMatMul.forward_shared(x, mats)
     for m, y in zip(mats, shared):
         assert torch.equal(y, m.forward(x))
+
+
+@pytest.mark.parametrize("rows", [1, 2, 5, 8, 9, 40])
+def test_matmul_from_a_quantized_activation_equals_forward(rows):
+    """qmm_matmul (the product from qmm_quantize_act's planes, the
+    swarm_mmq_quantize + swarm_mmq_matmul pair) gives forward's bits."""
+    from swarmllm_amd import _lib
+    from swarmllm_amd.qtensor import quantize_act
+
+    k, n = 1024, 200
+    rng = np.random.default_rng(14 + rows)
+    qt, _ = q4k(weights(rng, n, k))
+    x = upload(rng.standard_normal((rows, k)).astype(np.float32))
+    xq = quantize_act(x, _lib.ACT_Q8K)
+    out = torch.empty((rows, n), dtype=torch.float32, device=DEV)
+    st = lib().qmm_matmul(qref.Q4_K, qt.data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k, n, rows,
+                          torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    assert torch.equal(out, QMatMul(qt).forward(x))
