@@ -207,27 +207,38 @@ def dominant_kernel(layers, outs, stream, reps: int) -> dict:
             "us": us, "launches": launches, "alg_bytes": alg, "gbs": gbs}
 
 
-def prefill_gemm(layers, stream, reps: int) -> dict:
-    """BASELINE C3's headline product: the Q4_K gate projection 14336x4096 at
-    M = 512 (activations N(0,1) with 1% of channels scaled x20), the activation
-    quantized once (qmm_quantize_act), then the int8 matrix-core GEMM alone
-    (qmm_matmul) back to back over the layer copies' gate weights in one
-    graph, timed with HIP events on its stream. ops = 2*M*N*K per launch."""
+def prefill_inputs(M: int, n: int, k: int):
+    """C3's activation (N(0,1), 1% of channels x20) quantized once to Q8_K
+    planes, and the output buffer."""
     import torch
 
     from swarmllm_amd import fill_normal
     from swarmllm_amd._lib import check, lib
 
     L = lib()
-    M, n, k = 512, 14336, 4096
     x = fill_normal(M * k, seed=(3 << 40) | 0xB0).reshape(M, k)
     g = torch.Generator().manual_seed(3)
     ch = torch.randperm(k, generator=g)[: k // 100].to(x.device)
     x[:, ch] *= 20.0
     xq = torch.empty(L.qmm_act_bytes(ACT_Q8K, k, M), dtype=torch.uint8, device="cuda")
     out = torch.empty((M, n), dtype=torch.float32, device="cuda")
-    s = stream.cuda_stream
-    check("qmm_quantize_act", L.qmm_quantize_act(x.data_ptr(), xq.data_ptr(), ACT_Q8K, k, M, k, s))
+    check("qmm_quantize_act", L.qmm_quantize_act(x.data_ptr(), xq.data_ptr(), ACT_Q8K, k, M, k,
+                                                 torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return xq, out
+
+
+def prefill_gemm(layers, stream, reps: int) -> dict:
+    """BASELINE C3's headline product: the Q4_K gate projection 14336x4096 at
+    M = 512 (activations N(0,1) with 1% of channels scaled x20), the activation
+    quantized once (qmm_quantize_act), then the int8 matrix-core GEMM alone
+    (qmm_matmul) back to back over the layer copies' gate weights in one
+    graph, timed with HIP events on its stream. ops = 2*M*N*K per launch."""
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    M, n, k = 512, 14336, 4096
+    xq, out = prefill_inputs(M, n, k)
     before = L.qmm_gemm_launches()
 
     def fn(st):
@@ -247,7 +258,8 @@ def prefill_gemm(layers, stream, reps: int) -> dict:
     return {"workload": "C3: Q4_K gate 14336x4096 at M=512, int8 MFMA GEMM (activation quantized once, Q8_K)",
             "us_per_launch": round(us, 3), "ops_per_launch": int(ops), "tops": round(tops, 2),
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": 5000.0, "unit": "TOP/s",
-                         "frac": round(tops / 5000.0, 4), "kernel": "gemm_q4k_kernel"}}
+                         "frac": round(tops / 5000.0, 4), "kernel": "gemm_q4k_kernel",
+                         "traffic": measured_traffic("prefill_gemm")}}
 
 
 def cpu_baseline(layers, budget_s: float) -> dict:
@@ -289,6 +301,70 @@ def cpu_baseline(layers, budget_s: float) -> dict:
             "cpu": cpu_name(), "logical_cpus": os.cpu_count()}
 
 
+COPY_BYTES = 512 << 20  # the calibration copy: 512 MiB read + 512 MiB written
+
+
+def profile_only(which: str, layers, outs, stream, reps: int) -> None:
+    """Launch one kind of kernel alone, `reps` times, outside any graph, for
+    rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE): the dominant decode
+    launch rotating over the layer copies, the prefill GEMM, or a plain
+    device copy of COPY_BYTES whose counters calibrate the other two."""
+    import torch
+
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    s = stream.cuda_stream
+    if which == "copy":
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for _ in range(reps):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"profile copy: {reps} copies of {COPY_BYTES} bytes")
+        return
+    if which == "dominant":
+        x, ws = layers[0].acts["ffn_in"]
+        n, k = 14336, 4096
+        need = ctypes.c_size_t(0)
+        ns = (ctypes.c_int64 * 2)(n, n)
+        dp = (ctypes.c_void_p * 2)(outs["gate"].data_ptr(), outs["up"].data_ptr())
+        for i in range(reps):
+            lay = layers[i % len(layers)]
+            wp = (ctypes.c_void_p * 2)(lay.w["gate"].data_.data_ptr(), lay.w["up"].data_.data_ptr())
+            check("qmm_forward_shared", L.qmm_forward_shared(Q4K, 2, wp, ns, dp, ns, x.data_ptr(), k, ws.data_ptr(),
+                                                             ws.numel(), ctypes.byref(need), k, 1, 1, s))
+        torch.cuda.synchronize()
+        log(f"profile dominant: {reps} gate+up launches over {len(layers)} copies")
+        return
+    M, n, k = 512, 14336, 4096
+    xq, out = prefill_inputs(M, n, k)
+    for i in range(reps):
+        lay = layers[i % len(layers)]
+        check("qmm_matmul", L.qmm_matmul(Q4K, lay.w["gate"].data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k,
+                                         n, M, s))
+    torch.cuda.synchronize()
+    log(f"profile prefill: {reps} GEMM launches over {len(layers)} copies")
+
+
+def measured_traffic(kernel_key: str):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration), or
+    None when the summary is absent. Rows read `traffic <key> <bytes>`."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel_key:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_name() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -309,6 +385,8 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile", choices=["dominant", "prefill", "copy"],
+                    help="launch only this kernel --steps times (for rocprofv3 counter passes), print no JSON")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -339,6 +417,10 @@ def main() -> int:
     lb = layer_bytes()
     log(f"{args.copies} layer copies quantized on the device in {time.perf_counter() - t0:.1f} s "
         f"({args.copies * lb['weights'] / 2**30:.2f} GiB of weights)")
+
+    if args.profile:
+        profile_only(args.profile, layers, outs, stream, args.steps)
+        return 0
 
     rep = Replayer(layers, outs, stream)
     with torch.cuda.stream(stream):
@@ -381,7 +463,7 @@ def main() -> int:
                    "rows": 1, "layer_bytes": lb["total"], "weight_copies": args.copies,
                    "percent_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(dk["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gate_up"),
                      "kernel": dk["kernel"], "us_per_launch": round(dk["us"], 4),
                      "alg_bytes_per_launch": dk["alg_bytes"]},
         "cpu_baseline": cpu,
