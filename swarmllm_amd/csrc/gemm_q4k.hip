@@ -10,24 +10,39 @@
 //
 // Folding the 6-bit sub-block scale into the int8 operand. An int8 MFMA can
 // only take sc*q (up to 945) split in two: sc = 8*sh + sl (sh, sl in 0..7),
-// so sl*q and sh*q are both <= 105. Two MFMAs per K-chunk give
-// C_lo = sum y*sl*q and C_hi = sum y*sh*q, and 8*C_hi + C_lo is the exact
-// int32 sum_j sc_j sum_i q y of the super-block (the reference's own integer)
-// with no per-sub-block work on the accumulators. The split also makes the
-// dequantisation cheap: 4 nibbles packed one per byte times sl (<= 7) never
-// carry out of a byte, so one packed 16-bit multiply scales 4 codes.
-// Per super-block the f32 epilogue adds (d_n dy_m) * (8*C_hi + C_lo); the min
-// term, a K = 8 product of f16(dy_m * S_mj) and f16(-dmin_n * m_nj), runs as one
-// f16 MFMA accumulating into the same f32 tile.
+// so sl*q and sh*q are both <= 105. Per super-block a wave runs the eight
+// 32-deep K-chunks against sh*q into its int32 tiles, shifts them left by 3,
+// then runs the eight chunks again against sl*q into the same tiles: the
+// result is the exact int32 sum_j sc_j sum_i q y of the super-block (the
+// reference's own integer), with one set of accumulators and no
+// per-sub-block work on them. 4 nibbles packed one per byte times sh or sl
+// (<= 7) never carry out of a byte, so one packed 16-bit multiply scales 4
+// codes. The f32 epilogue then adds (d_n dy_m) * T; the min term, a K = 8
+// product of f16(dy_m * S_mj) and f16(-dmin_n * m_nj), runs as one f16 MFMA
+// accumulating into the same f32 tile.
 //
-// Tiles: a workgroup of 8 waves computes 128 x 128 outputs (2 x 4 waves of
-// 64 x 32, each 2 x 1 MFMA 32x32x32 tiles; two waves per SIMD, so one's
-// scaling work runs beside the other's matrix work), stepping K by one
-// super-block:
-// its activation codes and the two weight halves sl*q and sh*q go to LDS
-// ([row][256] padded to 272 bytes), and the next super-block's bytes load
-// into registers while this one is multiplied (~3000 cycles of work between
-// a load and its use). Rows past M or N are zero-filled and never stored.
+// Data movement, sized by what gfx950 measures (LDS reads of 16 bytes a
+// lane ~236 B/clk per CU, LDS writes ~72 B/clk): nothing the weights expand
+// into is written to LDS, and the raw bytes reach LDS without passing
+// through registers.
+//   - A workgroup of kWaves waves computes 128 rows x 32 kWaves columns,
+//     each wave 128 x 32 (4 MFMA 32x32x32 tiles).
+//   - Per super-block the workgroup's raw Q4_K weight bytes (144 per row)
+//     and activation codes (256 per row) are copied to LDS with the direct
+//     global-to-LDS loads (global_load_lds_dwordx4), one super-block ahead
+//     into the other half of a double buffer. Activation rows' 16-byte
+//     pieces are XOR-swizzled by row so the MFMA reads are conflict-free;
+//     weight bytes are stored as 9 planes of 16-byte pieces (plane j = piece
+//     j of every row), so each copy moves one piece of 64 rows and a lane's
+//     reads of consecutive rows are consecutive.
+//   - Each lane reads its weight row's header and the 16 code bytes
+//     32j + 16(lane/32) of each 32-byte chunk j — exactly its MFMA B-operand
+//     bytes for sub-blocks 2j (low nibbles) and 2j+1 (high nibbles) — and
+//     dequantises them in registers.
+//   - dy_m and f16(dy_m * S_mj) per super-block are loaded by the
+//     workgroup's threads and written to LDS (2.5 KB).
+// Rows past M or N are read as the last row (valid memory); their outputs
+// are never stored.
 #include "qmm_device.h"
 #include "qmm_launch.h"
 
@@ -38,24 +53,13 @@ namespace {
 typedef int i4v __attribute__((ext_vector_type(4)));
 typedef int i16v __attribute__((ext_vector_type(16)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int BM = 128, BN = 128, LDK = 256 + 16;  // one super-block of K per step, rows padded
-constexpr int kWavesM = 2, kWavesN = 4;             // waves of 64 x 32 outputs
-constexpr int kThreads = 64 * kWavesM * kWavesN;    // 512
+constexpr int BM = 128;  // rows of a workgroup tile
 
-struct __attribute__((aligned(16))) Smem {
-  int8_t a[BM][LDK];
-  int8_t blo[BN][LDK];
-  int8_t bhi[BN][LDK];
-  _Float16 amin[BM][8];  // f16(dy_m * S_mj)
-  _Float16 bmin[BN][8];  // f16(-dmin_n * m_nj)
-  float dy[BM];
-  float dw[BN];
-};
-
-// sl | sl << 16 for the packed multiply
 __device__ __forceinline__ uint32_t dup16(uint32_t v) { return v | (v << 16); }
 
 __device__ __forceinline__ uint32_t pkmul(uint32_t a, uint32_t s2) {
@@ -64,192 +68,276 @@ __device__ __forceinline__ uint32_t pkmul(uint32_t a, uint32_t s2) {
   return __builtin_bit_cast(uint32_t, x * y);
 }
 
-// What a thread carries from global memory for one super-block. Rows past M
-// or N are read as the last row (valid memory); their outputs are never stored.
-struct StepRegs {
-  uint4 a[4];   // activation codes: pieces tid + 512 i of the BM x 256 tile (16 per row)
-  uint4 hdr;    // header of weight row tid/4
-  uint4 q[2];   // its code bytes 32*(tid%4) .. +31 (chunk tid%4)
-  float dy;     // activation row tid's scale (tid < BM)
-  uint4 bs0, bs1;  // its 16 bsums (int16)
+__device__ __forceinline__ uint32_t word(const uint4& c, int e) {
+  return e == 0 ? c.x : e == 1 ? c.y : e == 2 ? c.z : c.w;
+}
+
+// Raw bytes a lane reads of its weight row for one super-block.
+struct WRaw {
+  uint4 hdr;             // d, dmin, 12 scale bytes
+  uint4 c0, c1, c2, c3;  // code bytes 32j + 16h .. +15 for j = 0..3
 };
 
-__global__ __launch_bounds__(kThreads, 1) void gemm_q4k_kernel(const uint8_t* __restrict__ W, int64_t N, int nsb,
-                                                                const int8_t* __restrict__ yq,
-                                                                const float* __restrict__ yd,
-                                                                const int16_t* __restrict__ ybs, int64_t M,
-                                                                float* __restrict__ dst, int64_t ldd) {
-  __shared__ Smem sm;
+__device__ __forceinline__ const uint4& chunk(const WRaw& r, int j) {
+  return j == 0 ? r.c0 : j == 1 ? r.c1 : j == 2 ? r.c2 : r.c3;
+}
+
+template <int kWaves>
+__global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t* __restrict__ W, int64_t N, int nsb,
+                                                                   const int8_t* __restrict__ yq,
+                                                                   const float* __restrict__ yd,
+                                                                   const int16_t* __restrict__ ybs, int64_t M,
+                                                                   float* __restrict__ dst, int64_t ldd) {
+  constexpr int BN = 32 * kWaves;               // columns (weight rows) of the tile
+  constexpr int kWInstr = BN * 144 / 1024;      // 1 KB copies of the weight tile per super-block
+  constexpr int kAInstr = BM * 256 / 1024;      // and of the activation tile
+  // Each half of each double buffer is its own object and the super-block
+  // loop is unrolled by two, so every access names its buffer statically and
+  // the compiler can tell reads of one half from copies into the other (it
+  // would otherwise wait for the copies before every LDS read).
+  __shared__ __attribute__((aligned(16))) int8_t s_a0[BM * 256], s_a1[BM * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t s_w0[BN * 144], s_w1[BN * 144];
+  // per-super-block activation scales (written by threads, not copied)
+  __shared__ __attribute__((aligned(16))) _Float16 s_amin[2][BM][8];
+  __shared__ __attribute__((aligned(16))) float s_dy[2][BM];
+
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv / kWavesN, wn = wv % kWavesN;  // this wave's 64 x 32 block of the tile
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
   const int64_t K = (int64_t)nsb * 256;
-  const int64_t rowbytes = (int64_t)nsb * 144;
+  const uint32_t rowbytes = (uint32_t)nsb * 144;
+  const int h = lane >> 5, r32 = lane & 31;
 
-  // the weight row and chunk this thread dequantises
-  const int bn = tid >> 2, bj = tid & 3;
-  const int64_t wr = n0 + bn < N ? n0 + bn : N - 1;
-  const uint8_t* wrow = W + wr * rowbytes;
-  const int64_t ar = m0 + tid < M ? m0 + tid : M - 1;  // activation row of the scale loads (tid < BM)
-  const int8_t* arow[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int p = tid + kThreads * i;
-    const int64_t r = m0 + (p >> 4) < M ? m0 + (p >> 4) : M - 1;
-    arow[i] = yq + r * K + 16 * (p & 15);
-  }
+  // Weight copies: the tile is stored as 9 planes, plane j holding 16-byte
+  // piece j of every row (piece 0 the header, pieces 1-8 the codes). Copy
+  // i = wv + kWaves u moves plane i % 9 of rows 64 (i / 9) .. +63, lane L row
+  // 64 (i / 9) + L (rows past N read the last row). Byte offsets from W: the
+  // host keeps N * rowbytes below 2^31.
+  const uint32_t wlane = (uint32_t)(n0 + lane) * rowbytes;
+  const uint32_t wlast = (uint32_t)(N - 1) * rowbytes;
+  // Activation copies: copy i moves rows 4i .. 4i+3 of the tile; lane L
+  // writes row 4i + L/16 at piece position L%16, which holds code piece
+  // (L%16) ^ (row & 15) = (L%16) ^ (4 (i & 3) + L/16). Byte offsets from yq,
+  // rows past M read the last row: the host keeps (M + BM) * K below 2^31.
+  const uint32_t lp = lane & 15, lq = lane >> 4;
+  const uint32_t arow0 = (uint32_t)((m0 + lq) * K);
+  const uint32_t alast = (uint32_t)((M - 1) * K);
+  const uint32_t kstep4 = (uint32_t)(4 * K);
 
-  auto load_sb = [&](StepRegs& r, int sb) {
+  auto issue = [&](int sb, uint8_t* sw, int8_t* sa) {
+    uint32_t wl0 = wlane;
+    asm volatile("" : "+v"(wl0));  // the offsets are recomputed per super-block, not held across it
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.a[i] = *(const uint4*)(arow[i] + (int64_t)sb * 256);
-    const uint8_t* blk = wrow + (int64_t)sb * 144;
-    r.hdr = *(const uint4*)blk;
-    r.q[0] = *(const uint4*)(blk + 16 + 32 * bj);
-    r.q[1] = *(const uint4*)(blk + 32 + 32 * bj);
-    if (tid < BM) {
-      r.dy = yd[ar * nsb + sb];
-      const uint4* bp = (const uint4*)(ybs + ar * (K / 16) + (int64_t)sb * 16);
-      r.bs0 = bp[0];
-      r.bs1 = bp[1];
+    for (int u = 0; u < 5; u++) {
+      const int i = wv + kWaves * u;
+      if (i < kWInstr) {
+        const int g = i / 9, j = i % 9;
+        const uint32_t row = wl0 + (uint32_t)(64 * g) * rowbytes;
+        const uint32_t off = (row < wlast ? row : wlast) + 16u * (uint32_t)j + 144u * (uint32_t)sb;
+        __builtin_amdgcn_global_load_lds((const void*)(W + off), (lds_void*)(sw + j * (BN * 16) + g * 1024), 16, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kAInstr / kWaves; u++) {
+      const int i = wv + kWaves * u;
+      const uint32_t row = arow0 + (uint32_t)(4 * i) * (kstep4 / 4);
+      const uint32_t off = (row < alast ? row : alast) + 16u * (lp ^ (4u * (uint32_t)(i & 3) + lq)) + 256u * (uint32_t)sb;
+      __builtin_amdgcn_global_load_lds((const void*)(yq + off), (lds_void*)(sa + 1024 * i), 16, 0, 0);
     }
   };
 
-  auto store_sb = [&](const StepRegs& r) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int p = tid + kThreads * i;
-      *(uint4*)&sm.a[p >> 4][16 * (p & 15)] = r.a[i];
+  // per-super-block activation scales: thread t < 256 takes row t/2, sub-blocks 4(t%2)..+3
+  const int srow = (tid & 255) >> 1, shalf = tid & 1;
+  const int64_t sgr = m0 + srow < M ? m0 + srow : M - 1;
+  const uint32_t doff = (uint32_t)(sgr * nsb);
+  const uint32_t boff = (uint32_t)(sgr * (K / 16) + 8 * shalf);
+  float sdy = 0.0f;
+  uint4 sbs = make_uint4(0, 0, 0, 0);
+  auto load_s = [&](int sb) {
+    if (tid < 256) {
+      sdy = yd[doff + (uint32_t)sb];
+      sbs = *(const uint4*)(ybs + (boff + 16u * (uint32_t)sb));
     }
-    // 6-bit scales and mins of the 8 sub-blocks (get_scale_min_k4, utils.rs:50-60)
-    const uint32_t u0 = r.hdr.y, u1 = r.hdr.z, u2 = r.hdr.w;
-    const uint32_t s03 = u0 & 0x3f3f3f3fu, m03 = u1 & 0x3f3f3f3fu;
-    const uint32_t s47 = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
-    const uint32_t m47 = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
-    if (bj == 0) {
-      const float d = h2f((uint16_t)(r.hdr.x & 0xFFFF)), dmin = h2f((uint16_t)(r.hdr.x >> 16));
-      h8 bm;
+  };
+  auto store_s = [&](int sb) {
+    _Float16 (*samin)[8] = s_amin[sb & 1];
+    float* sdyl = s_dy[sb & 1];
+    if (tid < 256) {
+      h4 am;
 #pragma unroll
-      for (int q = 0; q < 8; q++) bm[q] = (_Float16)(-dmin * (float)(((q < 4 ? m03 : m47) >> (8 * (q & 3))) & 0xFF));
-      *(h8*)&sm.bmin[bn][0] = bm;
-      sm.dw[bn] = d;
-    }
-    if (tid < BM) {
-      const uint32_t w[8] = {r.bs0.x, r.bs0.y, r.bs0.z, r.bs0.w, r.bs1.x, r.bs1.y, r.bs1.z, r.bs1.w};
-      h8 am;
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        // S_q = bsum_2q + bsum_2q+1 (the two int16 of word q)
-        const int sv = (int)(int16_t)(w[q] & 0xFFFF) + (int)(int16_t)(w[q] >> 16);
-        am[q] = (_Float16)(r.dy * (float)sv);
+      for (int q = 0; q < 4; q++) {
+        const uint32_t w = word(sbs, q);
+        const int sv = (int)(int16_t)(w & 0xFFFF) + (int)(int16_t)(w >> 16);
+        am[q] = (_Float16)(sdy * (float)sv);
       }
-      *(h8*)&sm.amin[tid][0] = am;
-      sm.dy[tid] = r.dy;
-    }
-    // chunk j = bj: code bytes 32j + 16i (i = 0, 1 -> offset l0 = 16i); low
-    // nibbles are values 64j + l0 + b (sub-block 2j), high 64j + 32 + l0 + b
-    const int j = bj;
-    const uint32_t sw = j < 2 ? s03 : s47;
-    const uint32_t sca = (sw >> (16 * (j & 1))) & 0xFF, scb = (sw >> (16 * (j & 1) + 8)) & 0xFF;
-    const uint32_t sla = dup16(sca & 7), sha = dup16(sca >> 3), slb = dup16(scb & 7), shb = dup16(scb >> 3);
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int l0 = 16 * i;
-      const uint32_t qw[4] = {r.q[i].x, r.q[i].y, r.q[i].z, r.q[i].w};
-      uint32_t lo_a[4], hi_a[4], lo_b[4], hi_b[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const uint32_t a = qw[e] & 0x0F0F0F0Fu, b = (qw[e] >> 4) & 0x0F0F0F0Fu;
-        lo_a[e] = pkmul(a, sla);
-        hi_a[e] = pkmul(a, sha);
-        lo_b[e] = pkmul(b, slb);
-        hi_b[e] = pkmul(b, shb);
-      }
-      *(uint4*)&sm.blo[bn][64 * j + l0] = make_uint4(lo_a[0], lo_a[1], lo_a[2], lo_a[3]);
-      *(uint4*)&sm.bhi[bn][64 * j + l0] = make_uint4(hi_a[0], hi_a[1], hi_a[2], hi_a[3]);
-      *(uint4*)&sm.blo[bn][64 * j + 32 + l0] = make_uint4(lo_b[0], lo_b[1], lo_b[2], lo_b[3]);
-      *(uint4*)&sm.bhi[bn][64 * j + 32 + l0] = make_uint4(hi_b[0], hi_b[1], hi_b[2], hi_b[3]);
+      *(h4*)&samin[srow][4 * shalf] = am;
+      if (shalf == 0) sdyl[srow] = sdy;
     }
   };
 
-  f16v acc[2];
+  f16v acc[4];
 #pragma unroll
-  for (int a = 0; a < 2; a++)
+  for (int t = 0; t < 4; t++)
 #pragma unroll
-    for (int i = 0; i < 16; i++) acc[a][i] = 0.0f;
+    for (int i = 0; i < 16; i++) acc[t][i] = 0.0f;
 
-  StepRegs regs;
-  load_sb(regs, 0);
-  const int r32 = lane & 31, kh = 16 * (lane >> 5);
-  const int nrow = 32 * wn + r32;  // this lane's weight row (output column) in the tile
-  for (int sb = 0; sb < nsb; sb++) {
-    // every wave is done with the previous super-block's LDS
-    if (sb > 0) __syncthreads();
-    store_sb(regs);
-    __syncthreads();
-    // the next super-block's bytes travel while this one is multiplied
-    if (sb + 1 < nsb) load_sb(regs, sb + 1);
+  issue(0, s_w0, s_a0);
+  load_s(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  store_s(0);
+  __syncthreads();
 
-    i16v clo[2], chi[2];
+  // The f32 epilogue of super-block sb: acc += (dy_m d_n) * T, then the min
+  // term f16(dy_m S_mj) x f16(-dmin_n m_nj) over the 8 sub-blocks (K padded
+  // to 16: lanes 32-63 carry zeros).
+  auto epilogue = [&](const i16v* c, int sb, float dw, float dmin, uint32_t m03, uint32_t m47) {
+    const float* sdyl = s_dy[sb & 1];
 #pragma unroll
-    for (int kc = 0; kc < 8; kc++) {
-      const i4v bl = *(const i4v*)&sm.blo[nrow][32 * kc + kh];
-      const i4v bhv = *(const i4v*)&sm.bhi[nrow][32 * kc + kh];
-#pragma unroll
-      for (int tm = 0; tm < 2; tm++) {
-        const i4v af = *(const i4v*)&sm.a[64 * wm + 32 * tm + r32][32 * kc + kh];
-        const i16v zero = {};
-        clo[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bl, kc ? clo[tm] : zero, 0, 0, 0);
-        chi[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bhv, kc ? chi[tm] : zero, 0, 0, 0);
-      }
-    }
-    // scale the super-block's integers into the f32 result, then the min term
-    const float dwn = sm.dw[nrow];
-#pragma unroll
-    for (int tm = 0; tm < 2; tm++) {
+    for (int t = 0; t < 4; t++) {
 #pragma unroll
       for (int g = 0; g < 4; g++) {
-        const float4 dy4 = *(const float4*)&sm.dy[64 * wm + 32 * tm + 8 * g + 4 * (lane >> 5)];
+        const float4 dy4 = *(const float4*)&sdyl[32 * t + 8 * g + 4 * h];
         const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const int i = 4 * g + e;
-          const int tot = (chi[tm][i] << 3) + clo[tm][i];
-          acc[tm][i] = __builtin_fmaf(dyv[e] * dwn, (float)tot, acc[tm][i]);
+          acc[t][i] = __builtin_fmaf(dyv[e] * dw, (float)c[t][i], acc[t][i]);
         }
       }
     }
-    const h8 z = {};
-    const h8 bmf = lane < 32 ? *(const h8*)&sm.bmin[nrow][0] : z;
+    h8 bm = {};
+    if (h == 0) {
 #pragma unroll
-    for (int tm = 0; tm < 2; tm++) {
-      const h8 amf = lane < 32 ? *(const h8*)&sm.amin[64 * wm + 32 * tm + r32][0] : z;
-      acc[tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(amf, bmf, acc[tm], 0, 0, 0);
+      for (int q = 0; q < 8; q++) bm[q] = (_Float16)(-dmin * (float)(((q < 4 ? m03 : m47) >> (8 * (q & 3))) & 0xFF));
     }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      h8 am = {};
+      if (h == 0) am = *(const h8*)&s_amin[sb & 1][32 * t + r32][0];
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, acc[t], 0, 0, 0);
+    }
+  };
+  i16v c[4];
+
+  const int wrow_lds = (32 * wv + r32) * 16;  // this lane's weight row in each plane
+  // one super-block from buffer half (sw, sa, samin, sdyl), the next one's
+  // copies into the other half
+  auto step = [&](int sb, const uint8_t* sw, const int8_t* sa, uint8_t* nw, int8_t* na) {
+    const bool more = sb + 1 < nsb;
+    if (more) {
+      load_s(sb + 1);
+      issue(sb + 1, nw, na);
+    }
+
+    WRaw cur;
+    {
+      const uint8_t* wl = sw + wrow_lds;
+      constexpr int P = BN * 16;  // bytes of a plane
+      cur.hdr = *(const uint4*)wl;
+      cur.c0 = *(const uint4*)(wl + (1 + h) * P);
+      cur.c1 = *(const uint4*)(wl + (3 + h) * P);
+      cur.c2 = *(const uint4*)(wl + (5 + h) * P);
+      cur.c3 = *(const uint4*)(wl + (7 + h) * P);
+    }
+    // this row's scales and mins (get_scale_min_k4, utils.rs:50-60)
+    const uint32_t u0 = cur.hdr.y, u1 = cur.hdr.z, u2 = cur.hdr.w;
+    const uint32_t s03 = u0 & 0x3f3f3f3fu, m03 = u1 & 0x3f3f3f3fu;
+    const uint32_t s47 = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+    const uint32_t m47 = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+    const float dw = h2f((uint16_t)(cur.hdr.x & 0xFFFF));
+    const float dmin = h2f((uint16_t)(cur.hdr.x >> 16));
+
+    // the int32 super-block sums: 8 * sum(y * sh q) + sum(y * sl q).
+    // A-operand piece of K-chunk kc: (2kc + h) ^ (r32 & 15) = 2 (kc ^ xh) + hl
+    const int xh = (r32 & 15) >> 1;
+    const int8_t* at = sa + r32 * 256 + 16 * (h ^ (r32 & 1));
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+      for (int kc = 0; kc < 8; kc++) {
+        const uint32_t sw = kc < 4 ? s03 : s47;
+        const uint32_t scv = (sw >> (8 * (kc & 3))) & 0xFF;
+        const uint32_t f = dup16(pass == 0 ? scv >> 3 : scv & 7);
+        const uint4& ch = chunk(cur, kc >> 1);
+        i4v b;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t w = word(ch, e);
+          b[e] = (int)pkmul((kc & 1) ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu, f);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const i4v a = *(const i4v*)(at + 32 * t * 256 + 32 * (kc ^ xh));
+          const i16v zero = {};
+          c[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, (pass == 0 && kc == 0) ? zero : c[t], 0, 0, 0);
+        }
+        // keep each K-chunk's operand loads next to its MFMAs (hoisting them all
+        // would hold 64 fragments in registers)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (pass == 0) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int i = 0; i < 16; i++) c[t][i] <<= 3;
+      }
+    }
+
+    epilogue(c, sb, dw, dmin, m03, m47);
+
+    if (more) {
+      // the next super-block's tiles and scales have landed
+      __builtin_amdgcn_s_waitcnt(0);
+      store_s(sb + 1);
+    }
+    // every wave is done with this buffer, and the next one is complete
+    __syncthreads();
+  };
+  for (int sb = 0; sb < nsb; sb += 2) {
+    step(sb, s_w0, s_a0, s_w1, s_a1);
+    if (sb + 1 < nsb) step(sb + 1, s_w1, s_a1, s_w0, s_a0);
   }
 
-  // store
-  const int64_t col = n0 + nrow;
+  const int64_t col = n0 + 32 * wv + r32;
   if (col < N) {
 #pragma unroll
-    for (int tm = 0; tm < 2; tm++)
+    for (int t = 0; t < 4; t++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const int64_t row = m0 + 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < M) dst[row * ldd + col] = acc[tm][i];
+        const int64_t row = m0 + 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (row < M) dst[row * ldd + col] = acc[t][i];
       }
   }
 }
+
+constexpr int kWavesWide = 8, kWavesNarrow = 4;
 
 }  // namespace
 
 int gemm_q4k_min_rows() { return 9; }
 
+bool gemm_q4k_fits(int64_t n, int64_t k, int64_t rows) {
+  // 32-bit byte offsets inside the kernel
+  return k % 256 == 0 && n * (k / 256) * 144 < ((int64_t)1 << 31) && (rows + BM) * k < ((int64_t)1 << 31);
+}
+
 hipError_t launch_gemm_q4k(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
                            int64_t ldd, hipStream_t st) {
-  const dim3 grid((unsigned)((n + BN - 1) / BN), (unsigned)((rows + BM - 1) / BM));
-  gemm_q4k_kernel<<<grid, kThreads, 0, st>>>((const uint8_t*)w, n, (int)(k / 256), p.codes, p.d,
-                                             (const int16_t*)p.sums, rows, dst, ldd);
+  // 256-column tiles where they give the grid at least one workgroup per
+  // CU-sized share, 128-column tiles otherwise
+  const int64_t mt = (rows + BM - 1) / BM;
+  const bool wide = ((n + 255) / 256) * mt >= 192;
+  const int nsb = (int)(k / 256);
+  if (wide) {
+    const dim3 grid((unsigned)((n + 255) / 256), (unsigned)mt);
+    gemm_q4k_kernel<kWavesWide><<<grid, 64 * kWavesWide, 0, st>>>((const uint8_t*)w, n, nsb, p.codes, p.d,
+                                                                  (const int16_t*)p.sums, rows, dst, ldd);
+  } else {
+    const dim3 grid((unsigned)((n + 127) / 128), (unsigned)mt);
+    gemm_q4k_kernel<kWavesNarrow><<<grid, 64 * kWavesNarrow, 0, st>>>((const uint8_t*)w, n, nsb, p.codes, p.d,
+                                                                      (const int16_t*)p.sums, rows, dst, ldd);
+  }
   return hipGetLastError();
 }
 

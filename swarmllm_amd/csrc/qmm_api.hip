@@ -76,6 +76,14 @@ int cu_count() {
   return cached[dev];
 }
 
+// The int8 matrix-core GEMM: Q4_K from gemm_q4k_min_rows() rows, weight and
+// quantized activation 16-byte aligned (its 16-byte copies), sizes inside its
+// 32-bit offsets.
+bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows) {
+  return type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && ((uintptr_t)w & 15) == 0 &&
+         ((uintptr_t)xq & 15) == 0 && qmm::gemm_q4k_fits(n, k, rows);
+}
+
 // The streaming decode kernels (Q4_K, Q6_K at 1-2 activation rows).
 bool stream_supported(int type, int64_t k, int64_t rows) {
   if (type == qmm::T_Q4_K) return qmm::mv_q4k_rows_supported(k, rows);
@@ -215,7 +223,7 @@ int qmm_matmul(int type, const void* w, const void* xq, float* dst, int64_t ldd,
   const qmm::ActPlanes p = qmm::act_planes(layout, (void*)xq, k, rows);
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
-  if (type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && ((uintptr_t)w & 15) == 0) {
+  if (gemm_takes(type, w, xq, n, k, rows)) {
     if (qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
@@ -256,7 +264,7 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   hipError_t e = qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st);
   if (e != hipSuccess) return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
-  if (type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && ((uintptr_t)w & 15) == 0) {
+  if (gemm_takes(type, w, workspace, n, k, rows)) {
     // prefill: the int8 matrix-core GEMM
     if (qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
@@ -312,7 +320,7 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
   const int64_t step = qmm::matvec_max_rows();
   for (int i = 0; i < count; i++) {
-    if (type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && ((uintptr_t)w[i] & 15) == 0) {
+    if (gemm_takes(type, w[i], workspace, n[i], k, rows)) {
       if (qmm::launch_gemm_q4k(w[i], n[i], k, p, rows, dst[i], ldd[i], st) != hipSuccess) return QMM_DEVICE_ERROR;
       g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
       continue;

@@ -91,6 +91,9 @@ hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, 
 // dst = x · Wᵀ for a Q4_K weight from the Q8_K activation planes of `rows`
 // rows (qmm_quantize_act ACT_Q8K); used from gemm_q4k_min_rows() rows up.
 int gemm_q4k_min_rows();
+// The GEMM indexes with 32-bit byte offsets: the weight below 2 GiB and
+// (rows + 128) * k below 2^31.
+bool gemm_q4k_fits(int64_t n, int64_t k, int64_t rows);
 hipError_t launch_gemm_q4k(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
                            int64_t ldd, hipStream_t s);
 
