@@ -7,6 +7,8 @@
 #pragma once
 
 #include "qmm_device.h"
+
+#include <mutex>
 #include "qmm_launch.h"
 
 namespace qmm {
@@ -169,5 +171,19 @@ __device__ __forceinline__ void lds_words(const uint8_t* lds, int off, uint32_t*
   for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], s);
 }
 __device__ __forceinline__ uint32_t lds_u16(const uint8_t* lds, int off) { return lds_u32(lds, off) & 0xFFFF; }
+
+// Dynamic LDS past 64 KiB needs the kernel's limit raised (to the 160 KiB of
+// a CU), once per kernel function.
+inline hipError_t set_max_dynamic_lds(const void* fn) {
+  static std::mutex mu;
+  static const void* done[64];
+  static int ndone = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < ndone; i++)
+    if (done[i] == fn) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (e == hipSuccess && ndone < 64) done[ndone++] = fn;
+  return e;
+}
 
 }  // namespace qmm

@@ -55,6 +55,53 @@ __device__ __forceinline__ void load_row(RowRegs<T>& rr, const uint8_t* __restri
   }
 }
 
+// The row as contiguous 16-byte pieces: lane L holds pieces L + 64c. Each
+// byte is loaded once, by one lane, so the loads can take the nontemporal
+// hint; a wave-private LDS slot then turns them into the per-lane layout of
+// RowRegs (unpack_row).
+template <int T>
+struct RowRaw {
+  static constexpr int kLoads = (9 * 16 * T + 63) / 64;  // 9 pieces per super-block
+  uint4 p[kLoads];
+};
+
+template <int T>
+__device__ __forceinline__ void load_raw(RowRaw<T>& rr, const uint8_t* __restrict__ row, int nsb, int lane) {
+  const int pieces = 9 * nsb;
+#pragma unroll
+  for (int c = 0; c < RowRaw<T>::kLoads; c++) {
+    const int pc = lane + 64 * c;
+    rr.p[c] = pc < pieces ? ld_stream16(row + 16 * pc) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Writes the row's pieces to the wave's LDS slot and reads back the header and
+// code bytes of this lane's units. The next row's writes reach the slot after
+// these reads: LDS operations of one wave complete in order.
+template <int T>
+__device__ __forceinline__ void unpack_row(const RowRaw<T>& rr, uint8_t* slot, RowRegs<T>& out, int nsb, int lane) {
+  const int pieces = 9 * nsb;
+#pragma unroll
+  for (int c = 0; c < RowRaw<T>::kLoads; c++) {
+    const int pc = lane + 64 * c;
+    if (pc < pieces) *(uint4*)(slot + 16 * pc) = rr.p[c];
+  }
+  wave_lds_sync();
+  const int j = lane & 3, sbl = lane >> 2;
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const int sb = sbl + 16 * t;
+    if (sb < nsb) {
+      const uint8_t* blk = slot + sb * 144;
+      out.h[t] = *(const uint4*)blk;
+      out.qa[t] = *(const uint4*)(blk + 16 + 32 * j);
+      out.qb[t] = *(const uint4*)(blk + 32 + 32 * j);
+    } else {
+      out.h[t] = out.qa[t] = out.qb[t] = make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
 // A lane's slice of one activation row: the 64 codes of its unit per
 // super-block t, dy, and the code sums of sub-blocks 2j, 2j+1.
 template <int T>
@@ -64,7 +111,7 @@ struct ActRegs {
   int32_t p0[T], p1[T];
 };
 
-template <int NR, int T, bool FUSED, int kWaves, bool PF>
+template <int NR, int T, bool FUSED, int kWaves, bool PF, bool XCHG>
 __global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
                                                             int64_t xstride, const int8_t* __restrict__ yq,
                                                             const float* __restrict__ yd,
@@ -92,13 +139,22 @@ __global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg
     return (const uint8_t*)tg.w[t] + lrow * rowbytes;
   };
 
+  // XCHG: the wave's LDS slot for unpacking contiguous row loads, after the activation
+  uint8_t* slot = smem + act_lds_bytes(NR, nsb) + (size_t)wv * 144 * nsb;
+
   // 1. activation loads, then the first row's weight loads
   ActBatch<NR, FUSED, kWaves> act;
   act.load(nsb, x, xstride, yq, yd, ybs);
   RowRegs<T> cur;
+  RowRaw<T> craw;
   float* out = nullptr;
   int64_t ldd = 0;
-  if (gw < n_total) load_row<T>(cur, row_ptr(gw, out, ldd), nsb, lane);
+  if (gw < n_total) {
+    if (XCHG)
+      load_raw<T>(craw, row_ptr(gw, out, ldd), nsb, lane);
+    else
+      load_row<T>(cur, row_ptr(gw, out, ldd), nsb, lane);
+  }
 
   // 2. the activation into LDS, then each lane's slice into registers
   act.store(s, nsb, x, xstride, yq, yd, ybs, qmax);
@@ -132,9 +188,16 @@ __global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg
   for (int64_t R = gw; R < n_total; R += W) {
     // PF: the next row's loads go out before this row's compute
     RowRegs<T> nxt;
+    RowRaw<T> nraw;
     float* nout = nullptr;
     int64_t nldd = 0;
-    if (PF && R + W < n_total) load_row<T>(nxt, row_ptr(R + W, nout, nldd), nsb, lane);
+    if (PF && R + W < n_total) {
+      if (XCHG)
+        load_raw<T>(nraw, row_ptr(R + W, nout, nldd), nsb, lane);
+      else
+        load_row<T>(nxt, row_ptr(R + W, nout, nldd), nsb, lane);
+    }
+    if (XCHG) unpack_row<T>(craw, slot, cur, nsb, lane);
 
     float acc[NR];
 #pragma unroll
@@ -150,27 +213,48 @@ __global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg
       if (lane == 0) out[r * ldd] = v;
     }
     if (PF) {
-      cur = nxt;
+      if (XCHG)
+        craw = nraw;
+      else
+        cur = nxt;
       out = nout;
       ldd = nldd;
     } else if (R + W < n_total) {
-      load_row<T>(cur, row_ptr(R + W, out, ldd), nsb, lane);
+      if (XCHG)
+        load_raw<T>(craw, row_ptr(R + W, out, ldd), nsb, lane);
+      else
+        load_row<T>(cur, row_ptr(R + W, out, ldd), nsb, lane);
     }
   }
+}
+
+// Rows are unpacked through LDS (contiguous nontemporal loads) up to 4096
+// values a row, where two 16-wave workgroups' slots (36 KB each) still fit a
+// CU beside their activations.
+inline bool q4k_xchg(int nsb) { return nsb <= 16; }
+
+template <int NR, int T, int WPG, bool PF, bool XCHG>
+hipError_t launch_stream_x(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
+                           float qmax, int64_t waves, hipStream_t st) {
+  const size_t lds = act_lds_bytes(NR, nsb) + (XCHG ? (size_t)WPG * 144 * nsb : 0);
+  const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
+  if (pre) {
+    auto* k = mv_q4k_stream_kernel<NR, T, false, WPG, PF, XCHG>;
+    if (lds > 65536 && set_max_dynamic_lds((const void*)k) != hipSuccess) return hipErrorInvalidValue;
+    k<<<grid, 64 * WPG, lds, st>>>(t, nsb, nullptr, 0, pre->codes, pre->d, (const int16_t*)pre->sums, qmax);
+  } else {
+    auto* k = mv_q4k_stream_kernel<NR, T, true, WPG, PF, XCHG>;
+    if (lds > 65536 && set_max_dynamic_lds((const void*)k) != hipSuccess) return hipErrorInvalidValue;
+    k<<<grid, 64 * WPG, lds, st>>>(t, nsb, x, xstride, nullptr, nullptr, nullptr, qmax);
+  }
+  return hipGetLastError();
 }
 
 template <int NR, int T, int WPG, bool PF>
 hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
                          float qmax, int64_t waves, hipStream_t st) {
-  const size_t lds = act_lds_bytes(NR, nsb);
-  const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
-  if (pre)
-    mv_q4k_stream_kernel<NR, T, false, WPG, PF><<<grid, 64 * WPG, lds, st>>>(t, nsb, nullptr, 0, pre->codes, pre->d,
-                                                                          (const int16_t*)pre->sums, qmax);
-  else
-    mv_q4k_stream_kernel<NR, T, true, WPG, PF><<<grid, 64 * WPG, lds, st>>>(t, nsb, x, xstride, nullptr, nullptr,
-                                                                         nullptr, qmax);
-  return hipGetLastError();
+  if (T <= 2 && q4k_xchg(nsb)) return launch_stream_x<NR, T, WPG, PF, true>(t, nsb, x, xstride, pre, qmax, waves, st);
+  return launch_stream_x<NR, T, WPG, PF, false>(t, nsb, x, xstride, pre, qmax, waves, st);
 }
 
 template <int NR, int T>

@@ -52,7 +52,7 @@ __device__ __forceinline__ void load_span(Span& sp, const uint8_t* __restrict__ 
 #pragma unroll
   for (int c = 0; c < kPiecesPerLane; c++) {
     const int pc = lane + 64 * c;
-    sp.p[c] = pc < pieces ? *(const uint4*)(a0 + 16 * pc) : make_uint4(0, 0, 0, 0);
+    sp.p[c] = pc < pieces ? ld_stream16(a0 + 16 * pc) : make_uint4(0, 0, 0, 0);
   }
 }
 

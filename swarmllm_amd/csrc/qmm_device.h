@@ -45,6 +45,16 @@ __device__ __constant__ static const int8_t kMxfp4Values[16] = {0, 1, 2, 3, 4, 6
 
 // ---- f16 <-> f32 (IEEE binary16, round to nearest even; f16 denormals kept)
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// A 16-byte load of weight bytes a product reads once, each byte by exactly
+// one load: the nontemporal hint streams them past the caches (measured ~10%
+// more HBM throughput for contiguous pieces on gfx950). Loads that share
+// cache lines must not use it: each would fetch the line again.
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  const v4u t = __builtin_nontemporal_load((const v4u*)p);
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
 // f32 -> f16 in integer arithmetic. A plain (_Float16) cast of a product may
 // be folded into a mixed-precision multiply-add with +0, which turns -0 into
 // +0; the conversion here is the IEEE one for every input, signed zeros and
