@@ -133,6 +133,29 @@ int qmm_forward_shared(int type, int count, const void *const *w, const int64_t 
                        size_t workspace_bytes, size_t *need, int64_t k, int64_t rows, int launch,
                        int64_t stream);
 
+/* Grouped expert products (mixture-of-experts layers). Routing entry i
+ * (i < size_m) pairs sorted_ids[i] (a token's k-th choice, numbered
+ * token * topk + k) with expert expert_ids[i]; it writes
+ *   dst[p][j] = scale_p * (x[in_p] . W_e[j])   for j < n,
+ * p = sorted_ids[i], e = expert_ids[i], in_p = p when topk_w is given (one
+ * input row per pair, size_m rows) else p / topk (one per token, size_m/topk
+ * rows), scale_p = topk_w[p] or 1. `w` holds num_experts weights of n x k
+ * back to back, each in GGUF blocks of `type` (Q8_0, IQ4_NL or MXFP4). The
+ * activation is quantized per 32 values (Q8_0). Entries whose expert or pair
+ * is out of range write nothing. Entries with one expert read its weights
+ * once when they are consecutive (ids sorted by expert); any order gives
+ * the same result. Each dst[p] equals qmm_forward of x[in_p] against W_e,
+ * times scale_p, bit for bit. Plan (launch == 0) and launch as qmm_forward:
+ * the workspace holds the quantized activation and the routing runs.
+ * Replaces moe_gemm_gguf (candle-kernels/src/moe/moe_gguf.cu:149-252,
+ * which allocates its own scratch) as called from
+ * src/layers/moe_card.rs:48-170, and QMatMul::matmul_many over the touched
+ * experts (quantized/mod.rs:697-780). */
+int qmm_moe_forward(int type, const void *w, int num_experts, const float *x, int64_t x_stride,
+                    const int32_t *sorted_ids, const int32_t *expert_ids, const float *topk_w, int topk,
+                    float *dst, int64_t ldd, void *workspace, size_t workspace_bytes, size_t *need, int64_t k,
+                    int64_t n, int64_t size_m, int launch, int64_t stream);
+
 /* Dequantize `nelem` values of weight type `type` into f32 (out_f16 == 0)
  * or IEEE f16 (out_f16 != 0; each value is f16 of the f32 one).
  * Replaces QCudaStorage::dequantize / dequantize_f16
@@ -166,6 +189,7 @@ int qmm_fill_normal(float *out, int64_t n, uint64_t seed, float mean, float std,
  * quantized/cuda.rs:937-945): matvec launches, GEMM launches. */
 uint64_t qmm_matvec_launches(void);
 uint64_t qmm_gemm_launches(void);
+uint64_t qmm_moe_launches(void);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,8 @@ SIGNATURES = {
     "qmm_forward": (_I, [_I, _P, _P, _I64, _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64, _I64, _I64, _I, _I64]),
     "qmm_forward_shared": (_I, [_I, _I, ctypes.POINTER(_P), ctypes.POINTER(_I64), ctypes.POINTER(_P),
                                 ctypes.POINTER(_I64), _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64, _I64, _I, _I64]),
+    "qmm_moe_forward": (_I, [_I, _P, _I, _P, _I64, _P, _P, _P, _I, _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64,
+                             _I64, _I64, _I, _I64]),
     "qmm_dequantize": (_I, [_I, _P, _P, _I, _I64, _I64]),
     "qmm_quantize_scratch_bytes": (_SZ, [_I, _I64]),
     "qmm_quantize_weights": (_I, [_I, _P, _P, _I64, _P, _SZ, _I64]),
@@ -47,6 +49,7 @@ SIGNATURES = {
     "qmm_fill_normal": (_I, [_P, _I64, _U64, ctypes.c_float, ctypes.c_float, _I64]),
     "qmm_matvec_launches": (_U64, []),
     "qmm_gemm_launches": (_U64, []),
+    "qmm_moe_launches": (_U64, []),
 }
 
 _lib = None

@@ -10,7 +10,7 @@
 //
 // Weights are read in GGUF bytes. The activation comes in the planes of
 // qmm_launch.h (codes / scales / group sums, 16-byte aligned).
-#include "mv_common.h"
+#include "b32_common.h"
 
 namespace qmm {
 
@@ -73,15 +73,6 @@ __global__ __launch_bounds__(256) void mv_q4k_kernel(const uint8_t* __restrict__
       const float v = wave_sum_dpp(acc[r][i]);
       if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
     }
-}
-
-// 16-entry int8 table lookup of the 4 nibbles in the bytes of n (each < 16).
-__device__ __forceinline__ int32_t lut16(uint32_t n, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
-  const uint32_t sel = n & 0x07070707u;
-  const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
-  const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
-  const uint32_t m = ((n >> 3) & 0x01010101u) * 0xFFu;
-  return (int32_t)((hi & m) | (lo & ~m));
 }
 
 // ===========================================================================
@@ -187,55 +178,9 @@ __global__ __launch_bounds__(256) void mv_q6k_kernel(const uint8_t* __restrict__
 
 // ===========================================================================
 // 32-value formats (Q8_0, MXFP4, IQ4_NL) from LDS. Lane = unit of two
-// blocks (64 values); a span is 128 blocks.
+// blocks (64 values); a span is 128 blocks. Decode and per-unit arithmetic:
+// b32_common.h.
 // ===========================================================================
-template <int FMT>
-struct Fmt32;
-template <>
-struct Fmt32<T_Q8_0> {
-  static constexpr int B = 34;
-  __device__ static void decode(const uint8_t* L, int off, uint32_t q[8], float& d, uint32_t, uint32_t, uint32_t,
-                                uint32_t) {
-    d = h2f((uint16_t)lds_u16(L, off));
-    lds_words<8>(L, off + 2, q);
-  }
-};
-template <>
-struct Fmt32<T_IQ4_NL> {
-  static constexpr int B = 18;
-  __device__ static void decode(const uint8_t* L, int off, uint32_t q[8], float& d, uint32_t t0, uint32_t t1,
-                                uint32_t t2, uint32_t t3) {
-    d = h2f((uint16_t)lds_u16(L, off));
-    uint32_t n[4];
-    lds_words<4>(L, off + 2, n);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      q[i] = (uint32_t)lut16(n[i] & 0x0F0F0F0Fu, t0, t1, t2, t3);
-      q[4 + i] = (uint32_t)lut16((n[i] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
-    }
-  }
-};
-template <>
-struct Fmt32<T_MXFP4> {
-  static constexpr int B = 17;
-  __device__ static void decode(const uint8_t* L, int off, uint32_t q[8], float& d, uint32_t t0, uint32_t t1,
-                                uint32_t t2, uint32_t t3) {
-    d = e8m0_half(lds_u32(L, off) & 0xFF);
-    uint32_t n[4];
-    lds_words<4>(L, off + 1, n);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      q[i] = (uint32_t)lut16(n[i] & 0x0F0F0F0Fu, t0, t1, t2, t3);
-      q[4 + i] = (uint32_t)lut16((n[i] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
-    }
-  }
-};
-
-__device__ __forceinline__ uint32_t pack4(const int8_t* t) {
-  return (uint32_t)(uint8_t)t[0] | ((uint32_t)(uint8_t)t[1] << 8) | ((uint32_t)(uint8_t)t[2] << 16) |
-         ((uint32_t)(uint8_t)t[3] << 24);
-}
-
 template <int FMT, int NR, int RPW>
 __global__ __launch_bounds__(256) void mv_b32_kernel(const uint8_t* __restrict__ W, int64_t n, int nb,
                                                      const int8_t* __restrict__ yq, const float* __restrict__ yd,
@@ -248,8 +193,8 @@ __global__ __launch_bounds__(256) void mv_b32_kernel(const uint8_t* __restrict__
   if (row0 >= n) return;
   const int64_t k = (int64_t)nb * 32;
   const int64_t rb = (int64_t)nb * F::B;
-  const int8_t* tab = FMT == T_MXFP4 ? kMxfp4Values : kIq4nlValues;
-  const uint32_t t0 = pack4(tab), t1 = pack4(tab + 4), t2 = pack4(tab + 8), t3 = pack4(tab + 12);
+  const Lut32<FMT> lut;
+  const uint32_t t0 = lut.t0, t1 = lut.t1, t2 = lut.t2, t3 = lut.t3;
   float acc[NR][RPW];
 #pragma unroll
   for (int r = 0; r < NR; r++)
@@ -285,35 +230,10 @@ __global__ __launch_bounds__(256) void mv_b32_kernel(const uint8_t* __restrict__
       const int64_t gb = b0 + bl;  // global block index within the row
 #pragma unroll
       for (int r = 0; r < NR; r++) {
-        const int8_t* yrow = yq + r * k + gb * 32;
-        int yv[2][8];
-        {
-          const int4 a = *(const int4*)yrow;
-          const int4 b = *(const int4*)(yrow + 16);
-          yv[0][0] = a.x; yv[0][1] = a.y; yv[0][2] = a.z; yv[0][3] = a.w;
-          yv[0][4] = b.x; yv[0][5] = b.y; yv[0][6] = b.z; yv[0][7] = b.w;
-        }
-        float dy0 = yd[r * nb + gb], dy1 = 0.0f;
-        if (two) {
-          const int4 a = *(const int4*)(yrow + 32);
-          const int4 b = *(const int4*)(yrow + 48);
-          yv[1][0] = a.x; yv[1][1] = a.y; yv[1][2] = a.z; yv[1][3] = a.w;
-          yv[1][4] = b.x; yv[1][5] = b.y; yv[1][6] = b.z; yv[1][7] = b.w;
-          dy1 = yd[r * nb + gb + 1];
-        } else {
+        Act64 av;
+        load_act64(av, yq, yd, r, k, nb, gb, two);
 #pragma unroll
-          for (int t = 0; t < 8; t++) yv[1][t] = 0;
-        }
-#pragma unroll
-        for (int i = 0; i < RPW; i++) {
-          int s0 = 0, s1 = 0;
-#pragma unroll
-          for (int t = 0; t < 8; t++) {
-            s0 = dot4((int)q[i][0][t], yv[0][t], s0);
-            s1 = dot4((int)q[i][1][t], yv[1][t], s1);
-          }
-          acc[r][i] += (dx[i][0] * dy0) * (float)s0 + (dx[i][1] * dy1) * (float)s1;
-        }
+        for (int i = 0; i < RPW; i++) acc[r][i] = b32_unit(q[i][0], q[i][1], dx[i][0], dx[i][1], av, acc[r][i]);
       }
     }
   }
@@ -321,7 +241,7 @@ __global__ __launch_bounds__(256) void mv_b32_kernel(const uint8_t* __restrict__
   for (int r = 0; r < NR; r++)
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
-      const float v = wave_sum(acc[r][i]);
+      const float v = wave_sum_dpp(acc[r][i]);
       if (lane == 0 && row0 + i < n) dst[r * ldd + row0 + i] = v;
     }
 }

@@ -16,6 +16,7 @@ namespace {
 std::atomic<uint64_t> g_matvec_launches{0};
 std::atomic<uint64_t> g_gemm_launches{0};
 std::atomic<bool> g_fail_next{false};
+std::atomic<uint64_t> g_moe_launches{0};
 
 int block_size(int type) {
   switch (type) {
@@ -360,6 +361,36 @@ int qmm_quantize_weights(int type, const float* x, void* w, int64_t nelem, void*
   clear_stale_error();
   return status_of(qmm::launch_weight_quantize(type, x, w, nelem, scratch, (hipStream_t)stream));
 }
+
+int qmm_moe_forward(int type, const void* w, int num_experts, const float* x, int64_t x_stride,
+                    const int32_t* sorted_ids, const int32_t* expert_ids, const float* topk_w, int topk, float* dst,
+                    int64_t ldd, void* workspace, size_t workspace_bytes, size_t* need, int64_t k, int64_t n,
+                    int64_t size_m, int launch, int64_t stream) {
+  if (!qmm::moe_supported(type) || !shape_ok(type, k, n, size_m) || need == nullptr || ldd < n || x_stride < k ||
+      num_experts < 1 || topk < 1 || (topk_w == nullptr && size_m % topk != 0) || size_m > ((int64_t)1 << 30))
+    return QMM_UNSUPPORTED;
+  const int64_t in_rows = topk_w ? size_m : size_m / topk;
+  const size_t act = (qmm::act_bytes(qmm::ACT_Q8_0, k, in_rows) + 255) / 256 * 256;
+  const size_t bytes = act + qmm::moe_runs_bytes(size_m);
+  *need = bytes;
+  if (!launch) return QMM_OK;
+  if (g_fail_next.exchange(false)) return QMM_NO_ROOM;
+  if (workspace_bytes < bytes || workspace == nullptr) return QMM_WORKSPACE_TOO_SMALL;
+  if (!w || !x || !dst || !sorted_ids || !expert_ids) return QMM_UNSUPPORTED;
+  const hipStream_t st = (hipStream_t)stream;
+  clear_stale_error();
+  if (qmm::launch_act_quantize(qmm::ACT_Q8_0, x, x_stride, k, in_rows, workspace, q8k_scale(), st) != hipSuccess)
+    return QMM_DEVICE_ERROR;
+  const qmm::ActPlanes p = qmm::act_planes(qmm::ACT_Q8_0, workspace, k, in_rows);
+  int32_t* runs = (int32_t*)((char*)workspace + act);
+  if (qmm::launch_moe(type, w, num_experts, n, k, p, runs, sorted_ids, expert_ids, topk_w, topk, size_m, dst, ldd,
+                      st) != hipSuccess)
+    return QMM_DEVICE_ERROR;
+  g_moe_launches.fetch_add(1, std::memory_order_relaxed);
+  return QMM_OK;
+}
+
+uint64_t qmm_moe_launches(void) { return g_moe_launches.load(std::memory_order_relaxed); }
 
 void qmm_fail_next_launch(void) { g_fail_next.store(true); }
 

@@ -11,11 +11,11 @@ namespace qmm {
 // ---- activation layouts on the device --------------------------------------
 // The codes, scales and sums are bit-for-bit those of candle's BlockQ8K /
 // BlockQ8_0 from_float; only their placement differs: planes, 16-B aligned.
-//   ACT_Q8K (per 256, for Q4_K / Q6_K):
+//   ACT_Q8K (per 256, for Q4_K / Q6_K, decode and the MFMA GEMM):
 //     codes  int8  [rows][k]
 //     d      f32   [rows][k/256]
 //     bsums  int16 [rows][k/16]
-//   ACT_Q8_0 (per 32, for Q8_0 / MXFP4 / IQ4_NL, and the MFMA GEMM of every type):
+//   ACT_Q8_0 (per 32, for Q8_0 / MXFP4 / IQ4_NL, products and grouped experts):
 //     codes  int8  [rows][k]
 //     d      f32   [rows][k/32]   (the f16 scale, widened exactly)
 //     sums   int32 [rows][k/32]   (exact sum of the block's codes)
@@ -90,6 +90,15 @@ hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, 
 // ---- prefill GEMM on the int8 matrix cores --------------------------------
 // dst = x · Wᵀ for a Q4_K weight from the Q8_K activation planes of `rows`
 // rows (qmm_quantize_act ACT_Q8K); used from gemm_q4k_min_rows() rows up.
+// Grouped expert products (moe.hip): types it covers, bytes of the run table
+// for size_m routing entries, and the launch (run pre-pass + grouped kernel)
+// from an activation already quantized in Q8_0 planes.
+bool moe_supported(int type);
+size_t moe_runs_bytes(int64_t size_m);
+hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
+                      int32_t* runs, const int32_t* ids, const int32_t* expert_ids, const float* topk_w, int topk,
+                      int64_t size_m, float* dst, int64_t ldd, hipStream_t st);
+
 int gemm_q4k_min_rows();
 // The GEMM indexes with 32-bit byte offsets: the weight below 2 GiB and
 // (rows + 128) * k below 2^31.

@@ -15,7 +15,7 @@ from __future__ import annotations
 import ctypes
 import enum
 from dataclasses import dataclass
-from typing import List, Sequence
+from typing import List, Optional, Sequence
 
 import torch
 
@@ -55,20 +55,35 @@ def fill_normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0, device="
 
 
 class QTensor:
-    """GGUF blocks of a 2-D weight [n, k] on the device (mod.rs:76)."""
+    """GGUF blocks of a weight on the device (mod.rs:76): [n, k] for a
+    product, [E, n, k] for a stack of expert weights (one n x k matrix per
+    expert, back to back, as stack_some / load_quantized_entries build them,
+    mod.rs:989-1025)."""
 
     def __init__(self, data: torch.Tensor, shape: Sequence[int], dtype: GgmlDType):
         dtype = GgmlDType(dtype)
-        n, k = shape
+        shape = tuple(int(d) for d in shape)
+        if len(shape) < 2:
+            raise ValueError(f"QTensor: shape {shape} has fewer than 2 dims")
+        k = shape[-1]
         qk = dtype.block_size()
         if k % qk:
             raise ValueError(f"quantized tensor must have their last dim divisible by block size {shape} {qk}")
-        want = lib().qmm_type_bytes(int(dtype), n * k)
+        nel = 1
+        for d in shape:
+            nel *= d
+        want = lib().qmm_type_bytes(int(dtype), nel)
         if data.dtype != torch.uint8 or data.numel() != want or not data.is_cuda:
             raise ValueError(f"QTensor: {data.numel()} device bytes for {shape} {dtype.name} (want {want})")
         self.data_ = data.contiguous()
-        self.shape = (int(n), int(k))
+        self.shape = shape
         self.dtype = dtype
+
+    def elem_count(self) -> int:
+        nel = 1
+        for d in self.shape:
+            nel *= d
+        return nel
 
     @staticmethod
     def from_data(raw: bytes, shape: Sequence[int], dtype: GgmlDType, device="cuda") -> "QTensor":
@@ -101,10 +116,9 @@ class QTensor:
         return self._dequant(True)
 
     def _dequant(self, f16: bool) -> torch.Tensor:
-        n, k = self.shape
-        out = torch.empty((n, k), dtype=torch.float16 if f16 else torch.float32, device=self.data_.device)
-        check("qmm_dequantize",
-              lib().qmm_dequantize(int(self.dtype), _ptr(self.data_), _ptr(out), int(f16), n * k, _stream()))
+        out = torch.empty(self.shape, dtype=torch.float16 if f16 else torch.float32, device=self.data_.device)
+        check("qmm_dequantize", lib().qmm_dequantize(int(self.dtype), _ptr(self.data_), _ptr(out), int(f16),
+                                                     self.elem_count(), _stream()))
         return out
 
     def data(self) -> bytes:
@@ -143,6 +157,8 @@ class QMatMul:
 
     def forward(self, xs: torch.Tensor) -> torch.Tensor:
         """x [..., k] f32 -> [..., n]; the CustomOp1 shape rules of cpu_fwd (mod.rs:1280-1333)."""
+        if len(self.qtensor.shape) != 2:
+            raise ValueError(f"QMatMul::forward: a [n, k] weight, not {self.qtensor.shape}")
         n, k = self.qtensor.shape
         if xs.dim() < 1 or xs.shape[-1] != k:
             raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with {self.qtensor.shape}")
@@ -206,6 +222,44 @@ class QMatMul:
             check("qmm_forward_shared", L.qmm_forward_shared(t, cnt, wp, ns, dp, ld, _ptr(xs), k, _ptr(buf),
                                                              buf.numel(), ctypes.byref(need), k, rows, 1, st))
         return outs
+
+
+def moe_forward(xs: torch.Tensor, experts: QTensor, sorted_ids: torch.Tensor, expert_ids: torch.Tensor,
+                topk_weights: Optional[torch.Tensor], topk: int, workspace: Optional[Workspace] = None) -> torch.Tensor:
+    """The grouped expert products of moe_gemm_gguf (candle-kernels/src/moe/
+    moe_gguf.cu:149-252, as layers::moe_card calls it, moe_card.rs:48-170):
+    experts [E, n, k] in GGUF blocks; routing entry i pairs sorted_ids[i]
+    (token * topk + k-th choice) with expert_ids[i]; xs holds one row per
+    pair when topk_weights is given (each output row then scaled by its
+    pair's weight), else one row per token. Returns [len(sorted_ids), n]
+    f32, row p the product of pair p (qmm_moe_forward)."""
+    if len(experts.shape) != 3:
+        raise ValueError(f"moe_forward: expert weights [E, n, k], not {experts.shape}")
+    e, n, k = experts.shape
+    if xs.dtype != torch.float32 or xs.dim() != 2 or xs.shape[1] != k or not xs.is_contiguous():
+        raise ValueError(f"moe_forward: input [rows, {k}] contiguous f32, not {tuple(xs.shape)} {xs.dtype}")
+    size_m = int(sorted_ids.numel())
+    for name, t in (("sorted_ids", sorted_ids), ("expert_ids", expert_ids)):
+        if t.dtype != torch.int32 or t.numel() != size_m or not t.is_contiguous():
+            raise ValueError(f"moe_forward: {name} must be {size_m} contiguous int32")
+    want_rows = size_m if topk_weights is not None else size_m // max(topk, 1)
+    if xs.shape[0] != want_rows:
+        raise ValueError(f"moe_forward: {xs.shape[0]} input rows, the routing reads {want_rows}")
+    if topk_weights is not None and (topk_weights.dtype != torch.float32 or topk_weights.numel() != size_m):
+        raise ValueError("moe_forward: topk_weights must be one f32 per routing entry")
+    out = torch.empty((size_m, n), dtype=torch.float32, device=xs.device)
+    if size_m == 0:
+        return out
+    L = lib()
+    st = _stream()
+    tw = _ptr(topk_weights) if topk_weights is not None else None
+    need = ctypes.c_size_t(0)
+    args = (int(experts.dtype), _ptr(experts.data_), e, _ptr(xs), k, _ptr(sorted_ids), _ptr(expert_ids), tw, topk,
+            _ptr(out), n)
+    check("qmm_moe_forward", L.qmm_moe_forward(*args, None, 0, ctypes.byref(need), k, n, size_m, 0, st))
+    buf = (workspace or Workspace()).get(need.value, xs.device)
+    check("qmm_moe_forward", L.qmm_moe_forward(*args, _ptr(buf), buf.numel(), ctypes.byref(need), k, n, size_m, 1, st))
+    return out
 
 
 def quantize_act(x: torch.Tensor, layout: int) -> torch.Tensor:

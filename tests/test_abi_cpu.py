@@ -74,6 +74,28 @@ def test_forward_plans_without_a_device_and_rejects_bad_shapes():
     assert L.qmm_matvec(12, None, None, None, 8, 256, 8, L.qmm_matvec_max_rows() + 1, 0) == _lib.QMM_UNSUPPORTED
 
 
+def test_moe_plans_without_a_device_and_rejects_bad_routing_shapes():
+    L = lib()
+    need = ctypes.c_size_t(0)
+    # C4 gate_up plan: 8 tokens x top-4, per-token inputs; no device touched
+    st = L.qmm_moe_forward(39, None, 32, None, 2880, None, None, None, 4, None, 5760, None, 0, ctypes.byref(need),
+                           2880, 5760, 32, 0, 0)
+    act = (L.qmm_act_bytes(_lib.ACT_Q8_0, 2880, 8) + 255) // 256 * 256
+    assert st == _lib.QMM_OK and need.value == act + 4 * (1 + 3 * 32)
+    # per-pair inputs (routing weights given) quantize one row per entry
+    fake_w = ctypes.c_void_p(16)
+    st = L.qmm_moe_forward(39, None, 32, None, 2880, None, None, fake_w, 4, None, 2880, None, 0, ctypes.byref(need),
+                           2880, 2880, 32, 0, 0)
+    assert st == _lib.QMM_OK and need.value == (L.qmm_act_bytes(_lib.ACT_Q8_0, 2880, 32) + 255) // 256 * 256 + 4 * 97
+    # size_m not a multiple of topk without weights, K-quant types, no experts
+    assert L.qmm_moe_forward(39, None, 32, None, 2880, None, None, None, 4, None, 5760, None, 0, ctypes.byref(need),
+                             2880, 5760, 30, 0, 0) == _lib.QMM_UNSUPPORTED
+    assert L.qmm_moe_forward(12, None, 32, None, 4096, None, None, None, 4, None, 64, None, 0, ctypes.byref(need),
+                             4096, 64, 32, 0, 0) == _lib.QMM_UNSUPPORTED
+    assert L.qmm_moe_forward(39, None, 0, None, 2880, None, None, None, 4, None, 64, None, 0, ctypes.byref(need),
+                             2880, 64, 32, 0, 0) == _lib.QMM_UNSUPPORTED
+
+
 def test_fault_injection_is_host_side_and_one_shot():
     L = lib()
     need = ctypes.c_size_t(0)

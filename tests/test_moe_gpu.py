@@ -1,0 +1,173 @@
+"""Grouped expert products (qmm_moe_forward, the reference's moe_gemm_gguf /
+QMatMul::matmul_many) against the CPU oracle, through the C ABI.
+
+Routing as BASELINE C4 draws it: N(0,1) router logits [tokens, experts],
+top-k per token with ties to the lower index, routing entries sorted by
+(expert, pair), pair = token * topk + choice, routing weights the softmax of
+the chosen logits. Each product is checked against the oracle's matmul of
+that pair's input row and expert weight (normalised error <= 1e-3, the decode
+bound) and must equal qmm_forward of the same pair times its scale bit for
+bit (matmul_many == per-job forward, quantized/mod.rs:743-745).
+"""
+import ctypes
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import TOL_MATVEC, normalised_error
+from oracle import qref
+from swarmllm_amd import GgmlDType, QMatMul, QTensor, fill_normal, moe_forward
+from swarmllm_amd._lib import QMM_NO_ROOM, QMM_UNSUPPORTED, QMM_WORKSPACE_TOO_SMALL, lib
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+MOE_TYPES = {"MXFP4": 39, "Q8_0": 8, "IQ4_NL": 20}
+
+
+def routing(tokens: int, experts: int, topk: int, seed: int):
+    rng = np.random.default_rng(seed)
+    logits = rng.standard_normal((tokens, experts)).astype(np.float32)
+    choice = np.argsort(-logits, axis=1, kind="stable")[:, :topk]
+    pairs = sorted((int(choice[t, j]), t * topk + j) for t in range(tokens) for j in range(topk))
+    expert_ids = np.array([e for e, _ in pairs], np.int32)
+    sorted_ids = np.array([p for _, p in pairs], np.int32)
+    sel = np.take_along_axis(logits, choice, axis=1).astype(np.float64)
+    w = np.exp(sel - sel.max(axis=1, keepdims=True))
+    w /= w.sum(axis=1, keepdims=True)
+    return sorted_ids, expert_ids, w.reshape(-1).astype(np.float32)
+
+
+def expert_stack(qtype: int, e: int, n: int, k: int, seed: int) -> QTensor:
+    """E experts [n, k] quantized on the device (bit-exact to from_float), stacked."""
+    parts = [QTensor.quantize(fill_normal(n * k, seed=(seed << 8) | i, std=0.02).reshape(n, k), GgmlDType(qtype))
+             for i in range(e)]
+    return QTensor(torch.cat([p.data_ for p in parts]), (e, n, k), GgmlDType(qtype))
+
+
+def t32(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def check_against_oracle(qtype, stack, x, out, sorted_ids, expert_ids, topk_w, topk):
+    e, n, k = stack.shape
+    wb = stack.data_.cpu().numpy()
+    per = wb.size // e
+    for i in range(len(sorted_ids)):
+        p, ex = int(sorted_ids[i]), int(expert_ids[i])
+        row = p if topk_w is not None else p // topk
+        scale = np.float32(topk_w[p]) if topk_w is not None else np.float32(1.0)
+        w_e = wb[ex * per:(ex + 1) * per]
+        want = qref.matmul(qtype, x[row][None, :], w_e, n)[0] * scale
+        wdeq = qref.to_float(qtype, w_e, n * k).reshape(n, k)
+        err = normalised_error(out[p][None, :], want[None, :], wdeq, (x[row] * scale)[None, :])
+        assert err <= TOL_MATVEC, f"pair {p} expert {ex}: {err}"
+
+
+def check_against_forward(stack, xs_dev, out, sorted_ids, expert_ids, topk_w, topk):
+    e, n, k = stack.shape
+    per = stack.data_.numel() // e
+    for i in range(len(sorted_ids)):
+        p, ex = int(sorted_ids[i]), int(expert_ids[i])
+        row = p if topk_w is not None else p // topk
+        qt = QTensor(stack.data_[ex * per:(ex + 1) * per], (n, k), stack.dtype)
+        y = QMatMul(qt).forward(xs_dev[row:row + 1]).cpu().numpy()[0]
+        scale = np.float32(topk_w[p]) if topk_w is not None else np.float32(1.0)
+        assert np.array_equal((y * scale).view(np.uint32), out[p].view(np.uint32)), f"pair {p}"
+
+
+@pytest.mark.parametrize("name", list(MOE_TYPES))
+@pytest.mark.parametrize("weighted", [False, True])
+def test_moe_parity_small(name, weighted):
+    qtype = MOE_TYPES[name]
+    E, n, k, tokens, topk = 8, 96, 320, 6, 3
+    seed = zlib.crc32(f"{name}-{weighted}".encode())
+    sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, seed)
+    stack = expert_stack(qtype, E, n, k, seed & 0xFFFF)
+    rows = tokens * topk if weighted else tokens
+    x = np.random.default_rng(seed).standard_normal((rows, k)).astype(np.float32)
+    xs = t32(x)
+    tw = topk_w if weighted else None
+    out = moe_forward(xs, stack, t32(sorted_ids), t32(expert_ids), t32(topk_w) if weighted else None, topk)
+    out = out.cpu().numpy()
+    check_against_oracle(qtype, stack, x, out, sorted_ids, expert_ids, tw, topk)
+    check_against_forward(stack, xs, out, sorted_ids, expert_ids, tw, topk)
+
+
+def test_moe_c4_gpt_oss_shapes():
+    """BASELINE C4: 32 MXFP4 experts, gate_up [5760, 2880] then down
+    [2880, 2880], 8 tokens with top-4 routing."""
+    qtype, E, tokens, topk = 39, 32, 8, 4
+    sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, 4)
+    before = lib().qmm_moe_launches()
+    gate_up = expert_stack(qtype, E, 5760, 2880, 41)
+    x = np.random.default_rng(40).standard_normal((tokens, 2880)).astype(np.float32)
+    y1 = moe_forward(t32(x), gate_up, t32(sorted_ids), t32(expert_ids), None, topk).cpu().numpy()
+    check_against_oracle(qtype, gate_up, x, y1, sorted_ids, expert_ids, None, topk)
+    del gate_up
+    down = expert_stack(qtype, E, 2880, 2880, 42)
+    x2 = np.random.default_rng(43).standard_normal((tokens * topk, 2880)).astype(np.float32)
+    xs2 = t32(x2)
+    y2 = moe_forward(xs2, down, t32(sorted_ids), t32(expert_ids), t32(topk_w), topk).cpu().numpy()
+    check_against_oracle(qtype, down, x2, y2, sorted_ids, expert_ids, topk_w, topk)
+    check_against_forward(down, xs2, y2, sorted_ids, expert_ids, topk_w, topk)
+    assert lib().qmm_moe_launches() >= before + 2
+
+
+def test_moe_order_of_entries_does_not_change_results():
+    qtype, E, n, k, tokens, topk = 39, 6, 64, 256, 5, 2
+    sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, 7)
+    stack = expert_stack(qtype, E, n, k, 77)
+    x = np.random.default_rng(7).standard_normal((tokens, k)).astype(np.float32)
+    ref = moe_forward(t32(x), stack, t32(sorted_ids), t32(expert_ids), None, topk).cpu().numpy()
+    perm = np.random.default_rng(8).permutation(len(sorted_ids))
+    got = moe_forward(t32(x), stack, t32(sorted_ids[perm]), t32(expert_ids[perm]), None, topk).cpu().numpy()
+    assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
+
+
+def test_moe_out_of_range_entries_write_nothing():
+    qtype, E, n, k, topk = 39, 4, 32, 64, 1
+    stack = expert_stack(qtype, E, n, k, 9)
+    x = np.random.default_rng(9).standard_normal((6, k)).astype(np.float32)
+    sorted_ids = np.array([0, 1, 2, 3, 4, 5], np.int32)
+    expert_ids = np.array([-1, 0, 0, 2, 4, 7], np.int32)  # -1, 4 and 7 are not experts
+    L = lib()
+    out = torch.full((6, n), 123.5, dtype=torch.float32, device=DEV)
+    xs, sid, eid = t32(x), t32(sorted_ids), t32(expert_ids)
+    need = ctypes.c_size_t(0)
+    args = (qtype, stack.data_.data_ptr(), E, xs.data_ptr(), k, sid.data_ptr(), eid.data_ptr(), None, topk,
+            out.data_ptr(), n)
+    assert L.qmm_moe_forward(*args, None, 0, ctypes.byref(need), k, n, 6, 0, 0) == 0
+    ws = torch.empty(need.value, dtype=torch.uint8, device=DEV)
+    assert L.qmm_moe_forward(*args, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 6, 1, 0) == 0
+    got = out.cpu().numpy()
+    for p in (0, 4, 5):
+        assert np.all(got[p] == 123.5), f"row {p} was written"
+    check_against_forward(stack, xs, got, sorted_ids[1:4], expert_ids[1:4], None, topk)
+
+
+def test_moe_status_paths():
+    qtype, E, n, k, topk = 39, 2, 32, 64, 2
+    stack = expert_stack(qtype, E, n, k, 11)
+    x = torch.zeros((2, k), dtype=torch.float32, device=DEV)
+    sid = t32(np.array([0, 1, 2, 3], np.int32))
+    eid = t32(np.array([0, 0, 1, 1], np.int32))
+    out = torch.empty((4, n), dtype=torch.float32, device=DEV)
+    L = lib()
+    need = ctypes.c_size_t(0)
+    args = (qtype, stack.data_.data_ptr(), E, x.data_ptr(), k, sid.data_ptr(), eid.data_ptr(), None, topk,
+            out.data_ptr(), n)
+    assert L.qmm_moe_forward(*args, None, 0, ctypes.byref(need), k, n, 4, 0, 0) == 0 and need.value > 0
+    ws = torch.empty(need.value, dtype=torch.uint8, device=DEV)
+    assert L.qmm_moe_forward(*args, ws.data_ptr(), need.value - 1, ctypes.byref(need), k, n, 4, 1, 0) == \
+        QMM_WORKSPACE_TOO_SMALL
+    L.qmm_fail_next_launch()
+    assert L.qmm_moe_forward(*args, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 4, 1, 0) == QMM_NO_ROOM
+    assert L.qmm_moe_forward(*args, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 4, 1, 0) == 0
+    # per-token inputs need size_m to be a multiple of topk; Q4_K is not a grouped type here
+    assert L.qmm_moe_forward(*args, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 3, 1, 0) == QMM_UNSUPPORTED
+    args_q4k = (12,) + args[1:]
+    assert L.qmm_moe_forward(*args_q4k, ws.data_ptr(), ws.numel(), ctypes.byref(need), 256, n, 4, 1, 0) == \
+        QMM_UNSUPPORTED
