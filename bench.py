@@ -63,16 +63,18 @@ def layer_bytes() -> dict:
 
 
 class Layer:
-    """Device buffers of one C2 layer copy plus the shared activations."""
+    """Device buffers of one layer's weights (a LAYER-like spec), quantized on
+    the device from N(0, 0.02) with seeds (config, copy, product)."""
 
-    def __init__(self, copy: int, acts: dict):
+    def __init__(self, copy: int, acts: dict, spec=None, config_seed: int = CONFIG_SEED):
         import torch
 
         from swarmllm_amd import GgmlDType, QTensor, fill_normal
 
+        self.spec = spec or LAYER
         self.w = {}
-        for p, (name, t, n, k) in enumerate(LAYER):
-            seed = (CONFIG_SEED << 40) | (copy << 8) | p
+        for p, (name, t, n, k) in enumerate(self.spec):
+            seed = (config_seed << 40) | (copy << 8) | p
             wf = fill_normal(n * k, seed=seed, std=0.02).reshape(n, k)
             self.w[name] = QTensor.quantize(wf, GgmlDType(t))
             del wf
@@ -80,31 +82,46 @@ class Layer:
         self.acts = acts
 
 
-def make_acts():
+def make_acts(spec=None, groups=None, rows: int = 1, config_seed: int = CONFIG_SEED):
+    """Per group of products sharing an activation: the f32 rows (N(0,1)) and
+    a workspace sized by the plan call; the outputs of every product."""
     import torch
 
     from swarmllm_amd import fill_normal
-    from swarmllm_amd._lib import lib
+    from swarmllm_amd._lib import check, lib
 
+    spec, groups = spec or LAYER, groups or GROUPS
+    shape = {name: (t, n, k) for name, t, n, k in spec}
     L = lib()
     acts = {}
-    for i, (g, k, _) in enumerate(GROUPS):
-        x = fill_normal(k, seed=(CONFIG_SEED << 40) | (0xA0 + i)).reshape(1, k)
-        ws = torch.empty(L.qmm_act_bytes(ACT_Q8K, k, 1), dtype=torch.uint8, device="cuda")
+    need = ctypes.c_size_t(0)
+    for i, (g, k, names) in enumerate(groups):
+        x = fill_normal(rows * k, seed=(config_seed << 40) | (0xA0 + i)).reshape(rows, k)
+        t = shape[names[0]][0]
+        if len(names) == 1:
+            check("qmm_forward", L.qmm_forward(t, None, None, k, None, shape[names[0]][1], None, 0,
+                                               ctypes.byref(need), k, shape[names[0]][1], rows, 0, 0))
+        else:
+            cnt = len(names)
+            ns = (ctypes.c_int64 * cnt)(*[shape[nm][1] for nm in names])
+            nulls = (ctypes.c_void_p * cnt)()
+            check("qmm_forward_shared", L.qmm_forward_shared(t, cnt, nulls, ns, nulls, ns, None, k, None, 0,
+                                                             ctypes.byref(need), k, rows, 0, 0))
+        ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device="cuda")
         acts[g] = (x, ws)
-    outs = {name: torch.empty((1, n), dtype=torch.float32, device="cuda") for name, _, n, _ in LAYER}
+    outs = {name: torch.empty((rows, n), dtype=torch.float32, device="cuda") for name, _, n, _ in spec}
     return acts, outs
 
 
-def enqueue_step(layer: Layer, outs: dict, stream: int) -> None:
+def enqueue_step(layer: Layer, outs: dict, stream: int, groups=None, rows: int = 1) -> None:
     """The layer's products: per group of weights sharing an activation one
     qmm_forward_shared (QMatMul::forward_shared), or qmm_forward for one."""
     from swarmllm_amd._lib import check, lib
 
     L = lib()
-    shape = {name: (t, n, k) for name, t, n, k in LAYER}
+    shape = {name: (t, n, k) for name, t, n, k in layer.spec}
     need = ctypes.c_size_t(0)
-    for g, k, names in GROUPS:
+    for g, k, names in groups or GROUPS:
         x, ws = layer.acts[g]
         t = shape[names[0]][0]
         if len(names) == 1:
@@ -112,14 +129,14 @@ def enqueue_step(layer: Layer, outs: dict, stream: int) -> None:
             _, n, _ = shape[name]
             check("qmm_forward", L.qmm_forward(t, layer.w[name].data_.data_ptr(), x.data_ptr(), k,
                                                outs[name].data_ptr(), n, ws.data_ptr(), ws.numel(),
-                                               ctypes.byref(need), k, n, 1, 1, stream))
+                                               ctypes.byref(need), k, n, rows, 1, stream))
             continue
         cnt = len(names)
         wp = (ctypes.c_void_p * cnt)(*[layer.w[nm].data_.data_ptr() for nm in names])
         ns = (ctypes.c_int64 * cnt)(*[shape[nm][1] for nm in names])
         dp = (ctypes.c_void_p * cnt)(*[outs[nm].data_ptr() for nm in names])
         check("qmm_forward_shared", L.qmm_forward_shared(t, cnt, wp, ns, dp, ns, x.data_ptr(), k, ws.data_ptr(),
-                                                         ws.numel(), ctypes.byref(need), k, 1, 1, stream))
+                                                         ws.numel(), ctypes.byref(need), k, rows, 1, stream))
 
 
 def capture(fn, stream):
@@ -301,6 +318,168 @@ def cpu_baseline(layers, budget_s: float) -> dict:
             "cpu": cpu_name(), "logical_cpus": os.cpu_count()}
 
 
+# BASELINE C5: one peer's shard of a Llama-3.3-70B-shaped model, 40 layers
+C5_LAYER = [("q", Q4K, 8192, 8192), ("k", Q4K, 1024, 8192), ("v", Q4K, 1024, 8192), ("o", Q4K, 8192, 8192),
+            ("gate", Q4K, 28672, 8192), ("up", Q4K, 28672, 8192), ("down", Q6K, 8192, 28672)]
+C5_GROUPS = [("attn_in", 8192, ["q", "k", "v"]), ("attn_out", 8192, ["o"]), ("ffn_in", 8192, ["gate", "up"]),
+             ("ffn_mid", 28672, ["down"])]
+C5_LAYERS = 40
+
+
+def c5_shard(stream, rows_list=(1, 8, 16), reps: int = 5) -> dict:
+    """BASELINE C5: the 40 layers resident (21.67 GB of Q4_K / Q6_K weights,
+    each layer its own N(0,0.02) draw), one forward = every layer's 7
+    products (4 launches a layer: q+k+v and gate+up share their activation)
+    captured as one HIP graph, at each speculative-verification width M.
+    GB/s = the shard's weight bytes per forward time (the weights are read
+    once per forward at any M <= 16 on the kernels that take M in one pass)."""
+    import torch
+
+    t0 = time.perf_counter()
+    layers = [Layer(c, None, spec=C5_LAYER, config_seed=5) for c in range(C5_LAYERS)]
+    wbytes = C5_LAYERS * sum(type_bytes(t, n, k) for _, t, n, k in C5_LAYER)
+    log(f"C5: {C5_LAYERS} layers ({wbytes / 1e9:.2f} GB) quantized in {time.perf_counter() - t0:.1f} s")
+    out = {"workload": "C5: Llama-3.3-70B shard, 40 layers, Q4_K (q/k/v/o/gate/up) + Q6_K (down), "
+                       "7 products a layer in 4 launches, one graph per forward",
+           "weight_bytes": wbytes, "by_rows": {}}
+    for rows in rows_list:
+        acts, outs = make_acts(C5_LAYER, C5_GROUPS, rows, config_seed=5)
+        for lay in layers:
+            lay.acts = acts
+
+        def fn(s, outs=outs, rows=rows):
+            for lay in layers:
+                enqueue_step(lay, outs, s, C5_GROUPS, rows)
+
+        g = capture(fn, stream)
+        for _ in range(2):
+            g.replay()
+        ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream) / reps
+        gbs = wbytes / (ms * 1e-3) / 1e9
+        out["by_rows"][str(rows)] = {"ms_per_forward": round(ms, 4), "weight_gbs": round(gbs, 1),
+                                     "percent_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+        log(f"C5 M={rows}: {ms:.3f} ms per forward, {gbs:.0f} GB/s")
+        del g
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
+MXFP4 = 39
+
+
+def c4_moe(stream, reps: int = 20, copies: int = 2) -> dict:
+    """BASELINE C4: gpt-oss-20b-shaped experts, 32 MXFP4 experts with gate_up
+    [5760, 2880] and down [2880, 2880]; 8 tokens routed top-4 from seeded
+    N(0,1) logits (ties to the lower index), entries sorted by (expert,
+    pair). One step = the gate_up grouped product (per-token inputs) and the
+    down grouped product (per-pair inputs, routing weights), back to back
+    over `copies` weight stacks. Algorithmic bytes = the touched experts'
+    weights + f32 inputs and outputs."""
+    import numpy as np
+    import torch
+
+    from swarmllm_amd import GgmlDType, QTensor, fill_normal
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    E, tokens, topk, hidden, inter = 32, 8, 4, 2880, 2880
+    rng = np.random.default_rng(4)
+    logits = rng.standard_normal((tokens, E)).astype(np.float32)
+    choice = np.argsort(-logits, axis=1, kind="stable")[:, :topk]
+    pairs = sorted((int(choice[t, j]), t * topk + j) for t in range(tokens) for j in range(topk))
+    eids = torch.tensor([e for e, _ in pairs], dtype=torch.int32, device="cuda")
+    sids = torch.tensor([p for _, p in pairs], dtype=torch.int32, device="cuda")
+    sel = np.take_along_axis(logits, choice, axis=1).astype(np.float64)
+    wts = np.exp(sel - sel.max(axis=1, keepdims=True))
+    wts /= wts.sum(axis=1, keepdims=True)
+    topk_w = torch.tensor(wts.reshape(-1), dtype=torch.float32, device="cuda")
+    touched = len(set(e for e, _ in pairs))
+
+    def stack(n, k, seed):
+        parts = [QTensor.quantize(fill_normal(n * k, seed=(seed << 8) | i, std=0.02).reshape(n, k), GgmlDType(MXFP4))
+                 for i in range(E)]
+        return torch.cat([p.data_ for p in parts])
+
+    gu = [stack(2 * inter, hidden, 40 + 2 * c) for c in range(copies)]
+    dn = [stack(hidden, inter, 41 + 2 * c) for c in range(copies)]
+    x1 = fill_normal(tokens * hidden, seed=(4 << 40) | 1).reshape(tokens, hidden)
+    x2 = fill_normal(tokens * topk * inter, seed=(4 << 40) | 2).reshape(tokens * topk, inter)
+    y1 = torch.empty((tokens * topk, 2 * inter), dtype=torch.float32, device="cuda")
+    y2 = torch.empty((tokens * topk, hidden), dtype=torch.float32, device="cuda")
+    need = ctypes.c_size_t(0)
+    size_m = tokens * topk
+    check("qmm_moe_forward", L.qmm_moe_forward(MXFP4, None, E, None, hidden, None, None, None, topk, None, 2 * inter,
+                                               None, 0, ctypes.byref(need), hidden, 2 * inter, size_m, 0, 0))
+    ws1 = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+    check("qmm_moe_forward", L.qmm_moe_forward(MXFP4, None, E, None, inter, None, None, ctypes.c_void_p(16), topk,
+                                               None, hidden, None, 0, ctypes.byref(need), inter, hidden, size_m, 0, 0))
+    ws2 = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+    before = L.qmm_moe_launches()
+
+    def fn(s):
+        for c in range(copies):
+            check("qmm_moe_forward", L.qmm_moe_forward(
+                MXFP4, gu[c].data_ptr(), E, x1.data_ptr(), hidden, sids.data_ptr(), eids.data_ptr(), None, topk,
+                y1.data_ptr(), 2 * inter, ws1.data_ptr(), ws1.numel(), ctypes.byref(need), hidden, 2 * inter, size_m,
+                1, s))
+            check("qmm_moe_forward", L.qmm_moe_forward(
+                MXFP4, dn[c].data_ptr(), E, x2.data_ptr(), inter, sids.data_ptr(), eids.data_ptr(),
+                topk_w.data_ptr(), topk, y2.data_ptr(), hidden, ws2.data_ptr(), ws2.numel(), ctypes.byref(need),
+                inter, hidden, size_m, 1, s))
+
+    g = capture(fn, stream)
+    if L.qmm_moe_launches() < before + 2 * copies:
+        raise RuntimeError("the C4 step did not run the grouped expert kernels")
+    for _ in range(2):
+        g.replay()
+    ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+    us = ms * 1e3 / (reps * copies)
+    per_expert = 2 * inter * (hidden // 32) * 17 + hidden * (inter // 32) * 17
+    alg = touched * per_expert + 4 * (tokens * hidden + size_m * inter + size_m * 2 * inter + size_m * hidden)
+    gbs = alg / (us * 1e-6) / 1e9
+    log(f"C4: {us:.2f} us per MoE step ({touched} experts touched), {gbs:.0f} GB/s")
+    return {"workload": "C4: gpt-oss-20b MoE, 32 MXFP4 experts, 8 tokens top-4, gate_up + down grouped products",
+            "experts_touched": touched, "us_per_step": round(us, 3), "alg_bytes": alg, "gbs": round(gbs, 1),
+            "percent_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+
+
+def c1_q8_0(stream, reps: int = 50, copies: int = 16) -> dict:
+    """BASELINE C1 (the reference's CPU-runnable case) on the device: Q8_0
+    4096 x 4096 (N(0,0.02), seed 0) against one N(0,1) row, rotated over
+    `copies` weights."""
+    import torch
+
+    from swarmllm_amd import GgmlDType, QTensor, fill_normal
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    n = k = 4096
+    ws = [QTensor.quantize(fill_normal(n * k, seed=c, std=0.02).reshape(n, k), GgmlDType(8)) for c in range(copies)]
+    x = fill_normal(k, seed=1 << 32).reshape(1, k)
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    need = ctypes.c_size_t(0)
+    check("qmm_forward", L.qmm_forward(8, None, None, k, None, n, None, 0, ctypes.byref(need), k, n, 1, 0, 0))
+    buf = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+
+    def fn(s):
+        for w in ws:
+            check("qmm_forward", L.qmm_forward(8, w.data_.data_ptr(), x.data_ptr(), k, y.data_ptr(), n,
+                                               buf.data_ptr(), buf.numel(), ctypes.byref(need), k, n, 1, 1, s))
+
+    g = capture(fn, stream)
+    for _ in range(2):
+        g.replay()
+    ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+    us = ms * 1e3 / (reps * copies)
+    alg = n * (k // 32) * 34 + 4 * k + 4 * n
+    gbs = alg / (us * 1e-6) / 1e9
+    log(f"C1: {us:.2f} us per Q8_0 product (quantize + matvec), {gbs:.0f} GB/s")
+    return {"workload": "C1: Q8_0 4096x4096 at M=1 (activation quantize + matvec launches)",
+            "us_per_product": round(us, 3), "alg_bytes": alg, "gbs": round(gbs, 1),
+            "percent_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+
+
 COPY_BYTES = 512 << 20  # the calibration copy: 512 MiB read + 512 MiB written
 
 
@@ -385,6 +564,7 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extra", action="store_true", help="skip the C1 / C4 / C5 sections")
     ap.add_argument("--profile", choices=["dominant", "prefill", "copy"],
                     help="launch only this kernel --steps times (for rocprofv3 counter passes), print no JSON")
     args = ap.parse_args()
@@ -441,6 +621,12 @@ def main() -> int:
     pre = prefill_gemm(layers, stream, max(2, args.kernel_reps // 5))
     log(f"prefill GEMM: {pre['us_per_launch']:.2f} us/launch, {pre['tops']:.1f} TOP/s")
 
+    extra = {}
+    if not args.no_extra:
+        extra["c1"] = c1_q8_0(stream)
+        extra["c4"] = c4_moe(stream)
+        extra["c5"] = c5_shard(stream)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(layers, args.cpu_seconds)
@@ -468,6 +654,7 @@ def main() -> int:
                      "alg_bytes_per_launch": dk["alg_bytes"]},
         "cpu_baseline": cpu,
         "prefill": pre,
+        **extra,
     }
     print(json.dumps(line), flush=True)
     return 0
