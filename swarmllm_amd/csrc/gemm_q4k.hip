@@ -315,7 +315,7 @@ constexpr int kWavesWide = 8, kWavesNarrow = 4;
 
 }  // namespace
 
-int gemm_q4k_min_rows() { return 9; }
+int gemm_q4k_min_rows() { return 33; }  // fewer rows: gemm_q4k_skinny.hip
 
 bool gemm_q4k_fits(int64_t n, int64_t k, int64_t rows) {
   // 32-bit byte offsets inside the kernel

@@ -77,12 +77,30 @@ int cu_count() {
   return cached[dev];
 }
 
-// The int8 matrix-core GEMM: Q4_K from gemm_q4k_min_rows() rows, weight and
-// quantized activation 16-byte aligned (its 16-byte copies), sizes inside its
-// 32-bit offsets.
+// The reference's few-rows line (mmq_takes_few_rows, mmq_fewest_rows_default,
+// quantized/cuda.rs:775-839): K-quant products of 4 to 8 rows against a
+// weight of 2 MiB or more go to the matrix cores, as do all of more than 8.
+constexpr int64_t kFewRowsLeastBytes = (int64_t)2 << 20;
+constexpr int kFewRowsKQuant = 4;
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// The skinny matrix-core kernel: Q4_K up to gemm_q4k_skinny_max_rows() rows
+// past the few-rows line.
+bool skinny_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows) {
+  if (type != qmm::T_Q4_K || rows > qmm::gemm_q4k_skinny_max_rows() || !aligned16(w) || !aligned16(xq) ||
+      !qmm::gemm_q4k_skinny_fits(k, rows))
+    return false;
+  if (rows > qmm::matvec_max_rows()) return true;
+  return rows >= kFewRowsKQuant && n * (k / 256) * 144 >= kFewRowsLeastBytes;
+}
+
+// The tiled int8 matrix-core GEMM: Q4_K past the skinny kernel's rows,
+// weight and quantized activation 16-byte aligned (its 16-byte copies),
+// sizes inside its 32-bit offsets.
 bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows) {
-  return type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && ((uintptr_t)w & 15) == 0 &&
-         ((uintptr_t)xq & 15) == 0 && qmm::gemm_q4k_fits(n, k, rows);
+  return type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && aligned16(w) && aligned16(xq) &&
+         qmm::gemm_q4k_fits(n, k, rows);
 }
 
 // The streaming decode kernels (Q4_K, Q6_K at 1-2 activation rows).
@@ -217,15 +235,24 @@ int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd,
   return status_of(e);
 }
 
-int qmm_matmul(int type, const void* w, const void* xq, float* dst, int64_t ldd, int64_t k, int64_t n, int64_t rows,
-               int64_t stream) {
-  if (!shape_ok(type, k, n, rows) || ldd < n || !w || !xq || !dst) return QMM_UNSUPPORTED;
-  const int layout = qmm_act_layout(type, rows);
-  const qmm::ActPlanes p = qmm::act_planes(layout, (void*)xq, k, rows);
-  const hipStream_t st = (hipStream_t)stream;
-  clear_stale_error();
+// One product from an activation already quantized into planes p (buffer
+// xq): the matrix-core kernels past the few-rows line, else the decode
+// kernels a chunk of at most matvec_max_rows() rows at a time.
+int launch_product(int type, const void* w, int64_t n, int64_t k, const void* xq, const qmm::ActPlanes& p,
+                   int layout, int64_t rows, float* dst, int64_t ldd, hipStream_t st) {
   if (gemm_takes(type, w, xq, n, k, rows)) {
     if (qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
+    g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+    return QMM_OK;
+  }
+  if (skinny_takes(type, w, xq, n, k, rows)) {
+    qmm::MvTargets t{};
+    t.w[0] = w;
+    t.dst[0] = dst;
+    t.ldd[0] = ldd;
+    t.row_end[0] = n;
+    t.count = 1;
+    if (qmm::launch_gemm_q4k_skinny(t, k, p, rows, cu_count(), st) != hipSuccess) return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
   }
@@ -241,6 +268,15 @@ int qmm_matmul(int type, const void* w, const void* xq, float* dst, int64_t ldd,
     g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
   }
   return QMM_OK;
+}
+
+int qmm_matmul(int type, const void* w, const void* xq, float* dst, int64_t ldd, int64_t k, int64_t n, int64_t rows,
+               int64_t stream) {
+  if (!shape_ok(type, k, n, rows) || ldd < n || !w || !xq || !dst) return QMM_UNSUPPORTED;
+  const int layout = qmm_act_layout(type, rows);
+  const qmm::ActPlanes p = qmm::act_planes(layout, (void*)xq, k, rows);
+  clear_stale_error();
+  return launch_product(type, w, n, k, xq, p, layout, rows, dst, ldd, (hipStream_t)stream);
 }
 
 int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float* dst, int64_t ldd, void* workspace,
@@ -262,29 +298,10 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
     g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
   }
-  hipError_t e = qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st);
-  if (e != hipSuccess) return QMM_DEVICE_ERROR;
+  if (qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st) != hipSuccess)
+    return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
-  if (gemm_takes(type, w, workspace, n, k, rows)) {
-    // prefill: the int8 matrix-core GEMM
-    if (qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
-    g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
-    return QMM_OK;
-  }
-  const int64_t step = qmm::matvec_max_rows();
-  for (int64_t r0 = 0; r0 < rows; r0 += step) {
-    const int64_t nr = rows - r0 < step ? rows - r0 : step;
-    const qmm::ActPlanes pr = qmm::act_rows(layout, p, k, r0);
-    if (stream_supported(type, k, nr)) {
-      float* d = dst + r0 * ldd;
-      e = launch_stream_targets(type, 1, &w, &n, &d, &ldd, k, nr, nullptr, 0, &pr, st);
-    } else {
-      e = qmm::launch_matvec(type, w, n, k, pr, nr, dst + r0 * ldd, ldd, st);
-    }
-    if (e != hipSuccess) return QMM_DEVICE_ERROR;
-    g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
-  }
-  return QMM_OK;
+  return launch_product(type, w, n, k, workspace, p, layout, rows, dst, ldd, st);
 }
 
 int qmm_forward_shared(int type, int count, const void* const* w, const int64_t* n, float* const* dst,
@@ -319,28 +336,31 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
   if (qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st) != hipSuccess)
     return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
-  const int64_t step = qmm::matvec_max_rows();
+  // the weights the skinny kernel takes share its launches (kMaxTargets each)
+  qmm::MvTargets grp{};
+  int64_t end = 0;
+  auto flush = [&]() -> int {
+    if (grp.count == 0) return QMM_OK;
+    if (qmm::launch_gemm_q4k_skinny(grp, k, p, rows, cu_count(), st) != hipSuccess) return QMM_DEVICE_ERROR;
+    g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+    grp = qmm::MvTargets{};
+    end = 0;
+    return QMM_OK;
+  };
   for (int i = 0; i < count; i++) {
-    if (gemm_takes(type, w[i], workspace, n[i], k, rows)) {
-      if (qmm::launch_gemm_q4k(w[i], n[i], k, p, rows, dst[i], ldd[i], st) != hipSuccess) return QMM_DEVICE_ERROR;
-      g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+    if (!gemm_takes(type, w[i], workspace, n[i], k, rows) && skinny_takes(type, w[i], workspace, n[i], k, rows)) {
+      grp.w[grp.count] = w[i];
+      grp.dst[grp.count] = dst[i];
+      grp.ldd[grp.count] = ldd[i];
+      end += n[i];
+      grp.row_end[grp.count] = end;
+      if (++grp.count == qmm::kMaxTargets && flush() != QMM_OK) return QMM_DEVICE_ERROR;
       continue;
     }
-    for (int64_t r0 = 0; r0 < rows; r0 += step) {
-      const int64_t nr = rows - r0 < step ? rows - r0 : step;
-      const qmm::ActPlanes pr = qmm::act_rows(layout, p, k, r0);
-      hipError_t e;
-      if (stream_supported(type, k, nr)) {
-        float* d = dst[i] + r0 * ldd[i];
-        e = launch_stream_targets(type, 1, w + i, n + i, &d, ldd + i, k, nr, nullptr, 0, &pr, st);
-      } else {
-        e = qmm::launch_matvec(type, w[i], n[i], k, pr, nr, dst[i] + r0 * ldd[i], ldd[i], st);
-      }
-      if (e != hipSuccess) return QMM_DEVICE_ERROR;
-      g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
-    }
+    const int r = launch_product(type, w[i], n[i], k, workspace, p, layout, rows, dst[i], ldd[i], st);
+    if (r != QMM_OK) return r;
   }
-  return QMM_OK;
+  return flush();
 }
 
 int qmm_dequantize(int type, const void* w, void* out, int out_f16, int64_t nelem, int64_t stream) {

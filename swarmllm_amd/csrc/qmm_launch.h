@@ -99,6 +99,13 @@ hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64
                       int32_t* runs, const int32_t* ids, const int32_t* expert_ids, const float* topk_w, int topk,
                       int64_t size_m, float* dst, int64_t ldd, hipStream_t st);
 
+// Q4_K products of a few rows (gemm_q4k_skinny.hip): up to
+// gemm_q4k_skinny_max_rows() activation rows, targets as the stream kernels.
+int gemm_q4k_skinny_max_rows();
+bool gemm_q4k_skinny_fits(int64_t k, int64_t rows);
+hipError_t launch_gemm_q4k_skinny(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, int cus,
+                                  hipStream_t st);
+
 int gemm_q4k_min_rows();
 // The GEMM indexes with 32-bit byte offsets: the weight below 2 GiB and
 // (rows + 128) * k below 2^31.

@@ -134,3 +134,67 @@ def test_matmul_from_a_quantized_activation_equals_forward(rows):
                           torch.cuda.current_stream().cuda_stream)
     assert st == 0
     assert torch.equal(out, QMatMul(qt).forward(x))
+
+
+# ---------------------------------------------------------------------------
+# the skinny matrix-core kernel: 4-8 rows on weights of 2 MiB or more (the
+# reference's few-rows line, quantized/cuda.rs:775-839) and 9-32 rows
+# ---------------------------------------------------------------------------
+SKINNY_SHAPES = [  # (k, n, rows): past the 2 MiB line at 4-8 rows; ragged n; one and two 16-row tiles
+    (4096, 2048, 4), (4096, 2050, 5), (8192, 1030, 8), (2048, 4100, 7), (256, 100, 9), (4096, 300, 16),
+    (14336, 64, 17), (1024, 500, 24), (8192, 129, 32),
+]
+
+
+@pytest.mark.parametrize("k,n,rows", SKINNY_SHAPES)
+def test_q4k_skinny_parity(k, n, rows):
+    rng = np.random.default_rng(zlib.crc32(f"skinny-{k}-{n}-{rows}".encode()))
+    w = weights(rng, n, k)
+    x = activations(rng, rows, k, outliers=True)
+    qt, wq = q4k(w)
+    L = lib()
+    before = L.qmm_gemm_launches()
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert L.qmm_gemm_launches() == before + 1, "the matrix-core kernel did not run"
+    want = qref.matmul(qref.Q4_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q4_K, wq, n * k).reshape(n, k)
+    err = normalised_error(y, want, wdeq, x)
+    assert err <= TIGHT, f"k={k} n={n} rows={rows}: {err}"
+
+
+def test_q4k_small_weight_few_rows_stay_on_the_decode_kernels():
+    """Below 2 MiB, 4-8 rows keep the decode kernels (batch-invariant)."""
+    rng = np.random.default_rng(5)
+    qt, _ = q4k(weights(rng, 256, 4096))  # 576 KiB
+    L = lib()
+    before = L.qmm_gemm_launches()
+    QMatMul(qt).forward(upload(activations(rng, 8, 4096)))
+    assert L.qmm_gemm_launches() == before
+
+
+@pytest.mark.parametrize("rows", [8, 16])
+def test_q4k_skinny_c5_gate_projection(rows):
+    """BASELINE C5's gate projection (28672 x 8192 Q4_K) at the
+    speculative-verification widths."""
+    rng = np.random.default_rng(50 + rows)
+    w = weights(rng, 28672, 8192)
+    x = activations(rng, rows, 8192)
+    qt, wq = q4k(w)
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    want = qref.matmul(qref.Q4_K, x, wq, 28672)
+    wdeq = qref.to_float(qref.Q4_K, wq, 28672 * 8192).reshape(28672, 8192)
+    assert normalised_error(y, want, wdeq, x) <= TIGHT
+
+
+@pytest.mark.parametrize("rows", [6, 16, 30])
+def test_q4k_skinny_shared_activation_equals_forward(rows):
+    """q/k/v-like weights through one qmm_forward_shared (grouped skinny
+    launches, more weights than one launch takes) equal each weight's own
+    forward bit for bit."""
+    rng = np.random.default_rng(70 + rows)
+    k = 4096
+    mats = [QMatMul(q4k(weights(rng, n, k))[0]) for n in (2048, 512, 512, 1040, 2048)]
+    x = upload(activations(rng, rows, k))
+    shared = QMatMul.forward_shared(x, mats)
+    for m, y in zip(mats, shared):
+        assert torch.equal(y, m.forward(x))
