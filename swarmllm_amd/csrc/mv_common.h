@@ -126,6 +126,73 @@ struct ActBatch {
   }
 };
 
+// The same fill with a Q8_K block per wave pass (lane L: values 4L..4L+3,
+// q8k_block_wave): every wave of the workgroup has a block while the blocks
+// are at least as many as the waves, and each lane's dependent chain is four
+// values long. Pass p of wave w covers block p * kWaves + w.
+template <int NR, bool FUSED, int kWaves, int kPre>
+struct ActBatchW {
+  uint4 v[kPre];  // FUSED: 4 f32 values; else .x = 4 codes, .y = d bits, .z = the quad's sum
+
+  __device__ __forceinline__ static void load_pass(uint4& v, int b, int nsb, const float* __restrict__ x,
+                                                   int64_t xstride, const int8_t* __restrict__ yq,
+                                                   const float* __restrict__ yd, const int16_t* __restrict__ ybs) {
+    const int lane = threadIdx.x & 63;
+    v = make_uint4(0, 0, 0, 0);
+    if (b >= NR * nsb) return;
+    const int r = b / nsb, sb = b - r * nsb;
+    if (FUSED) {
+      v = *(const uint4*)(x + r * xstride + sb * 256 + 4 * lane);  // rows 16-byte aligned
+    } else {
+      const int k = nsb * 256;
+      v.x = *(const uint32_t*)(yq + (int64_t)r * k + sb * 256 + 4 * lane);
+      v.y = __float_as_uint(yd[r * nsb + sb]);
+      v.z = (uint32_t)(int32_t)ybs[(r * nsb + sb) * 16 + (lane >> 2)];
+    }
+  }
+
+  __device__ __forceinline__ static void store_pass(const ActLds& s, const uint4& v, int b, int nsb, float qmax) {
+    const int lane = threadIdx.x & 63;
+    uint32_t c;
+    int32_t sum16;
+    float d;
+    if (FUSED) {
+      const float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+      q8k_block_wave(f, lane, qmax, c, sum16, d);
+    } else {
+      c = v.x;
+      d = __uint_as_float(v.y);
+      sum16 = (int32_t)v.z;
+    }
+    if (b >= NR * nsb) return;
+    const int k = nsb * 256;
+    const int r = b / nsb, sb = b - r * nsb;
+    *(uint32_t*)(s.codes + r * k + sb * 256 + 4 * lane) = c;
+    if ((lane & 3) == 0) s.s16[(r * nsb + sb) * 16 + (lane >> 2)] = sum16;
+    if (lane == 0) s.dy[r * nsb + sb] = d;
+  }
+
+  __device__ __forceinline__ void load(int nsb, const float* x, int64_t xstride, const int8_t* yq, const float* yd,
+                                       const int16_t* ybs) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int p = 0; p < kPre; p++) load_pass(v[p], p * kWaves + wv, nsb, x, xstride, yq, yd, ybs);
+  }
+
+  __device__ __forceinline__ void store(const ActLds& s, int nsb, const float* x, int64_t xstride, const int8_t* yq,
+                                        const float* yd, const int16_t* ybs, float qmax) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int p = 0; p < kPre; p++)
+      if (p * kWaves + wv < NR * nsb) store_pass(s, v[p], p * kWaves + wv, nsb, qmax);
+    for (int p = kPre; p * kWaves + wv < NR * nsb; p++) {
+      uint4 t;
+      load_pass(t, p * kWaves + wv, nsb, x, xstride, yq, yd, ybs);
+      store_pass(s, t, p * kWaves + wv, nsb, qmax);
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // LDS staging for formats whose blocks are not 16-byte aligned. A wave
 // copies a span of a weight row (4096 values) into its own LDS region with
@@ -152,7 +219,8 @@ __device__ __forceinline__ int stage_span(const uint8_t* __restrict__ W, int64_t
   return (int)(start - a0);
 }
 
-// 4 bytes from LDS at any byte offset (two aligned dword reads + alignbyte).
+// 4 bytes from LDS at any byte offset (two aligned dword reads + alignbyte;
+// the hardware takes unaligned LDS reads too, but measured slower).
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t* lds, int off) {
   const int a = off & ~3;
   const uint32_t lo = *(const uint32_t*)(lds + a);

@@ -40,7 +40,8 @@ struct Span {
 // Loads the 16-byte aligned pieces (aligned as device addresses) from the one
 // holding byte p to the one holding byte p + len*210 - 1. Every piece read
 // holds at least one byte of the span, and an aligned piece never crosses a
-// page, so the bytes read beyond the span stay in mapped memory.
+// page, so the bytes read beyond the span stay in mapped memory. Lane L holds
+// pieces L + 64c.
 __device__ __forceinline__ void load_span(Span& sp, const uint8_t* __restrict__ p, int len, int lane) {
   // rounded down by pointer arithmetic: the compiler keeps these global
   // loads (an integer round trip would make them flat loads, which every LDS
@@ -49,45 +50,46 @@ __device__ __forceinline__ void load_span(Span& sp, const uint8_t* __restrict__ 
   const uint8_t* a0 = p - sp.off;
   sp.len = len;
   const int pieces = (int)((sp.off + len * 210 + 15) >> 4);
+  // every lane loads (no branches): lanes past the span's pieces load its
+  // last piece again, whose bytes are never read
 #pragma unroll
   for (int c = 0; c < kPiecesPerLane; c++) {
     const int pc = lane + 64 * c;
-    sp.p[c] = pc < pieces ? ld_stream16(a0 + 16 * pc) : make_uint4(0, 0, 0, 0);
+    sp.p[c] = ld_stream16(a0 + 16u * (uint32_t)(pc < pieces ? pc : pieces - 1));
   }
 }
 
-// Work: the spans of a row go to different waves of one workgroup. With
-// nspan spans per row, a workgroup of kWaves waves takes G = kWaves / nspan
-// rows at a time: wave wv works span wv % nspan of row-slot wv / nspan. Each
-// wave reduces its span's partial sum (wave_sum_dpp) into LDS; after the
-// workgroup barrier the span-0 wave of each row-slot adds the partials in
-// span order and writes the row. Row-slots walk the rows
-// (blockIdx.x + i * gridDim.x) * G + g, every wave of the grid the same
-// number of iterations (a wave without a row still meets the barriers).
-template <int NR, bool FUSED, int kWaves, bool PF>
-__global__ __launch_bounds__(64 * kWaves) void mv_q6k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
-                                                                    int64_t xstride, const int8_t* __restrict__ yq,
-                                                                    const float* __restrict__ yd,
-                                                                    const int16_t* __restrict__ ybs, float qmax) {
+// Work: each wave owns whole rows, gw, gw + W, ... (gw its index among the
+// W waves of the grid), and walks their spans in order with the loads of the
+// next kPfd spans in flight in a register ring (the loop is unrolled by kPfd,
+// so every buffer keeps its registers). A span is written to the wave's LDS
+// buffer, read back per lane, reduced (wave_sum_dpp) and added to its row's
+// sum in span order: the arithmetic of the multi-row kernel (matvec.hip), so
+// a row's result does not depend on the batch width. No barrier after the
+// activation fill: the waves run independently, and with one row per wave
+// every byte of a matrix of up to W rows is requested at once.
+constexpr int kPfd = 3;  // spans in flight per wave (3 x 16 registers)
+
+template <int NR, bool FUSED>
+__global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int nsb, int64_t W,
+                                                             const float* __restrict__ x, int64_t xstride,
+                                                             const int8_t* __restrict__ yq,
+                                                             const float* __restrict__ yd,
+                                                             const int16_t* __restrict__ ybs, float qmax) {
+  constexpr int kWaves = 16;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const ActLds s = act_lds(smem, NR, nsb);
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* const part_base = smem + (act_lds_bytes(NR, nsb) + 15) / 16 * 16;  // [2][kWaves][NR] floats
-  uint8_t* buf = part_base + 2 * kWaves * NR * 4 + (size_t)wv * kSpanBuf;
-  float* const part = (float*)part_base;
+  uint8_t* const buf = smem + (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + (size_t)wv * kSpanBuf;
   const int k = nsb * 256;
   const int64_t rowbytes = (int64_t)nsb * 210;
   const int64_t n_total = tg.row_end[tg.count - 1];
   const int nspan = (nsb + kSpanSb - 1) / kSpanSb;
-  const int G = kWaves / nspan;  // rows per workgroup iteration
-  const int g = wv / nspan, span = wv - g * nspan;
-  const bool active = g < G;
-  const int s0 = span * kSpanSb;
-  const int len = nsb - s0 < kSpanSb ? nsb - s0 : kSpanSb;
-  const int64_t rows_per_iter = (int64_t)gridDim.x * G;
-  const int64_t iters = (n_total + rows_per_iter - 1) / rows_per_iter;
+  const int64_t gw = (int64_t)blockIdx.x * kWaves + wv;
+  // spans of this wave: its rows times the spans of a row
+  const int64_t nrows = gw < n_total ? (n_total - 1 - gw) / W + 1 : 0;
+  const int64_t S = nrows * nspan;
 
-  auto row_of = [&](int64_t i) -> int64_t { return ((int64_t)blockIdx.x + i * gridDim.x) * G + g; };
   auto row_ptr = [&](int64_t R, float*& out, int64_t& ldd) -> const uint8_t* {
     int t = 0;
 #pragma unroll
@@ -99,153 +101,146 @@ __global__ __launch_bounds__(64 * kWaves) void mv_q6k_stream_kernel(MvTargets tg
     return (const uint8_t*)tg.w[t] + lrow * rowbytes;
   };
 
-  // 1. activation loads, then the first span's weight loads
+  // the loads: span lsp of row lR, whose bytes start at lrow
+  int64_t lR = gw;
+  int lsp = 0;
+  const uint8_t* lrow = nullptr;
+  auto load_next = [&](Span& sp) {
+    if (lsp == 0) {
+      float* o;
+      int64_t l;
+      lrow = row_ptr(lR, o, l);
+    }
+    const int s0 = lsp * kSpanSb;
+    load_span(sp, lrow + (int64_t)s0 * 210, nsb - s0 < kSpanSb ? nsb - s0 : kSpanSb, lane);
+    if (++lsp == nspan) {
+      lsp = 0;
+      lR += W;
+    }
+  };
+
+  // 1. activation loads, then the first spans' loads
   ActBatch<NR, FUSED, kWaves> act;
   act.load(nsb, x, xstride, yq, yd, ybs);
-  Span cur;
-  float* out = nullptr;
-  int64_t ldd = 0;
-  if (active && row_of(0) < n_total) load_span(cur, row_ptr(row_of(0), out, ldd) + (int64_t)s0 * 210, len, lane);
+  Span ring[kPfd];
+#pragma unroll
+  for (int j = 0; j < kPfd; j++)
+    if (j < S) load_next(ring[j]);
 
   // 2. the activation into LDS
   act.store(s, nsb, x, xstride, yq, yd, ybs, qmax);
   __syncthreads();
 
-  // 3. stream the rows
+  // 3. the spans, in order
   const int sbl = lane >> 2, u = lane & 3, h = u >> 1, l0 = 16 * (u & 1);
-  for (int64_t i = 0; i < iters; i++) {
-    const int64_t R = row_of(i);
-    const bool have = active && R < n_total;
-    float* cout = out;
-    const int64_t cldd = ldd;
+  int64_t R = gw;  // the span being computed: span sp of row R
+  int sp = 0;
+  float* out = nullptr;
+  int64_t ldd = 0;
+  float tot[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) tot[r] = 0.0f;
+
+  auto step = [&](Span& cur, int64_t sigma) {
+    if (sp == 0) (void)row_ptr(R, out, ldd);
+    // the span into this wave's LDS buffer (the previous span's reads are done)
+    wave_lds_sync();
+#pragma unroll
+    for (int c = 0; c < kPiecesPerLane; c++)
+      if (lane + 64 * c < kSpanPieces) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
+    wave_lds_sync();
+    const int off = cur.off, len = cur.len;
+    // this buffer's next span
+    if (sigma + kPfd < S) load_next(cur);
     float acc[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) acc[r] = 0.0f;
-    Span nxt;
-    if (have) {
-      // the span into this wave's LDS buffer
-      wave_lds_sync();  // the previous span's reads are done
+    if (sbl < len) {
+      const int b = off + 210 * sbl;
+      uint32_t qlA[4], qlB[4], qh[4], s4[2];
+      lds_words<4>(buf, b + 64 * h + l0, qlA);
+      lds_words<4>(buf, b + 64 * h + 32 + l0, qlB);
+      lds_words<4>(buf, b + 128 + 32 * h + l0, qh);
+      lds_words<2>(buf, b + 192 + 8 * h, s4);  // scales 8h .. 8h+7
+      int sc[4];
 #pragma unroll
-      for (int c = 0; c < kPiecesPerLane; c++)
-        if (lane + 64 * c < kSpanPieces) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
-      wave_lds_sync();
-      const int off = cur.off;
-      if (PF && row_of(i + 1) < n_total)
-        load_span(nxt, row_ptr(row_of(i + 1), out, ldd) + (int64_t)s0 * 210, len, lane);
-      if (sbl < len) {
-        const int b = off + 210 * sbl;
-        uint32_t qlA[4], qlB[4], qh[4], s4[2];
-        lds_words<4>(buf, b + 64 * h + l0, qlA);
-        lds_words<4>(buf, b + 64 * h + 32 + l0, qlB);
-        lds_words<4>(buf, b + 128 + 32 * h + l0, qh);
-        lds_words<2>(buf, b + 192 + 8 * h, s4);  // scales 8h .. 8h+7
-        int sc[4];
+      for (int t = 0; t < 4; t++) {
+        const int gg = (l0 >> 4) + 2 * t;
+        sc[t] = (int)(int8_t)((s4[gg >> 2] >> (8 * (gg & 3))) & 0xFF);
+      }
+      const float dx = h2f((uint16_t)lds_u16(buf, b + 208));
+      const int sb = sp * kSpanSb + sbl;
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        const int8_t* yrow = s.codes + r * k + sb * 256 + 128 * h + l0;
+        int yv[4][4], bs[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-          const int gg = (l0 >> 4) + 2 * t;
-          sc[t] = (int)(int8_t)((s4[gg >> 2] >> (8 * (gg & 3))) & 0xFF);
+          const int4 q = *(const int4*)(yrow + 32 * t);
+          yv[t][0] = q.x; yv[t][1] = q.y; yv[t][2] = q.z; yv[t][3] = q.w;
+          bs[t] = s.s16[(r * nsb + sb) * 16 + 8 * h + 2 * t + (l0 >> 4)];
         }
-        const float dx = h2f((uint16_t)lds_u16(buf, b + 208));
-        const int sb = s0 + sbl;
-#pragma unroll
-        for (int r = 0; r < NR; r++) {
-          const int8_t* yrow = s.codes + r * k + sb * 256 + 128 * h + l0;
-          int yv[4][4], bs[4];
-#pragma unroll
-          for (int t = 0; t < 4; t++) {
-            const int4 q = *(const int4*)(yrow + 32 * t);
-            yv[t][0] = q.x; yv[t][1] = q.y; yv[t][2] = q.z; yv[t][3] = q.w;
-            bs[t] = s.s16[(r * nsb + sb) * 16 + 8 * h + 2 * t + (l0 >> 4)];
-          }
-          acc[r] = q6k_unit(qlA, qlB, qh, sc, dx, yv, s.dy[r * nsb + sb], bs, acc[r]);
-        }
+        acc[r] = q6k_unit(qlA, qlB, qh, sc, dx, yv, s.dy[r * nsb + sb], bs, acc[r]);
       }
     }
-    // partial sums of the spans, added in span order
-    float* slot = part + (i & 1) * kWaves * NR;
+    // the span's sum, added to its row's in span order
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       const float v = wave_sum_dpp(acc[r]);
-      if (lane == 0) slot[wv * NR + r] = v;
+      tot[r] = sp == 0 ? v : __fadd_rn(tot[r], v);
     }
-    __syncthreads();
-    if (have && span == 0 && lane == 0) {
+    if (++sp == nspan) {
+      if (lane == 0) {
 #pragma unroll
-      for (int r = 0; r < NR; r++) {
-        float tot = slot[(g * nspan) * NR + r];
-        for (int q = 1; q < nspan; q++) tot = __fadd_rn(tot, slot[(g * nspan + q) * NR + r]);
-        cout[r * cldd] = tot;
+        for (int r = 0; r < NR; r++) out[r * ldd] = tot[r];
       }
+      sp = 0;
+      R += W;
     }
-    if (PF) {
-      cur = nxt;
-    } else if (active && row_of(i + 1) < n_total) {
-      load_span(cur, row_ptr(row_of(i + 1), out, ldd) + (int64_t)s0 * 210, len, lane);
-    }
+  };
+
+  for (int64_t sigma = 0; sigma < S; sigma += kPfd) {
+#pragma unroll
+    for (int j = 0; j < kPfd; j++)
+      if (sigma + j < S) step(ring[j], sigma + j);
   }
 }
 
-template <int NR, int WPG, bool PF>
-size_t stream_lds(int nsb) {
-  return (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + 2 * WPG * NR * 4 + (size_t)WPG * kSpanBuf;
-}
-
-template <int NR, int WPG, bool PF>
+// one workgroup of 16 waves a CU (up to 128 registers a lane, kPfd spans in
+// flight), a wave a row where the rows are few
+template <int NR>
 hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
-                         float qmax, int64_t waves, hipStream_t st) {
-  const size_t lds = stream_lds<NR, WPG, PF>(nsb);
-  const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
-  // dynamic LDS past 64 KiB needs the kernel's limit raised (to the 160 KiB
-  // of a CU), once per kernel
-  static bool raised[2] = {false, false};
+                         float qmax, int cus, hipStream_t st) {
+  const int64_t n_total = t.row_end[t.count - 1];
+  int64_t waves = (int64_t)cus * 16;
+  if (waves > n_total) waves = (n_total + 15) / 16 * 16;
+  const size_t lds = (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + 16 * (size_t)kSpanBuf;
+  const dim3 grid((unsigned)(waves / 16));
   if (pre) {
-    auto* kfn = &mv_q6k_stream_kernel<NR, false, WPG, PF>;
-    if (!raised[0]) {
-      if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-        return hipErrorInvalidValue;
-      raised[0] = true;
-    }
-    kfn<<<grid, 64 * WPG, lds, st>>>(t, nsb, nullptr, 0, pre->codes, pre->d, (const int16_t*)pre->sums, qmax);
+    auto* kfn = &mv_q6k_stream_kernel<NR, false>;
+    if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+    kfn<<<grid, 1024, lds, st>>>(t, nsb, waves, nullptr, 0, pre->codes, pre->d, (const int16_t*)pre->sums, qmax);
   } else {
-    auto* kfn = &mv_q6k_stream_kernel<NR, true, WPG, PF>;
-    if (!raised[1]) {
-      if (hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-        return hipErrorInvalidValue;
-      raised[1] = true;
-    }
-    kfn<<<grid, 64 * WPG, lds, st>>>(t, nsb, x, xstride, nullptr, nullptr, nullptr, qmax);
+    auto* kfn = &mv_q6k_stream_kernel<NR, true>;
+    if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+    kfn<<<grid, 1024, lds, st>>>(t, nsb, waves, x, xstride, nullptr, nullptr, nullptr, qmax);
   }
   return hipGetLastError();
-}
-
-template <int NR>
-hipError_t launch_shape(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
-                        float qmax, const MvShape& sh, hipStream_t st) {
-  return sh.prefetch ? launch_stream<NR, 16, true>(t, nsb, x, xstride, pre, qmax, sh.waves, st)
-                     : launch_stream<NR, 16, false>(t, nsb, x, xstride, pre, qmax, sh.waves, st);
 }
 
 }  // namespace
 
 // LDS: the activation (rows x k codes + scales + sums) and one span buffer
-// per wave of a 16-wave workgroup, within a CU's 160 KiB; a row's spans must
-// fit the 16 waves.
+// per wave of a 16-wave workgroup, within a CU's 160 KiB.
 bool mv_q6k_rows_supported(int64_t k, int64_t rows) {
-  return rows >= 1 && rows <= 2 && k % 256 == 0 && k >= 256 && k <= 16 * kSpanSb * 256 && k * rows <= 32768;
-}
-
-int mv_q6k_rows_per_group(int64_t k) { return 16 / (int)((k / 256 + kSpanSb - 1) / kSpanSb); }
-
-size_t mv_q6k_rows_lds(int64_t k, int64_t rows, int wpg) {
-  const int nsb = (int)(k / 256);
-  return (act_lds_bytes((int)rows, nsb) + 15) / 16 * 16 + 2 * (size_t)wpg * rows * 4 + (size_t)wpg * kSpanBuf;
+  return rows >= 1 && rows <= 2 && k % 256 == 0 && k >= 256 && k * rows <= 65536;
 }
 
 hipError_t launch_mv_q6k_rows(const MvTargets& t, int64_t k, int64_t rows, const float* x, int64_t xstride,
-                              const ActPlanes* pre, float qmax, const MvShape& sh, hipStream_t st) {
+                              const ActPlanes* pre, float qmax, int cus, hipStream_t st) {
   const int nsb = (int)(k / 256);
-  if (rows == 1) return launch_shape<1>(t, nsb, x, xstride, pre, qmax, sh, st);
-  return launch_shape<2>(t, nsb, x, xstride, pre, qmax, sh, st);
+  if (rows == 1) return launch_stream<1>(t, nsb, x, xstride, pre, qmax, cus, st);
+  return launch_stream<2>(t, nsb, x, xstride, pre, qmax, cus, st);
 }
 
 }  // namespace qmm

@@ -110,29 +110,17 @@ bool stream_supported(int type, int64_t k, int64_t rows) {
   return false;
 }
 
-// Launch shape for n_total weight rows. Q4_K: up to 32 waves per CU, about
-// 1.5 rows per wave where the rows are few, 16-wave workgroups (one
-// activation fill per 16 waves). Q6_K: 16-wave workgroups taking
-// mv_q6k_rows_per_group rows at a time, one workgroup per CU at most (each
-// workgroup fills the activation once, and further groups per CU cost more
-// in fills than they give in bytes in flight), the next span prefetched when
-// a workgroup has 2 or more rounds. Q4_K prefetches when a wave has 3 or
-// more rows.
-qmm::MvShape stream_shape(int type, int64_t k, int64_t rows, int64_t n_total) {
-  (void)rows;
+// Launch shape of the Q4_K decode kernel for n_total weight rows: up to 32
+// waves per CU, about 1.5 rows per wave where the rows are few, 16-wave
+// workgroups (one activation fill per 16 waves), the next row's loads in
+// flight whenever a wave has more than one row.
+qmm::MvShape stream_shape(int64_t n_total) {
   const int64_t cus = cu_count();
-  if (type == qmm::T_Q6_K) {
-    const int64_t G = qmm::mv_q6k_rows_per_group(k);
-    int64_t groups = (n_total + G - 1) / G;
-    if (groups > cus) groups = cus;
-    const int64_t iters = (n_total + groups * G - 1) / (groups * G);
-    return qmm::MvShape{groups * 16, 16, iters >= 2};
-  }
   int64_t waves = n_total * 2 / 3;
   if (waves < 1024) waves = 1024;
   if (waves > cus * 32) waves = cus * 32;
   waves = (waves + 15) / 16 * 16;
-  return qmm::MvShape{waves, 16, n_total >= 3 * waves};
+  return qmm::MvShape{waves, 16, n_total > waves};
 }
 
 // One streaming launch over up to kMaxTargets weights.
@@ -149,9 +137,8 @@ hipError_t launch_stream_targets(int type, int count, const void* const* w, cons
     t.row_end[i] = end;
   }
   t.count = count;
-  const qmm::MvShape sh = stream_shape(type, k, rows, end);
-  if (type == qmm::T_Q6_K) return qmm::launch_mv_q6k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), sh, st);
-  return qmm::launch_mv_q4k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), sh, st);
+  if (type == qmm::T_Q6_K) return qmm::launch_mv_q6k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), (int)cu_count(), st);
+  return qmm::launch_mv_q4k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), stream_shape(end), st);
 }
 
 }  // namespace

@@ -169,10 +169,25 @@ __device__ __forceinline__ void q8k_block_group16(const float v[16], int gl, flo
   uint32_t lo = amax != 0.0f
                     ? ((uint32_t)(0xFFFF - (16 * gl + first)) << 1) | (__float_as_uint(v[first]) >> 31)
                     : 0u;
+  // the largest (hi, lo) of the 16 lanes, through DPP within the lane's row
+  // of 16 (pairs, pairs of pairs, then the mirrored quads and halves): a
+  // maximum, so the order does not matter
 #pragma unroll
-  for (int m = 1; m <= 8; m <<= 1) {
-    const uint32_t ohi = (uint32_t)__shfl_xor((int)hi, m, kWave);
-    const uint32_t olo = (uint32_t)__shfl_xor((int)lo, m, kWave);
+  for (int step = 0; step < 4; step++) {
+    uint32_t ohi, olo;
+    if (step == 0) {
+      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0xB1, 0xF, 0xF, true);  // quad 1,0,3,2
+      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0xB1, 0xF, 0xF, true);
+    } else if (step == 1) {
+      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x4E, 0xF, 0xF, true);  // quad 2,3,0,1
+      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x4E, 0xF, 0xF, true);
+    } else if (step == 2) {
+      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x141, 0xF, 0xF, true);  // half mirror
+      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x141, 0xF, 0xF, true);
+    } else {
+      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x140, 0xF, 0xF, true);  // mirror
+      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x140, 0xF, 0xF, true);
+    }
     if (ohi > hi || (ohi == hi && olo > lo)) { hi = ohi; lo = olo; }
   }
   amax = __uint_as_float(hi);
@@ -190,6 +205,69 @@ __device__ __forceinline__ void q8k_block_group16(const float v[16], int gl, flo
     }
     d = 1.0f / iscale;
   }
+}
+
+// The same Q8_K block held by a whole wave: lane L holds values 4L..4L+3 in
+// v[0..3]. The key's maximum is taken within each row of 16 lanes (DPP), then
+// over the four rows (readlane, uniform). Returns the lane's 4 codes packed
+// in c, the sum of the 16 values of the lane's quad (lanes 4g..4g+3: the
+// reference's bsums entry g) in sum16, and d. All 64 lanes must call.
+__device__ __forceinline__ void q8k_block_wave(const float v[4], int lane, float qmax, uint32_t& c, int32_t& sum16,
+                                               float& d) {
+#pragma clang fp contract(off)
+  float amax = 0.0f;
+  int first = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float a = fabsf(v[i]);
+    if (amax < a) { amax = a; first = i; }
+  }
+  uint32_t hi = __float_as_uint(amax);
+  uint32_t lo = amax != 0.0f ? ((uint32_t)(0xFFFF - (4 * lane + first)) << 1) | (__float_as_uint(v[first]) >> 31)
+                             : 0u;
+#pragma unroll
+  for (int step = 0; step < 4; step++) {
+    uint32_t ohi, olo;
+    if (step == 0) {
+      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0xB1, 0xF, 0xF, true);
+      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0xB1, 0xF, 0xF, true);
+    } else if (step == 1) {
+      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x4E, 0xF, 0xF, true);
+      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x4E, 0xF, 0xF, true);
+    } else if (step == 2) {
+      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x141, 0xF, 0xF, true);
+      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x141, 0xF, 0xF, true);
+    } else {
+      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x140, 0xF, 0xF, true);
+      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x140, 0xF, 0xF, true);
+    }
+    if (ohi > hi || (ohi == hi && olo > lo)) { hi = ohi; lo = olo; }
+  }
+  uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)hi, 0), bl = (uint32_t)__builtin_amdgcn_readlane((int)lo, 0);
+#pragma unroll
+  for (int r = 1; r < 4; r++) {
+    const uint32_t oh = (uint32_t)__builtin_amdgcn_readlane((int)hi, 16 * r);
+    const uint32_t ol = (uint32_t)__builtin_amdgcn_readlane((int)lo, 16 * r);
+    if (oh > bh || (oh == bh && ol > bl)) { bh = oh; bl = ol; }
+  }
+  amax = __uint_as_float(bh);
+  c = 0u;
+  int32_t s = 0;
+  d = 0.0f;
+  if (amax != 0.0f) {
+    const float mx = (bl & 1u) ? -amax : amax;
+    const float iscale = -qmax / mx;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int q = rs_as_i8(rs_min(roundf(iscale * v[i]), 127.0f));
+      c |= (uint32_t)(q & 0xFF) << (8 * i);
+      s += q;
+    }
+    d = 1.0f / iscale;
+  }
+  s += __builtin_amdgcn_mov_dpp(s, 0xB1, 0xF, 0xF, true);
+  s += __builtin_amdgcn_mov_dpp(s, 0x4E, 0xF, 0xF, true);
+  sum16 = s;
 }
 
 // Q4_K 6-bit scale/min of sub-block j (k_quants utils.rs:50-60).
@@ -248,17 +326,25 @@ __device__ __forceinline__ float q4k_unit(uint4 h, uint4 qa, uint4 qb, const int
 __device__ __forceinline__ float q6k_unit(const uint32_t qlA[4], const uint32_t qlB[4], const uint32_t qh[4],
                                           const int sc[4], float dx, const int y[4][4], float dy, const int bs[4],
                                           float acc) {
+  // q6 = (ql nibble) | (qh bits 2t, 2t+1) << 4 for every byte, the high bits
+  // taken where they already sit, shifted by 4 - 2t
+  int sums[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const uint32_t h = qh[q];
+    const uint32_t q0 = (qlA[q] & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+    const uint32_t q1 = (qlB[q] & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+    const uint32_t q2 = ((qlA[q] >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+    const uint32_t q3 = ((qlB[q] >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+    sums[0] = dot4((int)q0, y[0][q], sums[0]);
+    sums[1] = dot4((int)q1, y[1][q], sums[1]);
+    sums[2] = dot4((int)q2, y[2][q], sums[2]);
+    sums[3] = dot4((int)q3, y[3][q], sums[3]);
+  }
   int tot = 0;
 #pragma unroll
   for (int t = 0; t < 4; t++) {
-    const uint32_t* ql = (t & 1) ? qlB : qlA;
-    const int nsh = 4 * (t >> 1);
-    int s = 0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const uint32_t q6 = ((ql[q] >> nsh) & 0x0F0F0F0Fu) | (((qh[q] >> (2 * t)) & 0x03030303u) << 4);
-      s = dot4((int)q6, y[t][q], s);
-    }
+    const int s = sums[t];
     // |s - 32*bs| <= 16*63*127 + 32*16*127 < 2^23: a 24-bit product is exact
     tot += __mul24(sc[t], s - 32 * bs[t]);
   }

@@ -74,15 +74,14 @@ struct MvShape {
 };
 int64_t mv_q4k_rows_waves(int64_t n_total, int per_wave);
 
-// Q6_K decode matvec over 1-2 activation rows, streaming spans of 16
-// super-blocks through per-wave LDS buffers, the spans of a row on different
-// waves of one 16-wave workgroup (mv_q6k_rows_per_group rows at a time; sh.wpg
-// is ignored). mv_q6k_rows_lds = dynamic LDS bytes of a workgroup.
+// Q6_K decode matvec over 1-2 activation rows: each wave streams whole rows
+// in spans of 16 super-blocks through its LDS buffer, the next spans' loads in
+// flight; one 16-wave workgroup per CU (cus), a wave per row where rows are
+// few. Quantizes the f32 activation in LDS (pre == nullptr) or reads
+// pre-quantized Q8_K planes.
 bool mv_q6k_rows_supported(int64_t k, int64_t rows);
-int mv_q6k_rows_per_group(int64_t k);
-size_t mv_q6k_rows_lds(int64_t k, int64_t rows, int wpg);
 hipError_t launch_mv_q6k_rows(const MvTargets& t, int64_t k, int64_t rows, const float* x, int64_t xstride,
-                              const ActPlanes* pre, float qmax, const MvShape& sh, hipStream_t s);
+                              const ActPlanes* pre, float qmax, int cus, hipStream_t s);
 hipError_t launch_mv_q4k_rows(const MvTargets& t, int64_t k, int64_t rows, const float* x, int64_t xstride,
                               const ActPlanes* pre, float qmax, const MvShape& sh, hipStream_t s);
 hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
