@@ -85,14 +85,25 @@ constexpr int kFewRowsKQuant = 4;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// The skinny matrix-core kernel: Q4_K up to gemm_q4k_skinny_max_rows() rows
-// past the few-rows line.
+// The few-row matrix-core kernels (Q4_K, Q6_K): up to
+// gemm_q4k_skinny_max_rows() rows past the few-rows line.
 bool skinny_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows) {
-  if (type != qmm::T_Q4_K || rows > qmm::gemm_q4k_skinny_max_rows() || !aligned16(w) || !aligned16(xq) ||
-      !qmm::gemm_q4k_skinny_fits(k, rows))
+  if (rows > qmm::gemm_q4k_skinny_max_rows() || !aligned16(w) || !aligned16(xq)) return false;
+  int64_t wbytes;
+  if (type == qmm::T_Q4_K && qmm::gemm_q4k_skinny_fits(k, rows))
+    wbytes = n * (k / 256) * 144;
+  else if (type == qmm::T_Q6_K && qmm::gemm_q6k_skinny_fits(k, rows))
+    wbytes = n * (k / 256) * 210;
+  else
     return false;
   if (rows > qmm::matvec_max_rows()) return true;
-  return rows >= kFewRowsKQuant && n * (k / 256) * 144 >= kFewRowsLeastBytes;
+  return rows >= kFewRowsKQuant && wbytes >= kFewRowsLeastBytes;
+}
+
+hipError_t launch_skinny(int type, const qmm::MvTargets& t, int64_t k, const qmm::ActPlanes& p, int64_t rows,
+                         hipStream_t st) {
+  if (type == qmm::T_Q6_K) return qmm::launch_gemm_q6k_skinny(t, k, p, rows, (int)cu_count(), st);
+  return qmm::launch_gemm_q4k_skinny(t, k, p, rows, (int)cu_count(), st);
 }
 
 // The tiled int8 matrix-core GEMM: Q4_K past the skinny kernel's rows,
@@ -239,7 +250,7 @@ int launch_product(int type, const void* w, int64_t n, int64_t k, const void* xq
     t.ldd[0] = ldd;
     t.row_end[0] = n;
     t.count = 1;
-    if (qmm::launch_gemm_q4k_skinny(t, k, p, rows, cu_count(), st) != hipSuccess) return QMM_DEVICE_ERROR;
+    if (launch_skinny(type, t, k, p, rows, st) != hipSuccess) return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
   }
@@ -328,7 +339,7 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
   int64_t end = 0;
   auto flush = [&]() -> int {
     if (grp.count == 0) return QMM_OK;
-    if (qmm::launch_gemm_q4k_skinny(grp, k, p, rows, cu_count(), st) != hipSuccess) return QMM_DEVICE_ERROR;
+    if (launch_skinny(type, grp, k, p, rows, st) != hipSuccess) return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     grp = qmm::MvTargets{};
     end = 0;

@@ -105,6 +105,12 @@ bool gemm_q4k_skinny_fits(int64_t k, int64_t rows);
 hipError_t launch_gemm_q4k_skinny(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, int cus,
                                   hipStream_t st);
 
+// Q6_K products of a few rows (gemm_q6k_skinny.hip): up to 32 activation
+// rows, targets as the stream kernels.
+bool gemm_q6k_skinny_fits(int64_t k, int64_t rows);
+hipError_t launch_gemm_q6k_skinny(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, int cus,
+                                  hipStream_t st);
+
 int gemm_q4k_min_rows();
 // The GEMM indexes with 32-bit byte offsets: the weight below 2 GiB and
 // (rows + 128) * k below 2^31.

@@ -198,3 +198,63 @@ def test_q4k_skinny_shared_activation_equals_forward(rows):
     shared = QMatMul.forward_shared(x, mats)
     for m, y in zip(mats, shared):
         assert torch.equal(y, m.forward(x))
+
+
+# ---------------------------------------------------------------------------
+# the Q6_K few-row matrix-core kernel: every inner sum an exact int32, so the
+# gap to the oracle is the order of the f32 scaling (~1e-7)
+# ---------------------------------------------------------------------------
+TIGHT_Q6K = 1e-5
+
+Q6K_SKINNY_SHAPES = [  # (k, n, rows): past the 2 MiB line at 4-8 rows; rows of 3 and 5 super-blocks
+    # (210-byte blocks at every 2-byte offset); ragged n; one and two 16-row tiles
+    (4096, 2048, 4), (14336, 1000, 8), (2048, 1300, 6), (768, 700, 12), (1280, 513, 24),
+    (256, 100, 9), (28672, 80, 16), (512, 129, 32),
+]
+
+
+def q6k(w: np.ndarray):
+    wq = qref.from_float(qref.Q6_K, w)
+    return QTensor.from_data(wq.tobytes(), w.shape, GgmlDType.Q6K, device=DEV), wq
+
+
+@pytest.mark.parametrize("k,n,rows", Q6K_SKINNY_SHAPES)
+def test_q6k_skinny_parity(k, n, rows):
+    rng = np.random.default_rng(zlib.crc32(f"q6skinny-{k}-{n}-{rows}".encode()))
+    w = weights(rng, n, k)
+    x = activations(rng, rows, k, outliers=True)
+    qt, wq = q6k(w)
+    L = lib()
+    before = L.qmm_gemm_launches()
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert L.qmm_gemm_launches() == before + 1, "the matrix-core kernel did not run"
+    want = qref.matmul(qref.Q6_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q6_K, wq, n * k).reshape(n, k)
+    err = normalised_error(y, want, wdeq, x)
+    assert err <= TIGHT_Q6K, f"k={k} n={n} rows={rows}: {err}"
+
+
+@pytest.mark.parametrize("rows", [8, 16])
+def test_q6k_skinny_c5_down_projection(rows):
+    """BASELINE C5's down projection (8192 x 28672 Q6_K) at the
+    speculative-verification widths."""
+    rng = np.random.default_rng(60 + rows)
+    w = weights(rng, 8192, 28672)
+    x = activations(rng, rows, 28672)
+    qt, wq = q6k(w)
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    want = qref.matmul(qref.Q6_K, x, wq, 8192)
+    wdeq = qref.to_float(qref.Q6_K, wq, 8192 * 28672).reshape(8192, 28672)
+    assert normalised_error(y, want, wdeq, x) <= TIGHT_Q6K
+
+
+def test_q6k_skinny_shared_activation_equals_forward():
+    """Q6_K weights through one qmm_forward_shared equal each weight's own
+    forward bit for bit."""
+    rng = np.random.default_rng(77)
+    k = 2048
+    mats = [QMatMul(q6k(weights(rng, n, k))[0]) for n in (1300, 100, 1500)]
+    x = upload(activations(rng, 12, k))
+    shared = QMatMul.forward_shared(x, mats)
+    for m, y in zip(mats, shared):
+        assert torch.equal(y, m.forward(x))

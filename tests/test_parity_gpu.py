@@ -25,10 +25,13 @@ TIGHT_MATVEC = 1e-5
 
 def takes_matrix_cores(qtype, k, n, rows):
     """The library's few-rows policy (the reference's mmq_takes_few_rows,
-    quantized/cuda.rs:790-839): Q4_K products of more than 8 rows, or of 4
-    and more on weights of 2 MiB and more, run on the int8 matrix cores."""
-    wbytes = n * (k // 256) * 144
-    return qtype == qref.Q4_K and (rows > 8 or (rows >= 4 and wbytes >= 2 << 20))
+    quantized/cuda.rs:790-839): Q4_K and Q6_K products of more than 8 rows,
+    or of 4 and more on weights of 2 MiB and more, run on the int8 matrix
+    cores."""
+    if qtype not in (qref.Q4_K, qref.Q6_K):
+        return False
+    wbytes = n * (k // 256) * (144 if qtype == qref.Q4_K else 210)
+    return rows > 8 or (rows >= 4 and wbytes >= 2 << 20)
 
 
 def upload(a: np.ndarray) -> torch.Tensor:
@@ -195,8 +198,7 @@ def test_matvec_parity(name, k, n, rows):
     err = normalised_error(y, want, wdeq, x)
     assert err <= TOL_MATVEC, f"{name} k={k} n={n} rows={rows}: {err}"
     if takes_matrix_cores(qtype, k, n, rows):
-        # the few-rows matrix-core product: its min term multiplies f16-rounded
-        # operands (test_gemm_gpu.py bounds it)
+        # the few-rows matrix-core products (test_gemm_gpu.py covers them)
         assert err <= 5e-4, f"{name} k={k} n={n} rows={rows}: {err}"
         return
     # Both sides sum the same exact int32 block products and differ only in
@@ -249,8 +251,9 @@ def test_batch_invariance(name):
     mm = QMatMul(qt)
     xs = upload(rng.standard_normal((12, k)).astype(np.float32))
     alone = mm.forward(xs[:1].contiguous())
-    # Q4_K from 9 rows on runs the prefill GEMM (test_gemm_gpu.py covers it)
-    widths = (2, 3, 4, 5, 6, 7, 8) if qtype == 12 else (2, 3, 4, 5, 6, 7, 8, 9, 12)
+    # Q4_K and Q6_K from 9 rows on run on the matrix cores (test_gemm_gpu.py
+    # covers them)
+    widths = (2, 3, 4, 5, 6, 7, 8) if qtype in (12, 14) else (2, 3, 4, 5, 6, 7, 8, 9, 12)
     for rows in widths:
         y = mm.forward(xs[:rows].contiguous())
         assert torch.equal(y[0], alone[0]), rows
