@@ -99,9 +99,12 @@ int qmm_matvec(int type, const void *w, const void *xq, float *dst, int64_t ldd,
                int64_t rows, int64_t stream);
 
 /* dst = x · Wᵀ for any rows >= 1 from an activation already quantized in
- * qmm_act_layout(type, rows) (qmm_quantize_act): the decode kernels up to
- * qmm_matvec_max_rows() rows, the int8 matrix-core GEMM from 9 rows for
- * Q4_K. Nothing is allocated. Replaces swarm_mmq_matmul's launch step
+ * qmm_act_layout(type, rows) (qmm_quantize_act), the kernel picked by the
+ * reference's few-rows policy (quantized/cuda.rs:775-839): the decode
+ * kernels up to qmm_matvec_max_rows() rows; for Q4_K and Q6_K the few-row
+ * int8 matrix-core kernels from 4 rows on weights of 2 MiB or more and for
+ * 9-32 rows, and for Q4_K the int8 matrix-core GEMM from 33 rows; the other
+ * types run the decode kernels 8 rows at a time. Nothing is allocated. Replaces swarm_mmq_matmul's launch step
  * (mmq_entry.cu:162-203), which multiplies the activation swarm_mmq_quantize
  * produced. */
 int qmm_matmul(int type, const void *w, const void *xq, float *dst, int64_t ldd, int64_t k, int64_t n,
@@ -121,10 +124,11 @@ int qmm_forward(int type, const void *w, const float *x, int64_t x_stride, float
 /* dst[i] = x · W[i]ᵀ for `count` weights of one type and the same k that
  * share the activation x (rows x k f32, `x_stride` floats apart): the
  * activation is quantized once for all of them. Weight i has n[i] rows and
- * writes dst[i] with leading dimension ldd[i]. For Q4_K at 1-2 rows the
- * products run as one launch per 4 weights, each quantizing the activation
- * in LDS (workspace unused); otherwise the activation is quantized once into
- * the workspace and each weight's product reads it. Plan (launch == 0) and
+ * writes dst[i] with leading dimension ldd[i]. For Q4_K and Q6_K at 1-2
+ * rows the products run as one launch per 4 weights, each quantizing the
+ * activation in LDS (workspace unused); otherwise the activation is
+ * quantized once into the workspace and each weight's product reads it, the
+ * weights the few-row matrix-core kernels take sharing one launch per 4. Plan (launch == 0) and
  * launch as qmm_forward. Replaces QMatMul::forward_shared with the CUDA
  * arm's shared activation (quantized/mod.rs:1221-1263,
  * quantized/cuda.rs:622-720). */
