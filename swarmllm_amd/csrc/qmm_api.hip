@@ -116,6 +116,7 @@ bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, i
 
 // The streaming decode kernels (Q4_K, Q6_K at 1-2 activation rows).
 bool stream_supported(int type, int64_t k, int64_t rows) {
+  if (qmm::mv_b32_rows_supported(type, k, rows)) return true;
   if (type == qmm::T_Q4_K) return qmm::mv_q4k_rows_supported(k, rows);
   if (type == qmm::T_Q6_K) return qmm::mv_q6k_rows_supported(k, rows);
   return false;
@@ -149,6 +150,7 @@ hipError_t launch_stream_targets(int type, int count, const void* const* w, cons
   }
   t.count = count;
   if (type == qmm::T_Q6_K) return qmm::launch_mv_q6k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), (int)cu_count(), st);
+  if (type != qmm::T_Q4_K) return qmm::launch_mv_b32_rows(type, t, k, rows, x, x_stride, pre, (int)cu_count(), st);
   return qmm::launch_mv_q4k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), stream_shape(end), st);
 }
 

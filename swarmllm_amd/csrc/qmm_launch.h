@@ -84,6 +84,13 @@ hipError_t launch_mv_q6k_rows(const MvTargets& t, int64_t k, int64_t rows, const
                               const ActPlanes* pre, float qmax, int cus, hipStream_t s);
 hipError_t launch_mv_q4k_rows(const MvTargets& t, int64_t k, int64_t rows, const float* x, int64_t xstride,
                               const ActPlanes* pre, float qmax, const MvShape& sh, hipStream_t s);
+// Q8_0 / IQ4_NL / MXFP4 decode matvec over 1-2 activation rows (mv_b32s.hip):
+// each wave streams whole rows in spans of 128 blocks, the next span in
+// flight; one 16-wave workgroup per CU. Quantizes the f32 activation in LDS
+// (pre == nullptr; rows 16-byte aligned) or reads pre-quantized Q8_0 planes.
+bool mv_b32_rows_supported(int type, int64_t k, int64_t rows);
+hipError_t launch_mv_b32_rows(int type, const MvTargets& t, int64_t k, int64_t rows, const float* x, int64_t xstride,
+                              const ActPlanes* pre, int cus, hipStream_t st);
 hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
 
 // ---- prefill GEMM on the int8 matrix cores --------------------------------
