@@ -474,8 +474,8 @@ def c1_q8_0(stream, reps: int = 50, copies: int = 16) -> dict:
     us = ms * 1e3 / (reps * copies)
     alg = n * (k // 32) * 34 + 4 * k + 4 * n
     gbs = alg / (us * 1e-6) / 1e9
-    log(f"C1: {us:.2f} us per Q8_0 product (quantize + matvec), {gbs:.0f} GB/s")
-    return {"workload": "C1: Q8_0 4096x4096 at M=1 (activation quantize + matvec launches)",
+    log(f"C1: {us:.2f} us per Q8_0 product (one launch, activation quantized in it), {gbs:.0f} GB/s")
+    return {"workload": "C1: Q8_0 4096x4096 at M=1 (qmm_forward: one launch, the activation quantized in it)",
             "us_per_product": round(us, 3), "alg_bytes": alg, "gbs": round(gbs, 1),
             "percent_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
 

@@ -162,6 +162,203 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_b32_kernel(
   }
 }
 
+// The streaming form: a workgroup of kMoeSWaves waves takes one run and a
+// block of the expert's rows, copies the quantized activation rows of up to
+// kMoePairs of the run's entries into LDS once, and each wave streams
+// kMoeRows consecutive weight rows (their spans of 128 blocks, the next span's
+// pieces in flight in registers), applying each to every entry of the chunk.
+// The rows a wave streams (rpw) are a launch parameter.
+// Per entry the unit arithmetic, the lane's partial across the spans of a
+// row and the wave reduction are those of the 1-2 row decode kernel
+// (mv_b32s.hip), so each entry's result is bit-identical to qmm_forward of
+// its input row, times its scale.
+constexpr int kMoeSWaves = 16;
+
+template <int FMT>
+struct MoeSpan {
+  static constexpr int kPieces = (15 + 128 * Fmt32<FMT>::B + 15) / 16;
+  static constexpr int kLoads = (kPieces + 63) / 64;
+  uint4 p[kLoads];
+  int off;
+  int len;
+};
+
+template <int FMT>
+__global__ __launch_bounds__(64 * kMoeSWaves) void moe_b32s_kernel(
+    const uint8_t* __restrict__ W, int64_t n, int nb, int64_t estride, int num_experts,
+    const int8_t* __restrict__ yq, const float* __restrict__ yd, const int32_t* __restrict__ runs,
+    const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int topk, int size_m,
+    float* __restrict__ dst, int64_t ldd, int rpw) {
+  using F = Fmt32<FMT>;
+  using Span = MoeSpan<FMT>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int k = nb * 32;
+  int8_t* const acodes = (int8_t*)smem;                          // [kMoePairs][k]
+  float* const ad = (float*)(smem + (size_t)kMoePairs * k);      // [kMoePairs][nb]
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t* const buf = smem + ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)wv * kStageBytes;
+
+  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  const int run = blockIdx.y;
+  if (run >= nruns) return;  // the whole workgroup: before any barrier
+  const int start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
+  const int len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
+  const int e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+  if (e < 0 || e >= num_experts) return;
+  const uint8_t* We = W + (int64_t)e * estride;
+  const int64_t rb = (int64_t)nb * F::B;
+  const int nspan = (nb + 127) / 128;
+  const int64_t r0 = ((int64_t)blockIdx.x * kMoeSWaves + wv) * rpw;
+  const int64_t nrows = r0 < n ? (n - r0 < rpw ? n - r0 : rpw) : 0;
+  const int64_t S = nrows * nspan;
+  const Lut32<FMT> lut;
+  const uint32_t t0 = lut.t0, t1 = lut.t1, t2 = lut.t2, t3 = lut.t3;
+  const int bl = 2 * lane;
+
+  for (int c0 = 0; c0 < len; c0 += kMoePairs) {
+    const int cnt = len - c0 < kMoePairs ? len - c0 : kMoePairs;
+    int64_t out_row[kMoePairs];
+    float scale[kMoePairs];
+    bool use[kMoePairs];
+    int64_t in_row[kMoePairs];
+#pragma unroll
+    for (int p = 0; p < kMoePairs; p++) {
+      const int pair = p < cnt ? __builtin_amdgcn_readfirstlane(ids[start + c0 + p]) : -1;
+      use[p] = pair >= 0 && pair < size_m;
+      out_row[p] = use[p] ? pair : 0;
+      in_row[p] = use[p] ? (topk_w ? pair : pair / topk) : 0;
+      scale[p] = use[p] && topk_w ? topk_w[pair] : 1.0f;
+    }
+    // the chunk's activation rows into LDS (after the previous chunk's reads)
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < kMoePairs; p++) {
+      if (!use[p]) continue;
+      for (int i = (int)threadIdx.x; i < k / 16; i += 64 * kMoeSWaves)
+        *(uint4*)(acodes + p * k + 16 * i) = *(const uint4*)(yq + in_row[p] * k + 16 * i);
+      for (int i = (int)threadIdx.x; i < nb; i += 64 * kMoeSWaves) ad[p * nb + i] = yd[in_row[p] * nb + i];
+    }
+    __syncthreads();
+
+    // stream the wave's rows
+    int64_t lr = r0;
+    int lsp = 0;
+    auto load_next = [&](Span& sp) {
+      const int b0 = lsp * 128;
+      const int blen = nb - b0 < 128 ? nb - b0 : 128;
+      const uint8_t* pp = We + lr * rb + (int64_t)b0 * F::B;
+      sp.off = (int)((uintptr_t)pp & 15);
+      sp.len = blen;
+      const uint8_t* a0 = pp - sp.off;
+      const int pieces = (sp.off + blen * F::B + 15) >> 4;
+#pragma unroll
+      for (int c = 0; c < Span::kLoads; c++) {
+        const int pc = lane + 64 * c;
+        sp.p[c] = ld_stream16(a0 + 16u * (uint32_t)(pc < pieces ? pc : pieces - 1));
+      }
+      if (++lsp == nspan) {
+        lsp = 0;
+        lr++;
+      }
+    };
+    Span sa, sb;
+    if (S > 0) load_next(sa);
+    if (S > 1) load_next(sb);
+    int64_t R = r0;
+    int sp = 0;
+    float acc[kMoePairs];
+#pragma unroll
+    for (int p = 0; p < kMoePairs; p++) acc[p] = 0.0f;
+    auto step = [&](Span& cur, int64_t sigma) {
+      wave_lds_sync();
+#pragma unroll
+      for (int c = 0; c < Span::kLoads; c++)
+        if (lane + 64 * c < Span::kPieces) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
+      wave_lds_sync();
+      const int off = cur.off, blen = cur.len;
+      if (sigma + 2 < S) load_next(cur);
+      if (bl < blen) {
+        const bool two = bl + 1 < blen;
+        uint32_t q0[8], q1[8];
+        float dx0, dx1;
+        F::decode(buf, off + bl * F::B, q0, dx0, t0, t1, t2, t3);
+        if (two) {
+          F::decode(buf, off + (bl + 1) * F::B, q1, dx1, t0, t1, t2, t3);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; t++) q1[t] = 0;
+          dx1 = 0.0f;
+        }
+        const int gb = sp * 128 + bl;
+#pragma unroll
+        for (int p = 0; p < kMoePairs; p++) {
+          if (!use[p]) continue;
+          Act64 a;
+          const int4* yp = (const int4*)(acodes + p * k + gb * 32);
+          const int4 a0 = yp[0], a1 = yp[1];
+          a.y[0][0] = a0.x; a.y[0][1] = a0.y; a.y[0][2] = a0.z; a.y[0][3] = a0.w;
+          a.y[0][4] = a1.x; a.y[0][5] = a1.y; a.y[0][6] = a1.z; a.y[0][7] = a1.w;
+          a.dy[0] = ad[p * nb + gb];
+          if (two) {
+            const int4 b0 = yp[2], b1 = yp[3];
+            a.y[1][0] = b0.x; a.y[1][1] = b0.y; a.y[1][2] = b0.z; a.y[1][3] = b0.w;
+            a.y[1][4] = b1.x; a.y[1][5] = b1.y; a.y[1][6] = b1.z; a.y[1][7] = b1.w;
+            a.dy[1] = ad[p * nb + gb + 1];
+          } else {
+#pragma unroll
+            for (int t = 0; t < 8; t++) a.y[1][t] = 0;
+            a.dy[1] = 0.0f;
+          }
+          acc[p] = b32_unit(q0, q1, dx0, dx1, a, acc[p]);
+        }
+      }
+      if (++sp == nspan) {
+#pragma unroll
+        for (int p = 0; p < kMoePairs; p++) {
+          if (!use[p]) continue;
+          const float v = wave_sum_dpp(acc[p]);
+          if (lane == 0) dst[out_row[p] * ldd + R] = __fmul_rn(v, scale[p]);
+          acc[p] = 0.0f;
+        }
+        sp = 0;
+        R++;
+      }
+    };
+    for (int64_t sigma = 0; sigma < S; sigma += 2) {
+      step(sa, sigma);
+      if (sigma + 1 < S) step(sb, sigma + 1);
+    }
+  }
+}
+
+template <int FMT>
+hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
+                        const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
+                        float* dst, int64_t ldd, int cus, hipStream_t st) {
+  const int nb = (int)(k / 32);
+  const int64_t estride = n * nb * Fmt32<FMT>::B;
+  const int64_t gy = size_m < num_experts ? size_m : num_experts;
+  // rows a wave: 8 (measured against 12-23 at C4's shapes: longer rows per
+  // wave lengthen each wave's chain of two-rows-in-flight steps more than
+  // fewer workgroups save in fills)
+  (void)cus;
+  const int64_t rpw = 8;
+  const int64_t rows_per_wg = (int64_t)kMoeSWaves * rpw;
+  const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
+  const size_t lds = ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)kMoeSWaves * kStageBytes;
+  auto* kfn = &moe_b32s_kernel<FMT>;
+  if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+  kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
+                                          topk_w, topk, (int)size_m, dst, ldd, (int)rpw);
+  return hipGetLastError();
+}
+
+// The streaming form's LDS: the chunk's activation rows and the waves' stage buffers.
+inline bool moe_stream_fits(int64_t k) {
+  const int64_t nb = k / 32;
+  return ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)kMoeSWaves * kStageBytes <= 160 * 1024;
+}
+
 template <int FMT>
 hipError_t launch_moe_fmt(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                           const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
@@ -185,10 +382,19 @@ size_t moe_runs_bytes(int64_t size_m) { return (size_t)(1 + 3 * size_m) * sizeof
 
 hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                       int32_t* runs, const int32_t* ids, const int32_t* expert_ids, const float* topk_w, int topk,
-                      int64_t size_m, float* dst, int64_t ldd, hipStream_t st) {
+                      int64_t size_m, float* dst, int64_t ldd, int cus, hipStream_t st) {
   moe_runs_kernel<<<1, 1024, 0, st>>>(expert_ids, (int)size_m, runs);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (moe_stream_fits(k)) {
+    switch (type) {
+      case T_Q8_0: return launch_moe_s<T_Q8_0>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+      case T_IQ4_NL:
+        return launch_moe_s<T_IQ4_NL>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+      case T_MXFP4: return launch_moe_s<T_MXFP4>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (type) {
     case T_Q8_0: return launch_moe_fmt<T_Q8_0>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, st);
     case T_IQ4_NL:

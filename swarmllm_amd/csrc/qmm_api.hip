@@ -404,7 +404,7 @@ int qmm_moe_forward(int type, const void* w, int num_experts, const float* x, in
   const qmm::ActPlanes p = qmm::act_planes(qmm::ACT_Q8_0, workspace, k, in_rows);
   int32_t* runs = (int32_t*)((char*)workspace + act);
   if (qmm::launch_moe(type, w, num_experts, n, k, p, runs, sorted_ids, expert_ids, topk_w, topk, size_m, dst, ldd,
-                      st) != hipSuccess)
+                      (int)cu_count(), st) != hipSuccess)
     return QMM_DEVICE_ERROR;
   g_moe_launches.fetch_add(1, std::memory_order_relaxed);
   return QMM_OK;

@@ -103,7 +103,7 @@ bool moe_supported(int type);
 size_t moe_runs_bytes(int64_t size_m);
 hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                       int32_t* runs, const int32_t* ids, const int32_t* expert_ids, const float* topk_w, int topk,
-                      int64_t size_m, float* dst, int64_t ldd, hipStream_t st);
+                      int64_t size_m, float* dst, int64_t ldd, int cus, hipStream_t st);
 
 // Q4_K products of a few rows (gemm_q4k_skinny.hip): up to
 // gemm_q4k_skinny_max_rows() activation rows, targets as the stream kernels.
