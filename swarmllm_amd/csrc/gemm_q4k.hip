@@ -252,36 +252,54 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
     // A-operand piece of K-chunk kc: (2kc + h) ^ (r32 & 15) = 2 (kc ^ xh) + hl
     const int xh = (r32 & 15) >> 1;
     const int8_t* at = sa + r32 * 256 + 16 * (h ^ (r32 & 1));
+    // The B operand of K-chunk kc of pass p: this lane's 16 code bytes of
+    // chunk kc/2 (low nibbles for even kc, high for odd) times sh or sl.
+    auto make_b = [&](int pass, int kc) {
+      const uint32_t sw = kc < 4 ? s03 : s47;
+      const uint32_t scv = (sw >> (8 * (kc & 3))) & 0xFF;
+      const uint32_t f = dup16(pass == 0 ? scv >> 3 : scv & 7);
+      const uint4& ch = chunk(cur, kc >> 1);
+      i4v b;
 #pragma unroll
-    for (int pass = 0; pass < 2; pass++) {
-#pragma unroll
-      for (int kc = 0; kc < 8; kc++) {
-        const uint32_t sw = kc < 4 ? s03 : s47;
-        const uint32_t scv = (sw >> (8 * (kc & 3))) & 0xFF;
-        const uint32_t f = dup16(pass == 0 ? scv >> 3 : scv & 7);
-        const uint4& ch = chunk(cur, kc >> 1);
-        i4v b;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const uint32_t w = word(ch, e);
-          b[e] = (int)pkmul((kc & 1) ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu, f);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-          const i4v a = *(const i4v*)(at + 32 * t * 256 + 32 * (kc ^ xh));
-          const i16v zero = {};
-          c[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, (pass == 0 && kc == 0) ? zero : c[t], 0, 0, 0);
-        }
-        // keep each K-chunk's operand loads next to its MFMAs (hoisting them all
-        // would hold 64 fragments in registers)
-        __builtin_amdgcn_sched_barrier(0);
+      for (int e = 0; e < 4; e++) {
+        const uint32_t w = word(ch, e);
+        b[e] = (int)pkmul((kc & 1) ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu, f);
       }
-      if (pass == 0) {
+      return b;
+    };
+    auto load_a = [&](int kc, i4v (&a)[4]) {
+#pragma unroll
+      for (int t = 0; t < 4; t++) a[t] = *(const i4v*)(at + 32 * t * 256 + 32 * (kc ^ xh));
+    };
+    // Software-pipelined by one K-chunk: each block issues its four MFMAs,
+    // then builds the next chunk's B operand and reads its A fragments, work
+    // that runs while the matrix unit is busy with the MFMAs before it.
+    i4v bq = make_b(0, 0);
+    i4v af[4];
+    load_a(0, af);
+#pragma unroll
+    for (int step = 0; step < 16; step++) {
+      const int pass = step >> 3, kc = step & 7;
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const i16v zero = {};
+        c[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[t], bq, step == 0 ? zero : c[t], 0, 0, 0);
+      }
+      if (step + 1 < 16) {
+        bq = make_b((step + 1) >> 3, (step + 1) & 7);
+        load_a((step + 1) & 7, af);
+      }
+      if (step == 7) {
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
           for (int i = 0; i < 16; i++) c[t][i] <<= 3;
       }
+      // keep each K-chunk's work in its block (hoisting the operand loads of
+      // every chunk would hold 64 fragments in registers)
+      __builtin_amdgcn_sched_barrier(0);
+      (void)pass;
+      (void)kc;
     }
 
     epilogue(c, sb, dw, dmin, m03, m47);
