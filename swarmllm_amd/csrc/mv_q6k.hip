@@ -66,12 +66,25 @@ __device__ __forceinline__ void load_span(Span& sp, const uint8_t* __restrict__ 
 // buffer, read back per lane, reduced (wave_sum_dpp) and added to its row's
 // sum in span order: the arithmetic of the multi-row kernel (matvec.hip), so
 // a row's result does not depend on the batch width. No barrier after the
-// activation fill: the waves run independently, and with one row per wave
-// every byte of a matrix of up to W rows is requested at once.
-constexpr int kPfd = 3;  // spans in flight per wave (3 x 16 registers)
+// activation fill: the waves run independently.
+//
+// Every step issues exactly one span's loads and writes all of its pieces,
+// whatever the position in the wave's work: past the wave's last span the
+// loads read a cached piece of the activation (never used) and lanes past a
+// span's pieces write their copy of its last piece to the slack piece. Only
+// the arithmetic and the output store depend on the position. The compiler
+// then counts the loads in flight exactly and waits for the oldest span only;
+// a load issued on one path and not another would make it wait for them all.
+//
+// Spans in flight per wave: one, the next span's loads issued while the
+// current one is computed. Measured on C2's down projection (4096 x 14336,
+// a row per wave): 14.6 us with one span in flight, 16.1 us with two, 18.0 us
+// with three; more requests outstanding at once (41 MB with three) lower
+// what HBM delivers rather than hide more latency.
+constexpr int kPfd = 1;
 
 template <int NR, bool FUSED>
-__global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int nsb, int64_t W,
+__global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int nsb, int W,
                                                              const float* __restrict__ x, int64_t xstride,
                                                              const int8_t* __restrict__ yq,
                                                              const float* __restrict__ yd,
@@ -83,36 +96,40 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
   uint8_t* const buf = smem + (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + (size_t)wv * kSpanBuf;
   const int k = nsb * 256;
   const int64_t rowbytes = (int64_t)nsb * 210;
-  const int64_t n_total = tg.row_end[tg.count - 1];
+  // row numbers fit an int (the host checks)
+  const int n_total = (int)tg.row_end[tg.count - 1];
   const int nspan = (nsb + kSpanSb - 1) / kSpanSb;
-  const int64_t gw = (int64_t)blockIdx.x * kWaves + wv;
+  const int gw = blockIdx.x * kWaves + wv;
   // spans of this wave: its rows times the spans of a row
-  const int64_t nrows = gw < n_total ? (n_total - 1 - gw) / W + 1 : 0;
-  const int64_t S = nrows * nspan;
+  const int nrows = gw < n_total ? (n_total - 1 - gw) / W + 1 : 0;
+  const int S = nrows * nspan;
 
-  auto row_ptr = [&](int64_t R, float*& out, int64_t& ldd) -> const uint8_t* {
+  auto target_of = [&](int R, int& lrow) {
     int t = 0;
 #pragma unroll
     for (int q = 0; q < kMaxTargets - 1; q++)
-      if (q < tg.count - 1 && R >= tg.row_end[q]) t = q + 1;
-    const int64_t lrow = R - (t ? tg.row_end[t - 1] : 0);
-    out = tg.dst[t] + lrow;
-    ldd = tg.ldd[t];
-    return (const uint8_t*)tg.w[t] + lrow * rowbytes;
+      if (q < tg.count - 1 && R >= (int)tg.row_end[q]) t = q + 1;
+    lrow = R - (t ? (int)tg.row_end[t - 1] : 0);
+    return t;
   };
 
-  // the loads: span lsp of row lR, whose bytes start at lrow
-  int64_t lR = gw;
-  int lsp = 0;
+  // the loads: span lsp of row lR, whose bytes start at lrow; past the
+  // wave's last row, the first 224 bytes of the activation (16-byte aligned,
+  // at least 256 bytes long, and just read by every workgroup, so cached)
+  int lR = gw, lsp = 0;
   const uint8_t* lrow = nullptr;
+  const uint8_t* const idle = FUSED ? (const uint8_t*)x : (const uint8_t*)yq;
   auto load_next = [&](Span& sp) {
-    if (lsp == 0) {
-      float* o;
-      int64_t l;
-      lrow = row_ptr(lR, o, l);
+    if (lsp == 0 && lR < n_total) {
+      int lr;
+      const int t = target_of(lR, lr);
+      lrow = (const uint8_t*)tg.w[t] + (int64_t)lr * rowbytes;
     }
     const int s0 = lsp * kSpanSb;
-    load_span(sp, lrow + (int64_t)s0 * 210, nsb - s0 < kSpanSb ? nsb - s0 : kSpanSb, lane);
+    if (lR < n_total)
+      load_span(sp, lrow + (int64_t)s0 * 210, nsb - s0 < kSpanSb ? nsb - s0 : kSpanSb, lane);
+    else
+      load_span(sp, idle, 1, lane);
     if (++lsp == nspan) {
       lsp = 0;
       lR += W;
@@ -124,8 +141,7 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
   act.load(nsb, x, xstride, yq, yd, ybs);
   Span ring[kPfd];
 #pragma unroll
-  for (int j = 0; j < kPfd; j++)
-    if (j < S) load_next(ring[j]);
+  for (int j = 0; j < kPfd; j++) load_next(ring[j]);
 
   // 2. the activation into LDS
   act.store(s, nsb, x, xstride, yq, yd, ybs, qmax);
@@ -133,25 +149,25 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
 
   // 3. the spans, in order
   const int sbl = lane >> 2, u = lane & 3, h = u >> 1, l0 = 16 * (u & 1);
-  int64_t R = gw;  // the span being computed: span sp of row R
+  int R = gw;  // the span being computed: span sp of row R
   int sp = 0;
-  float* out = nullptr;
-  int64_t ldd = 0;
   float tot[NR];
 #pragma unroll
   for (int r = 0; r < NR; r++) tot[r] = 0.0f;
 
-  auto step = [&](Span& cur, int64_t sigma) {
-    if (sp == 0) (void)row_ptr(R, out, ldd);
+  auto step = [&](Span& cur, int sigma) {
     // the span into this wave's LDS buffer (the previous span's reads are done)
     wave_lds_sync();
 #pragma unroll
-    for (int c = 0; c < kPiecesPerLane; c++)
-      if (lane + 64 * c < kSpanPieces) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
+    for (int c = 0; c < kPiecesPerLane; c++) {
+      const int pc = lane + 64 * c;
+      *(uint4*)(buf + 16 * (pc < kSpanPieces ? pc : kSpanPieces - 1)) = cur.p[c];
+    }
     wave_lds_sync();
     const int off = cur.off, len = cur.len;
     // this buffer's next span
-    if (sigma + kPfd < S) load_next(cur);
+    load_next(cur);
+    if (sigma >= S) return;
     float acc[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) acc[r] = 0.0f;
@@ -191,29 +207,32 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
     }
     if (++sp == nspan) {
       if (lane == 0) {
+        int lr;
+        const int t = target_of(R, lr);
+        float* out = tg.dst[t] + lr;
 #pragma unroll
-        for (int r = 0; r < NR; r++) out[r * ldd] = tot[r];
+        for (int r = 0; r < NR; r++) out[r * tg.ldd[t]] = tot[r];
       }
       sp = 0;
       R += W;
     }
   };
 
-  for (int64_t sigma = 0; sigma < S; sigma += kPfd) {
+  for (int sigma = 0; sigma < S; sigma += kPfd) {
 #pragma unroll
-    for (int j = 0; j < kPfd; j++)
-      if (sigma + j < S) step(ring[j], sigma + j);
+    for (int j = 0; j < kPfd; j++) step(ring[j], sigma + j);
   }
 }
 
-// one workgroup of 16 waves a CU (up to 128 registers a lane, kPfd spans in
-// flight), a wave a row where the rows are few
+// one workgroup of 16 waves a CU (up to 128 registers a lane), a wave a row
+// where the rows are few
 template <int NR>
 hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
                          float qmax, int cus, hipStream_t st) {
   const int64_t n_total = t.row_end[t.count - 1];
-  int64_t waves = (int64_t)cus * 16;
-  if (waves > n_total) waves = (n_total + 15) / 16 * 16;
+  if (n_total >= ((int64_t)1 << 30)) return hipErrorInvalidValue;  // row numbers are ints in the kernel
+  int waves = cus * 16;
+  if (waves > n_total) waves = (int)((n_total + 15) / 16 * 16);
   const size_t lds = (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + 16 * (size_t)kSpanBuf;
   const dim3 grid((unsigned)(waves / 16));
   if (pre) {
