@@ -111,8 +111,12 @@ struct ActRegs {
   int32_t p0[T], p1[T];
 };
 
+// Rows of up to 4096 values (T == 1) hold 8 waves a SIMD (two 16-wave
+// workgroups a CU, 64 registers a lane): the grid of the largest products
+// (gate+up) is sized for that.
 template <int NR, int T, bool FUSED, int kWaves, bool PF, bool XCHG>
-__global__ __launch_bounds__(64 * kWaves) void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(T == 1 && NR == 1 ? 8 : 1)))
+void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
                                                             int64_t xstride, const int8_t* __restrict__ yq,
                                                             const float* __restrict__ yd,
                                                             const int16_t* __restrict__ ybs, float qmax) {

@@ -122,12 +122,15 @@ bool stream_supported(int type, int64_t k, int64_t rows) {
   return false;
 }
 
-// Launch shape of the Q4_K decode kernel for n_total weight rows: up to 32
-// waves per CU, about 1.5 rows per wave where the rows are few, 16-wave
-// workgroups (one activation fill per 16 waves), the next row's loads in
-// flight whenever a wave has more than one row.
+// Launch shape of the Q4_K decode kernel for n_total weight rows, in 16-wave
+// workgroups (one activation fill per 16 waves): a row per wave up to 16
+// waves a CU; beyond that, about 1.5 rows per wave up to 32 waves a CU, the
+// next row's loads in flight whenever a wave has more than one row.
 qmm::MvShape stream_shape(int64_t n_total) {
   const int64_t cus = cu_count();
+  // a row per wave while the rows fit one 16-wave workgroup a CU (o, 4096
+  // rows: 5.5 us against 6.2 us for 2736 waves with the next row in flight)
+  if (n_total <= cus * 16) return qmm::MvShape{(n_total + 15) / 16 * 16, 16, false};
   int64_t waves = n_total * 2 / 3;
   if (waves < 1024) waves = 1024;
   if (waves > cus * 32) waves = cus * 32;

@@ -146,123 +146,135 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // ---- activation quantizer -------------------------------------------------
-// Q8_K (BlockQ8K::from_float, k_quants.rs:2882-2927) of one 256-value block
-// held by a group of 16 lanes (gl = lane within the group, 0..15), lane gl
-// holding values 16gl..16gl+15 in v[0..15]. The block's scale value is the
-// signed value of the FIRST element of largest |x| (strict <), found in one
-// 4-step reduction as the maximum of the key
-// (|x| bits, 0xFFFF - index, sign): |x| orders as its bits (NaN never
-// qualifies, as `amax < |x|` is false for it), the lower index wins a tie,
-// and the sign rides along. Returns the lane's 16 codes packed in c[0..3],
-// their sum (the reference's bsums entry gl) and d. All 64 lanes must call.
+// One Q8_K code (BlockQ8K::from_float, k_quants.rs:2917-2920): the reference
+// computes t = iscale * x, then t.round() (half away from zero), .min(127.)
+// (which gives 127 for NaN) and `as i8` (saturating). For every float t that
+// equals trunc(clamp(t + copysign(0.49999997, t), -128.49, 127.49)): adding
+// the float just below one half reaches the next integer exactly when t is at
+// or above the tie (round to nearest even resolves the one boundary case,
+// 0.49999997 + 0.5, upwards), and the clamp, taken with min first, sends NaN
+// to 127 and the infinities (a denormal block maximum can make iscale
+// infinite) to the saturated codes. Checked against the reference's steps for
+// all 2^32 floats (tests/test_q8k_rounding.py restates the check on the
+// half-integer neighbourhoods). Four instructions and the conversion.
+__device__ __forceinline__ int32_t q8k_code(float t) {
+#pragma clang fp contract(off)
+  const float s = t + __builtin_copysignf(0.49999997f, t);
+  return (int32_t)fmaxf(fminf(s, 127.49f), -128.49f);
+}
+
+// 4 codes (each in -128..127) packed one per byte, code 0 in the low byte.
+__device__ __forceinline__ uint32_t pack4_i8(int32_t a, int32_t b, int32_t c, int32_t d) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0C0C0400u);  // a.b0, b.b0, 0, 0
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000C0Cu);  // 0, 0, c.b0, d.b0
+  return lo | hi;
+}
+
+// Maximum over the lane's row of 16 (DPP: pairs, pairs of pairs, then the
+// mirrored halves and rows); every lane of the row gets the result.
+template <int CTL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint32_t row16_maxu(uint32_t k) {
+  k = max(k, dpp_u<0xB1>(k));
+  k = max(k, dpp_u<0x4E>(k));
+  k = max(k, dpp_u<0x141>(k));
+  return max(k, dpp_u<0x140>(k));
+}
+
+// The reference's block scale value is the signed value of the FIRST element
+// of largest |x| (strict <; NaN never qualifies, as `amax < |x|` is false for
+// it). With p the largest of 0 and the values and m the largest of 0 and the
+// negated values (fmaxf ignores NaN, so neither is NaN and both are >= 0,
+// ordered as their bits), |max| = max(p, m) and its sign is p's or n's unless
+// p == m != 0, where both signs reach it and the first such element decides:
+// that rare case takes the maximum of the key (0xFFFF - index, sign), the
+// lowest index. The key's base is made opaque inside the branch so that the
+// compiler does not keep the per-value keys live outside it.
+
+// Q8_K of one 256-value block held by a group of 16 lanes (gl = lane within
+// the group, 0..15), lane gl holding values 16gl..16gl+15 in v[0..15].
+// Returns the lane's 16 codes packed in c[0..3], their sum (the reference's
+// bsums entry gl) and d. All 64 lanes must call.
 __device__ __forceinline__ void q8k_block_group16(const float v[16], int gl, float qmax, uint32_t c[4],
                                                   int32_t& sum16, float& d) {
 #pragma clang fp contract(off)
-  float amax = 0.0f;
-  int first = 0;
+  float p = 0.0f, m = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; i++) {
-    const float a = fabsf(v[i]);
-    if (amax < a) { amax = a; first = i; }
+    p = fmaxf(p, v[i]);
+    m = fmaxf(m, -v[i]);
   }
-  uint32_t hi = __float_as_uint(amax);
-  uint32_t lo = amax != 0.0f
-                    ? ((uint32_t)(0xFFFF - (16 * gl + first)) << 1) | (__float_as_uint(v[first]) >> 31)
-                    : 0u;
-  // the largest (hi, lo) of the 16 lanes, through DPP within the lane's row
-  // of 16 (pairs, pairs of pairs, then the mirrored quads and halves): a
-  // maximum, so the order does not matter
-#pragma unroll
-  for (int step = 0; step < 4; step++) {
-    uint32_t ohi, olo;
-    if (step == 0) {
-      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0xB1, 0xF, 0xF, true);  // quad 1,0,3,2
-      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0xB1, 0xF, 0xF, true);
-    } else if (step == 1) {
-      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x4E, 0xF, 0xF, true);  // quad 2,3,0,1
-      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x4E, 0xF, 0xF, true);
-    } else if (step == 2) {
-      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x141, 0xF, 0xF, true);  // half mirror
-      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x141, 0xF, 0xF, true);
-    } else {
-      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x140, 0xF, 0xF, true);  // mirror
-      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x140, 0xF, 0xF, true);
-    }
-    if (ohi > hi || (ohi == hi && olo > lo)) { hi = ohi; lo = olo; }
-  }
-  amax = __uint_as_float(hi);
+  const uint32_t pb = row16_maxu(__float_as_uint(p)), mb = row16_maxu(__float_as_uint(m));
+  const float amax = __uint_as_float(max(pb, mb));
   sum16 = 0;
   d = 0.0f;
   c[0] = c[1] = c[2] = c[3] = 0u;
   if (amax != 0.0f) {
-    const float mx = (lo & 1u) ? -amax : amax;
+    float mx = pb > mb ? amax : -amax;
+    if (pb == mb) {
+      uint32_t base = (uint32_t)(0xFFFF - 16 * gl) << 1;
+      asm volatile("" : "+v"(base));
+      uint32_t key = 0;
+#pragma unroll
+      for (int i = 15; i >= 0; i--)
+        if (fabsf(v[i]) == amax) key = (base - 2u * (uint32_t)i) | (__float_as_uint(v[i]) >> 31);
+      key = row16_maxu(key);
+      mx = (key & 1u) ? -amax : amax;
+    }
     const float iscale = -qmax / mx;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int q = rs_as_i8(rs_min(roundf(iscale * v[i]), 127.0f));
-      c[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
-      sum16 += q;
+    for (int w = 0; w < 4; w++) {
+      int32_t q[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) q[e] = q8k_code(iscale * v[4 * w + e]);
+      c[w] = pack4_i8(q[0], q[1], q[2], q[3]);
+      sum16 = __builtin_amdgcn_sdot4((int)c[w], 0x01010101, sum16, false);
     }
     d = 1.0f / iscale;
   }
 }
 
 // The same Q8_K block held by a whole wave: lane L holds values 4L..4L+3 in
-// v[0..3]. The key's maximum is taken within each row of 16 lanes (DPP), then
-// over the four rows (readlane, uniform). Returns the lane's 4 codes packed
-// in c, the sum of the 16 values of the lane's quad (lanes 4g..4g+3: the
+// v[0..3]. The maxima are taken within each row of 16 lanes (DPP), then over
+// the four rows (readlane, uniform). Returns the lane's 4 codes packed in c,
+// the sum of the 16 values of the lane's quad (lanes 4g..4g+3: the
 // reference's bsums entry g) in sum16, and d. All 64 lanes must call.
 __device__ __forceinline__ void q8k_block_wave(const float v[4], int lane, float qmax, uint32_t& c, int32_t& sum16,
                                                float& d) {
 #pragma clang fp contract(off)
-  float amax = 0.0f;
-  int first = 0;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float a = fabsf(v[i]);
-    if (amax < a) { amax = a; first = i; }
-  }
-  uint32_t hi = __float_as_uint(amax);
-  uint32_t lo = amax != 0.0f ? ((uint32_t)(0xFFFF - (4 * lane + first)) << 1) | (__float_as_uint(v[first]) >> 31)
-                             : 0u;
-#pragma unroll
-  for (int step = 0; step < 4; step++) {
-    uint32_t ohi, olo;
-    if (step == 0) {
-      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0xB1, 0xF, 0xF, true);
-      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0xB1, 0xF, 0xF, true);
-    } else if (step == 1) {
-      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x4E, 0xF, 0xF, true);
-      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x4E, 0xF, 0xF, true);
-    } else if (step == 2) {
-      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x141, 0xF, 0xF, true);
-      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x141, 0xF, 0xF, true);
-    } else {
-      ohi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x140, 0xF, 0xF, true);
-      olo = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x140, 0xF, 0xF, true);
-    }
-    if (ohi > hi || (ohi == hi && olo > lo)) { hi = ohi; lo = olo; }
-  }
-  uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)hi, 0), bl = (uint32_t)__builtin_amdgcn_readlane((int)lo, 0);
+  const float p = fmaxf(fmaxf(0.0f, v[0]), fmaxf(v[1], fmaxf(v[2], v[3])));
+  const float m = fmaxf(fmaxf(0.0f, -v[0]), fmaxf(-v[1], fmaxf(-v[2], -v[3])));
+  uint32_t pr = row16_maxu(__float_as_uint(p)), mr = row16_maxu(__float_as_uint(m));
+  uint32_t pb = (uint32_t)__builtin_amdgcn_readlane((int)pr, 0), mb = (uint32_t)__builtin_amdgcn_readlane((int)mr, 0);
 #pragma unroll
   for (int r = 1; r < 4; r++) {
-    const uint32_t oh = (uint32_t)__builtin_amdgcn_readlane((int)hi, 16 * r);
-    const uint32_t ol = (uint32_t)__builtin_amdgcn_readlane((int)lo, 16 * r);
-    if (oh > bh || (oh == bh && ol > bl)) { bh = oh; bl = ol; }
+    pb = max(pb, (uint32_t)__builtin_amdgcn_readlane((int)pr, 16 * r));
+    mb = max(mb, (uint32_t)__builtin_amdgcn_readlane((int)mr, 16 * r));
   }
-  amax = __uint_as_float(bh);
+  const float amax = __uint_as_float(max(pb, mb));
   c = 0u;
   int32_t s = 0;
   d = 0.0f;
   if (amax != 0.0f) {
-    const float mx = (bl & 1u) ? -amax : amax;
-    const float iscale = -qmax / mx;
+    float mx = pb > mb ? amax : -amax;
+    if (pb == mb) {
+      uint32_t base = (uint32_t)(0xFFFF - 4 * lane) << 1;
+      asm volatile("" : "+v"(base));
+      uint32_t key = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int q = rs_as_i8(rs_min(roundf(iscale * v[i]), 127.0f));
-      c |= (uint32_t)(q & 0xFF) << (8 * i);
-      s += q;
+      for (int i = 3; i >= 0; i--)
+        if (fabsf(v[i]) == amax) key = (base - 2u * (uint32_t)i) | (__float_as_uint(v[i]) >> 31);
+      key = row16_maxu(key);
+      uint32_t kb = (uint32_t)__builtin_amdgcn_readlane((int)key, 0);
+#pragma unroll
+      for (int r = 1; r < 4; r++) kb = max(kb, (uint32_t)__builtin_amdgcn_readlane((int)key, 16 * r));
+      mx = (kb & 1u) ? -amax : amax;
     }
+    const float iscale = -qmax / mx;
+    c = pack4_i8(q8k_code(iscale * v[0]), q8k_code(iscale * v[1]), q8k_code(iscale * v[2]), q8k_code(iscale * v[3]));
+    s = __builtin_amdgcn_sdot4((int)c, 0x01010101, 0, false);
     d = 1.0f / iscale;
   }
   s += __builtin_amdgcn_mov_dpp(s, 0xB1, 0xF, 0xF, true);

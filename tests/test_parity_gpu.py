@@ -58,6 +58,12 @@ def act_inputs(k: int, rows: int, seed: int) -> np.ndarray:
 def test_q8k_activation_bit_exact(k, rows):
     x = act_inputs(k, rows, 1)
     x[-1, 7] = np.nan  # a NaN is never the block's largest; it codes as 127
+    if k >= 768:
+        # +inf and -inf both reach the block's |max|: the first decides the
+        # sign; iscale is then -0, so inf * iscale is NaN (code 127) and d -inf
+        x[-1, 256 + 3] = np.inf
+        x[-1, 256 + 9] = -np.inf
+        x[-1, 512 + 5] = -np.inf
     buf = quantize_act(upload(x), _lib.ACT_Q8K)
     codes, scales, sums = (t.cpu().numpy() for t in act_planes(buf, _lib.ACT_Q8K, k, rows))
     for r in range(rows):
