@@ -32,9 +32,10 @@
 //     global-to-LDS loads (global_load_lds_dwordx4), one super-block ahead
 //     into the other half of a double buffer. Activation rows' 16-byte
 //     pieces are XOR-swizzled by row so the MFMA reads are conflict-free;
-//     weight bytes are stored as 9 planes of 16-byte pieces (plane j = piece
-//     j of every row), so each copy moves one piece of 64 rows and a lane's
-//     reads of consecutive rows are consecutive.
+//     weight rows are stored one after another (144 bytes each), each copy
+//     moving about 7 rows' contiguous bytes. (Copies of one 16-byte piece of
+//     64 rows, 2304 bytes apart, touch 64 cache lines each and made the
+//     kernel twice as slow on C3.)
 //   - Each lane reads its weight row's header and the 16 code bytes
 //     32j + 16(lane/32) of each 32-byte chunk j — exactly its MFMA B-operand
 //     bytes for sub-blocks 2j (low nibbles) and 2j+1 (high nibbles) — and
@@ -59,6 +60,32 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int BM = 128;  // rows of a workgroup tile
+
+// One global-to-LDS copy of 16 bytes a lane (global_load_lds_dwordx4): lane
+// L's 16 bytes at base + off[L] land at LDS byte lds + 16 L (lds uniform,
+// through M0, which is restored). Written as inline assembly: the compiler
+// counts its own form of this load among the LDS operations, in a way it
+// cannot order against them, and then waits for every LDS read with
+// lgkmcnt(0) for the rest of the super-block (the A fragments read a step
+// ahead were waited for at once). The kernel waits for the copies itself
+// (vmcnt(0) before the barrier that ends the super-block); the copies write
+// only the buffer half no wave reads until then.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off), "s"(base), "s"(lds)
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
 
 __device__ __forceinline__ uint32_t dup16(uint32_t v) { return v | (v << 16); }
 
@@ -109,12 +136,13 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
   const uint32_t rowbytes = (uint32_t)nsb * 144;
   const int h = lane >> 5, r32 = lane & 31;
 
-  // Weight copies: the tile is stored as 9 planes, plane j holding 16-byte
-  // piece j of every row (piece 0 the header, pieces 1-8 the codes). Copy
-  // i = wv + kWaves u moves plane i % 9 of rows 64 (i / 9) .. +63, lane L row
-  // 64 (i / 9) + L (rows past N read the last row). Byte offsets from W: the
-  // host keeps N * rowbytes below 2^31.
-  const uint32_t wlane = (uint32_t)(n0 + lane) * rowbytes;
+  // Weight copies: the tile is stored row by row, 144 bytes a row (9 pieces
+  // of 16 bytes: piece 0 the header, pieces 1-8 the codes). Copy i = wv +
+  // kWaves u moves pieces 64 i .. 64 i + 63 of the tile, lane L piece
+  // f = 64 i + L, row f / 9, piece f % 9: each copy reads about 7 rows'
+  // contiguous 144 bytes (a row of the tile per 9 lanes) rather than 16 bytes
+  // of 64 rows. Rows past N read the last row. Byte offsets from W: the host
+  // keeps N * rowbytes below 2^31.
   const uint32_t wlast = (uint32_t)(N - 1) * rowbytes;
   // Activation copies: copy i moves rows 4i .. 4i+3 of the tile; lane L
   // writes row 4i + L/16 at piece position L%16, which holds code piece
@@ -126,16 +154,17 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
   const uint32_t kstep4 = (uint32_t)(4 * K);
 
   auto issue = [&](int sb, uint8_t* sw, int8_t* sa) {
-    uint32_t wl0 = wlane;
-    asm volatile("" : "+v"(wl0));  // the offsets are recomputed per super-block, not held across it
+    uint32_t lane0 = (uint32_t)lane;
+    asm volatile("" : "+v"(lane0));  // the offsets are recomputed per super-block, not held across it
 #pragma unroll
-    for (int u = 0; u < 5; u++) {
+    for (int u = 0; u < (kWInstr + kWaves - 1) / kWaves; u++) {
       const int i = wv + kWaves * u;
       if (i < kWInstr) {
-        const int g = i / 9, j = i % 9;
-        const uint32_t row = wl0 + (uint32_t)(64 * g) * rowbytes;
-        const uint32_t off = (row < wlast ? row : wlast) + 16u * (uint32_t)j + 144u * (uint32_t)sb;
-        __builtin_amdgcn_global_load_lds((const void*)(W + off), (lds_void*)(sw + j * (BN * 16) + g * 1024), 16, 0, 0);
+        const uint32_t f = 64u * (uint32_t)i + lane0;
+        const uint32_t r = (f * 7282u) >> 16;  // f / 9 for f < 2^14
+        const uint32_t row = (uint32_t)(n0 + r) * rowbytes;
+        const uint32_t off = (row < wlast ? row : wlast) + 16u * (f - 9u * r) + 144u * (uint32_t)sb;
+        dma16(W, off, lds_addr(sw + 1024 * i));
       }
     }
 #pragma unroll
@@ -143,7 +172,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
       const int i = wv + kWaves * u;
       const uint32_t row = arow0 + (uint32_t)(4 * i) * (kstep4 / 4);
       const uint32_t off = (row < alast ? row : alast) + 16u * (lp ^ (4u * (uint32_t)(i & 3) + lq)) + 256u * (uint32_t)sb;
-      __builtin_amdgcn_global_load_lds((const void*)(yq + off), (lds_void*)(sa + 1024 * i), 16, 0, 0);
+      dma16(yq, off, lds_addr(sa + 1024 * i));
     }
   };
 
@@ -220,7 +249,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
   };
   i16v c[4];
 
-  const int wrow_lds = (32 * wv + r32) * 16;  // this lane's weight row in each plane
+  const int wrow_lds = (32 * wv + r32) * 144;  // this lane's weight row in the tile
   // one super-block from buffer half (sw, sa, samin, sdyl), the next one's
   // copies into the other half
   auto step = [&](int sb, const uint8_t* sw, const int8_t* sa, uint8_t* nw, int8_t* na) {
@@ -232,13 +261,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
 
     WRaw cur;
     {
+      // rows 144 bytes (36 dwords) apart: the 16-byte reads of 16 lanes
+      // cover the 64 banks once
       const uint8_t* wl = sw + wrow_lds;
-      constexpr int P = BN * 16;  // bytes of a plane
       cur.hdr = *(const uint4*)wl;
-      cur.c0 = *(const uint4*)(wl + (1 + h) * P);
-      cur.c1 = *(const uint4*)(wl + (3 + h) * P);
-      cur.c2 = *(const uint4*)(wl + (5 + h) * P);
-      cur.c3 = *(const uint4*)(wl + (7 + h) * P);
+      cur.c0 = *(const uint4*)(wl + 16 * (1 + h));
+      cur.c1 = *(const uint4*)(wl + 16 * (3 + h));
+      cur.c2 = *(const uint4*)(wl + 16 * (5 + h));
+      cur.c3 = *(const uint4*)(wl + 16 * (7 + h));
     }
     // this row's scales and mins (get_scale_min_k4, utils.rs:50-60)
     const uint32_t u0 = cur.hdr.y, u1 = cur.hdr.z, u2 = cur.hdr.w;
