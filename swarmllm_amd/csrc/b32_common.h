@@ -13,7 +13,13 @@ __device__ __forceinline__ int32_t lut16(uint32_t n, uint32_t t0, uint32_t t1, u
   const uint32_t sel = n & 0x07070707u;
   const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
   const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
-  const uint32_t m = ((n >> 3) & 0x01010101u) * 0xFFu;
+  // bit 3 of each nibble spread over its byte: t * 255 as (t << 8) - t, two
+  // full-rate instructions where the 32-bit multiply runs at quarter rate
+  // (the empty asm keeps the compiler from folding them back into it)
+  const uint32_t t = (n >> 3) & 0x01010101u;
+  uint32_t t8 = t << 8;
+  asm("" : "+v"(t8));
+  const uint32_t m = t8 - t;
   return (int32_t)((hi & m) | (lo & ~m));
 }
 

@@ -172,19 +172,26 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_b32_kernel(
 // row and the wave reduction are those of the 1-2 row decode kernel
 // (mv_b32s.hip), so each entry's result is bit-identical to qmm_forward of
 // its input row, times its scale.
-constexpr int kMoeSWaves = 16;
+constexpr int kMoeSWaves = 8;  // two workgroups a CU: one streams while the other starts
+constexpr int kMoeRing = 2;        // spans in flight per wave
+constexpr int kMoeActLoads = 4;    // 16-byte activation pieces a lane copies (k <= 4096; cv0..cv3)
+constexpr int kMoeScaleLoads = 2;  // and block scales (cd0, cd1)
+static_assert(kMoeSWaves == kMoePairs, "a wave copies each entry's activation row");
 
 template <int FMT>
 struct MoeSpan {
   static constexpr int kPieces = (15 + 128 * Fmt32<FMT>::B + 15) / 16;
   static constexpr int kLoads = (kPieces + 63) / 64;
+  // a wave's LDS staging buffer: the pieces and the bytes the block reads
+  // may touch past the last
+  static constexpr int kStage = kPieces * 16 + 16;
   uint4 p[kLoads];
   int off;
   int len;
 };
 
 template <int FMT>
-__global__ __launch_bounds__(64 * kMoeSWaves) void moe_b32s_kernel(
+__global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu(4))) void moe_b32s_kernel(
     const uint8_t* __restrict__ W, int64_t n, int nb, int64_t estride, int num_experts,
     const int8_t* __restrict__ yq, const float* __restrict__ yd, const int32_t* __restrict__ runs,
     const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int topk, int size_m,
@@ -196,14 +203,17 @@ __global__ __launch_bounds__(64 * kMoeSWaves) void moe_b32s_kernel(
   int8_t* const acodes = (int8_t*)smem;                          // [kMoePairs][k]
   float* const ad = (float*)(smem + (size_t)kMoePairs * k);      // [kMoePairs][nb]
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* const buf = smem + ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)wv * kStageBytes;
+  uint8_t* const buf = smem + ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)wv * Span::kStage;
 
-  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  // The run: its count and its (first entry, length, expert) are read
+  // together (the runs buffer holds 1 + 3 size_m ints and run < gridDim.y <=
+  // size_m); each lookup below is one batch of independent scalar loads.
   const int run = blockIdx.y;
-  if (run >= nruns) return;  // the whole workgroup: before any barrier
+  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
   const int start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
   const int len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
   const int e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+  if (run >= nruns) return;  // the whole workgroup: before any barrier
   if (e < 0 || e >= num_experts) return;
   const uint8_t* We = W + (int64_t)e * estride;
   const int64_t rb = (int64_t)nb * F::B;
@@ -217,36 +227,19 @@ __global__ __launch_bounds__(64 * kMoeSWaves) void moe_b32s_kernel(
 
   for (int c0 = 0; c0 < len; c0 += kMoePairs) {
     const int cnt = len - c0 < kMoePairs ? len - c0 : kMoePairs;
-    int64_t out_row[kMoePairs];
-    float scale[kMoePairs];
-    bool use[kMoePairs];
-    int64_t in_row[kMoePairs];
-#pragma unroll
-    for (int p = 0; p < kMoePairs; p++) {
-      const int pair = p < cnt ? __builtin_amdgcn_readfirstlane(ids[start + c0 + p]) : -1;
-      use[p] = pair >= 0 && pair < size_m;
-      out_row[p] = use[p] ? pair : 0;
-      in_row[p] = use[p] ? (topk_w ? pair : pair / topk) : 0;
-      scale[p] = use[p] && topk_w ? topk_w[pair] : 1.0f;
-    }
-    // the chunk's activation rows into LDS (after the previous chunk's reads)
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < kMoePairs; p++) {
-      if (!use[p]) continue;
-      for (int i = (int)threadIdx.x; i < k / 16; i += 64 * kMoeSWaves)
-        *(uint4*)(acodes + p * k + 16 * i) = *(const uint4*)(yq + in_row[p] * k + 16 * i);
-      for (int i = (int)threadIdx.x; i < nb; i += 64 * kMoeSWaves) ad[p * nb + i] = yd[in_row[p] * nb + i];
-    }
-    __syncthreads();
-
-    // stream the wave's rows
+    // The wave's weight rows: the loads run kMoeRing spans ahead of the
+    // arithmetic; past the wave's last span they read the first bytes of the
+    // quantized activation (cached, never used). Every step issues one span's
+    // loads and writes all of its pieces, so the compiler counts the loads
+    // in flight exactly and waits for the oldest span only. The first spans
+    // go out before the entries are looked up.
     int64_t lr = r0;
     int lsp = 0;
     auto load_next = [&](Span& sp) {
+      const bool real = lr < r0 + nrows;
       const int b0 = lsp * 128;
-      const int blen = nb - b0 < 128 ? nb - b0 : 128;
-      const uint8_t* pp = We + lr * rb + (int64_t)b0 * F::B;
+      const int blen = real ? (nb - b0 < 128 ? nb - b0 : 128) : 1;
+      const uint8_t* pp = real ? We + lr * rb + (int64_t)b0 * F::B : (const uint8_t*)yq;
       sp.off = (int)((uintptr_t)pp & 15);
       sp.len = blen;
       const uint8_t* a0 = pp - sp.off;
@@ -261,9 +254,66 @@ __global__ __launch_bounds__(64 * kMoeSWaves) void moe_b32s_kernel(
         lr++;
       }
     };
-    Span sa, sb;
-    if (S > 0) load_next(sa);
-    if (S > 1) load_next(sb);
+    Span ring[kMoeRing];
+#pragma unroll
+    for (int j = 0; j < kMoeRing; j++) load_next(ring[j]);
+
+    // the chunk's entries: their pair indices (indices clamped into the run),
+    // then their routing weights, each one batch
+    int pr[kMoePairs];
+#pragma unroll
+    for (int p = 0; p < kMoePairs; p++) pr[p] = __builtin_amdgcn_readfirstlane(ids[start + c0 + (p < cnt ? p : cnt - 1)]);
+    int64_t out_row[kMoePairs];
+    float scale[kMoePairs];
+    bool use[kMoePairs];
+    int64_t in_row[kMoePairs];
+#pragma unroll
+    for (int p = 0; p < kMoePairs; p++) {
+      use[p] = p < cnt && pr[p] >= 0 && pr[p] < size_m;
+      out_row[p] = use[p] ? pr[p] : 0;
+      in_row[p] = use[p] ? (topk_w ? pr[p] : pr[p] / topk) : 0;
+    }
+#pragma unroll
+    for (int p = 0; p < kMoePairs; p++) scale[p] = topk_w ? topk_w[use[p] ? pr[p] : 0] : 1.0f;
+    // The chunk's activation rows into LDS (after the previous chunk's
+    // reads): entry p is copied by wave p, each lane loading a fixed number
+    // of 16-byte code pieces and scales (addresses clamped to the row;
+    // k <= 4096, the launcher checks).
+    __syncthreads();
+    const int cp = wv;  // the entry this wave copies (uniform)
+    const int ct = lane;
+    const bool cuse = cp < kMoePairs && use[cp < kMoePairs ? cp : 0];
+    const int8_t* crow = yq + (cuse ? in_row[cp] * k : 0);
+    const float* cdrow = yd + (cuse ? in_row[cp] * nb : 0);
+    const int npc = k / 16;
+    auto ld_piece = [&](int j) {
+      const int i = ct + 64 * j;
+      return *(const uint4*)(crow + 16 * (i < npc ? i : npc - 1));
+    };
+    auto ld_scale = [&](int j) {
+      const int i = ct + 64 * j;
+      return cdrow[i < nb ? i : nb - 1];
+    };
+    // named registers (an array here was kept in scratch memory)
+    const uint4 cv0 = ld_piece(0), cv1 = ld_piece(1), cv2 = ld_piece(2), cv3 = ld_piece(3);
+    const float cd0 = ld_scale(0), cd1 = ld_scale(1);
+    if (cuse) {
+      auto st_piece = [&](int j, const uint4& v) {
+        const int i = ct + 64 * j;
+        if (i < npc) *(uint4*)(acodes + cp * k + 16 * i) = v;
+      };
+      auto st_scale = [&](int j, float v) {
+        const int i = ct + 64 * j;
+        if (i < nb) ad[cp * nb + i] = v;
+      };
+      st_piece(0, cv0);
+      st_piece(1, cv1);
+      st_piece(2, cv2);
+      st_piece(3, cv3);
+      st_scale(0, cd0);
+      st_scale(1, cd1);
+    }
+    __syncthreads();
     int64_t R = r0;
     int sp = 0;
     float acc[kMoePairs];
@@ -272,11 +322,14 @@ __global__ __launch_bounds__(64 * kMoeSWaves) void moe_b32s_kernel(
     auto step = [&](Span& cur, int64_t sigma) {
       wave_lds_sync();
 #pragma unroll
-      for (int c = 0; c < Span::kLoads; c++)
-        if (lane + 64 * c < Span::kPieces) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
+      for (int c = 0; c < Span::kLoads; c++) {
+        const int pc = lane + 64 * c;
+        *(uint4*)(buf + 16 * (pc < Span::kPieces ? pc : Span::kPieces - 1)) = cur.p[c];
+      }
       wave_lds_sync();
       const int off = cur.off, blen = cur.len;
-      if (sigma + 2 < S) load_next(cur);
+      load_next(cur);
+      if (sigma >= S) return;
       if (bl < blen) {
         const bool two = bl + 1 < blen;
         uint32_t q0[8], q1[8];
@@ -324,9 +377,9 @@ __global__ __launch_bounds__(64 * kMoeSWaves) void moe_b32s_kernel(
         R++;
       }
     };
-    for (int64_t sigma = 0; sigma < S; sigma += 2) {
-      step(sa, sigma);
-      if (sigma + 1 < S) step(sb, sigma + 1);
+    for (int64_t sigma = 0; sigma < S; sigma += kMoeRing) {
+#pragma unroll
+      for (int j = 0; j < kMoeRing; j++) step(ring[j], sigma + j);
     }
   }
 }
@@ -345,7 +398,7 @@ hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, co
   const int64_t rpw = 8;
   const int64_t rows_per_wg = (int64_t)kMoeSWaves * rpw;
   const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
-  const size_t lds = ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)kMoeSWaves * kStageBytes;
+  const size_t lds = ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)kMoeSWaves * MoeSpan<FMT>::kStage;
   auto* kfn = &moe_b32s_kernel<FMT>;
   if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
   kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
@@ -356,7 +409,8 @@ hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, co
 // The streaming form's LDS: the chunk's activation rows and the waves' stage buffers.
 inline bool moe_stream_fits(int64_t k) {
   const int64_t nb = k / 32;
-  return ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)kMoeSWaves * kStageBytes <= 160 * 1024;
+  return k / 16 <= 64 * kMoeActLoads && nb <= 64 * kMoeScaleLoads &&
+         ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)kMoeSWaves * kStageBytes <= 160 * 1024;
 }
 
 template <int FMT>
