@@ -120,11 +120,13 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q4k_skinny_kernel(MvTargets 
 #pragma unroll
     for (int t = 0; t < L; t++) pc.v[t] = ld_stream16(src[t] + (int64_t)sb * 144);
   };
+  // every lane writes (lanes past the pieces rewrite the last piece, which
+  // they loaded too): no branch, so the loads' wait counts stay exact
   auto stage_w = [&](const Pieces& pc) {
 #pragma unroll
     for (int t = 0; t < L; t++) {
       const int p = lane + 64 * t;
-      if (p < Pieces::P) *(uint4*)(buf + 16 * p) = pc.v[t];
+      *(uint4*)(buf + 16 * (p < Pieces::P ? p : Pieces::P - 1)) = pc.v[t];
     }
   };
 
@@ -222,7 +224,10 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q4k_skinny_kernel(MvTargets 
 
   // the loop, unrolled by two so the register buffers keep their registers:
   // stage super-block sb, reload its registers with sb + 2, load the
-  // activation of sb + 1, compute sb
+  // activation of sb + 1, compute sb. The main loop runs while both of its
+  // steps have all their loads, which it then issues unconditionally (a load
+  // issued on one path and not another makes the compiler wait for every
+  // load in flight); the last steps follow it, loading only what remains.
   Pieces pa, pb;
   SkAct<MT> aa, ab;
   if (sb0 < sb1) {
@@ -230,18 +235,30 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q4k_skinny_kernel(MvTargets 
     if (sb0 + 1 < sb1) load_w(pb, sb0 + 1);
     load_a(aa, sb0);
   }
-  auto step = [&](Pieces& pc, SkAct<MT>& cur, SkAct<MT>& nxt, int sb) {
+  auto step_full = [&](Pieces& pc, SkAct<MT>& cur, SkAct<MT>& nxt, int sb) {
     wave_lds_sync();  // the previous super-block's reads are done
+    stage_w(pc);
+    load_w(pc, sb + 2);
+    load_a(nxt, sb + 1);
+    wave_lds_sync();
+    compute(cur);
+  };
+  auto step_tail = [&](Pieces& pc, SkAct<MT>& cur, SkAct<MT>& nxt, int sb) {
+    wave_lds_sync();
     stage_w(pc);
     if (sb + 2 < sb1) load_w(pc, sb + 2);
     if (sb + 1 < sb1) load_a(nxt, sb + 1);
     wave_lds_sync();
     compute(cur);
   };
-  for (int sb = sb0; sb < sb1; sb += 2) {
-    step(pa, aa, ab, sb);
-    if (sb + 1 < sb1) step(pb, ab, aa, sb + 1);
+  int sb = sb0;
+  for (; sb + 3 < sb1; sb += 2) {
+    step_full(pa, aa, ab, sb);
+    step_full(pb, ab, aa, sb + 1);
   }
+  if (sb < sb1) step_tail(pa, aa, ab, sb);
+  if (sb + 1 < sb1) step_tail(pb, ab, aa, sb + 1);
+  if (sb + 2 < sb1) step_tail(pa, aa, ab, sb + 2);
 
   // the waves' partial sums of the tiles, added in wave order
   wave_lds_sync();

@@ -104,11 +104,14 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
       pc.v[t] = ld_stream16(s - ((uintptr_t)s & 15) + 16 * pj[t]);
     }
   };
+  // every lane writes (lanes past the pieces rewrite the last piece, which
+  // they loaded too): no branch, so the loads' wait counts stay exact
   auto stage_w = [&](const Pieces& pc) {
 #pragma unroll
     for (int t = 0; t < L; t++) {
       const int p = lane + 64 * t;
-      if (p < Pieces::P) *(uint4*)(buf + (p / 14) * kQ6Win + 16 * (p % 14)) = pc.v[t];
+      const int pp = p < Pieces::P ? p : Pieces::P - 1;
+      *(uint4*)(buf + (pp / 14) * kQ6Win + 16 * (pp % 14)) = pc.v[t];
     }
   };
   // the block offset of the lane's own rows within their staged windows
@@ -214,7 +217,19 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
     if (sb0 + 1 < sb1) load_w(pb, sb0 + 1);
     load_a(aa, sb0);
   }
-  auto step = [&](Pieces& pc, Q6Act<MT>& cur, Q6Act<MT>& nxt, int sb) {
+  // The main loop runs while both of its steps have all their loads, which
+  // it then issues unconditionally (a load issued on one path and not
+  // another makes the compiler wait for every load in flight); the last
+  // steps follow it, loading only what remains.
+  auto step_full = [&](Pieces& pc, Q6Act<MT>& cur, Q6Act<MT>& nxt, int sb) {
+    wave_lds_sync();
+    stage_w(pc);
+    load_w(pc, sb + 2);
+    load_a(nxt, sb + 1);
+    wave_lds_sync();
+    compute(cur, sb);
+  };
+  auto step_tail = [&](Pieces& pc, Q6Act<MT>& cur, Q6Act<MT>& nxt, int sb) {
     wave_lds_sync();
     stage_w(pc);
     if (sb + 2 < sb1) load_w(pc, sb + 2);
@@ -222,10 +237,14 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
     wave_lds_sync();
     compute(cur, sb);
   };
-  for (int sb = sb0; sb < sb1; sb += 2) {
-    step(pa, aa, ab, sb);
-    if (sb + 1 < sb1) step(pb, ab, aa, sb + 1);
+  int sb = sb0;
+  for (; sb + 3 < sb1; sb += 2) {
+    step_full(pa, aa, ab, sb);
+    step_full(pb, ab, aa, sb + 1);
   }
+  if (sb < sb1) step_tail(pa, aa, ab, sb);
+  if (sb + 1 < sb1) step_tail(pb, ab, aa, sb + 1);
+  if (sb + 2 < sb1) step_tail(pa, aa, ab, sb + 2);
 
   wave_lds_sync();
   float* part = (float*)buf;
