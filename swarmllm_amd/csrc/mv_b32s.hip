@@ -80,15 +80,21 @@ __global__ __launch_bounds__(1024) void mv_b32_stream_kernel(MvTargets tg, int n
   int64_t lR = gw;
   int lsp = 0;
   const uint8_t* lrow = nullptr;
+  // Past the wave's last row the loads read the first bytes of the
+  // activation (cached, never used): every step issues one span's loads and
+  // writes all of its pieces, so the compiler counts the loads in flight
+  // exactly and waits for the oldest span only.
+  const uint8_t* const idle = FUSED ? (const uint8_t*)x : (const uint8_t*)yq;
   auto load_next = [&](Span& sp) {
-    if (lsp == 0) {
+    const bool real = lR < n_total;
+    if (lsp == 0 && real) {
       float* o;
       int64_t l;
       lrow = row_ptr(lR, o, l);
     }
-    const int b0 = lsp * kB32SpanBlocks;
-    const int len = nb - b0 < kB32SpanBlocks ? nb - b0 : kB32SpanBlocks;
-    const uint8_t* p = lrow + (int64_t)b0 * F::B;
+    const int b0 = real ? lsp * kB32SpanBlocks : 0;
+    const int len = real ? (nb - b0 < kB32SpanBlocks ? nb - b0 : kB32SpanBlocks) : 1;
+    const uint8_t* p = real ? lrow + (int64_t)b0 * F::B : idle;
     sp.off = (int)((uintptr_t)p & 15);
     sp.len = len;
     const uint8_t* a0 = p - sp.off;
@@ -122,8 +128,8 @@ __global__ __launch_bounds__(1024) void mv_b32_stream_kernel(MvTargets tg, int n
     for (int p = 0; p < kPre; p++) xv[p] = xload(p);
   }
   Span sa, sb;
-  if (S > 0) load_next(sa);
-  if (S > 1) load_next(sb);
+  load_next(sa);
+  load_next(sb);
 
   // 2. the activation into LDS
   auto quant_pass = [&](int pass, const float4& v4) {
@@ -131,17 +137,17 @@ __global__ __launch_bounds__(1024) void mv_b32_stream_kernel(MvTargets tg, int n
     const int t = pass * 1024 + (int)threadIdx.x;
     const int blk = t >> 3, sub = t & 7;
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) amax = rs_max(amax, fabsf(v[i]));
-    amax = rs_max(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, true)));
-    amax = rs_max(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x4E, 0xF, 0xF, true)));
-    amax = rs_max(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x141, 0xF, 0xF, true)));
+    // amax as f32::max folds it (fmaxf ignores NaN the same way); >= 0, so
+    // the 8-lane maximum (DPP within rows of 16) is taken on its bits
+    const float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    uint32_t ab = __float_as_uint(fmaxf(am, 0.0f));
+    ab = max(ab, dpp_u<0xB1>(ab));
+    ab = max(ab, dpp_u<0x4E>(ab));
+    ab = max(ab, dpp_u<0x141>(ab));
+    const float amax = __uint_as_float(ab);
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t packed = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) packed |= (uint32_t)(rs_as_i8(roundf(v[i] * id)) & 0xFF) << (8 * i);
+    const uint32_t packed = pack4_i8(q8_0_code(v[0] * id), q8_0_code(v[1] * id), q8_0_code(v[2] * id), q8_0_code(v[3] * id));
     if (blk < nblk) {
       const int r = blk / nb, b = blk - r * nb;
       *(uint32_t*)(acodes + r * k + b * 32 + 4 * sub) = packed;
@@ -174,11 +180,14 @@ __global__ __launch_bounds__(1024) void mv_b32_stream_kernel(MvTargets tg, int n
   auto step = [&](Span& cur, int64_t sigma) {
     wave_lds_sync();
 #pragma unroll
-    for (int c = 0; c < Span::kLoads; c++)
-      if (lane + 64 * c < Span::kPieces) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
+    for (int c = 0; c < Span::kLoads; c++) {
+      const int pc = lane + 64 * c;
+      *(uint4*)(buf + 16 * (pc < Span::kPieces ? pc : Span::kPieces - 1)) = cur.p[c];
+    }
     wave_lds_sync();
     const int off = cur.off, len = cur.len;
-    if (sigma + 2 < S) load_next(cur);
+    load_next(cur);
+    if (sigma >= S) return;
     if (bl < len) {
       const bool two = bl + 1 < len;
       uint32_t q0[8], q1[8];
@@ -229,7 +238,7 @@ __global__ __launch_bounds__(1024) void mv_b32_stream_kernel(MvTargets tg, int n
   };
   for (int64_t sigma = 0; sigma < S; sigma += 2) {
     step(sa, sigma);
-    if (sigma + 1 < S) step(sb, sigma + 1);
+    step(sb, sigma + 1);
   }
 }
 

@@ -155,12 +155,29 @@ __device__ __forceinline__ float wave_sum(float v) {
 // 0.49999997 + 0.5, upwards), and the clamp, taken with min first, sends NaN
 // to 127 and the infinities (a denormal block maximum can make iscale
 // infinite) to the saturated codes. Checked against the reference's steps for
-// all 2^32 floats (tests/test_q8k_rounding.py restates the check on the
+// all 2^32 floats (tests/test_act_rounding.py restates the check on the
 // half-integer neighbourhoods). Four instructions and the conversion.
 __device__ __forceinline__ int32_t q8k_code(float t) {
 #pragma clang fp contract(off)
   const float s = t + __builtin_copysignf(0.49999997f, t);
   return (int32_t)fmaxf(fminf(s, 127.49f), -128.49f);
+}
+
+// One Q8_0 code (BlockQ8_0::from_float, k_quants.rs:1262-1265): the
+// reference computes t = x * id, then t.round() (half away from zero) and
+// `as i8` (saturating, NaN gives 0). The same rounding as q8k_code, then
+// v_cvt_i32_f32 (which truncates, saturates out-of-range values and gives 0
+// for NaN) and a clamp to -128..127. Checked against the reference's steps
+// for all 2^32 floats (tests/act_rounding_exhaustive.c).
+__device__ __forceinline__ int32_t cvt_i32_trunc_sat(float f) {
+  int32_t r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(f));
+  return r;
+}
+__device__ __forceinline__ int32_t q8_0_code(float t) {
+#pragma clang fp contract(off)
+  const int32_t q = cvt_i32_trunc_sat(t + __builtin_copysignf(0.49999997f, t));
+  return q < -128 ? -128 : (q > 127 ? 127 : q);
 }
 
 // 4 codes (each in -128..127) packed one per byte, code 0 in the low byte.

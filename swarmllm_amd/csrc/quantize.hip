@@ -123,21 +123,19 @@ __global__ __launch_bounds__(256) void q8_0_kernel(const float* __restrict__ x, 
 #pragma unroll
     for (int i = 0; i < 4; i++) v[i] = xp[i];
   }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; i++) amax = rs_max(amax, fabsf(v[i]));
-  amax = rs_max(amax, __shfl_xor(amax, 1, kWave));
-  amax = rs_max(amax, __shfl_xor(amax, 2, kWave));
-  amax = rs_max(amax, __shfl_xor(amax, 4, kWave));
+  // amax as f32::max folds it (fmaxf ignores NaN the same way); >= 0, so
+  // the 8-lane maximum is taken on its bits
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  uint32_t ab = __float_as_uint(fmaxf(amax, 0.0f));
+  ab = max(ab, (uint32_t)__shfl_xor((int)ab, 1, kWave));
+  ab = max(ab, (uint32_t)__shfl_xor((int)ab, 2, kWave));
+  ab = max(ab, (uint32_t)__shfl_xor((int)ab, 4, kWave));
+  amax = __uint_as_float(ab);
   const float d = amax / 127.0f;
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
-  int32_t packed = 0, s = 0;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int q = rs_as_i8(roundf(v[i] * id));
-    packed |= (q & 0xFF) << (8 * i);
-    s += q;
-  }
+  const int32_t packed =
+      (int32_t)pack4_i8(q8_0_code(v[0] * id), q8_0_code(v[1] * id), q8_0_code(v[2] * id), q8_0_code(v[3] * id));
+  int32_t s = __builtin_amdgcn_sdot4(packed, 0x01010101, 0, false);
   const uint16_t dh = f2h(d);
   if (kGguf) {
     uint8_t* o = gguf + blk * 34;

@@ -1,13 +1,15 @@
-"""The device Q8_K quantizer's rounding formula (q8k_code in
-swarmllm_amd/csrc/qmm_device.h): trunc(clamp(t + copysign(0.49999997, t),
--128.49, 127.49)) gives the reference's code for t = iscale * x
-(BlockQ8K::from_float, vendor/candle/candle-core/src/quantized/k_quants.rs:2917-2920:
-t.round() half away from zero, .min(127.) with NaN -> 127, `as i8`).
+"""The device activation quantizers' rounding formulas (swarmllm_amd/csrc/qmm_device.h):
+q8k_code, trunc(clamp(t + copysign(0.49999997, t), -128.49, 127.49)), gives
+the reference's Q8_K code for t = iscale * x (BlockQ8K::from_float,
+vendor/candle/candle-core/src/quantized/k_quants.rs:2917-2920: t.round() half
+away from zero, .min(127.) with NaN -> 127, `as i8`); q8_0_code, the same
+rounding through v_cvt_i32_f32 and a clamp, gives its Q8_0 code
+(BlockQ8_0::from_float, :1262-1265: t.round() as i8, NaN -> 0).
 
 Two checks: a numpy restatement over the places a rounding formula can go
 wrong (every float within 64 ulps of each half-integer and integer in
 [-130, 130], the special values, a random sample of bit patterns), and the
-exhaustive C check over all 2^32 floats (about 8 s on 8 threads)."""
+exhaustive C check of both over all 2^32 floats (about 10 s on 8 threads)."""
 import os
 import shutil
 import subprocess
@@ -67,9 +69,9 @@ def test_exhaustive_over_all_floats(tmp_path):
     cc = shutil.which("gcc")
     if cc is None:
         pytest.skip("gcc not available")
-    exe = tmp_path / "q8k_rounding"
+    exe = tmp_path / "act_rounding"
     subprocess.run([cc, "-O2", "-fopenmp", "-ffp-contract=off", "-o", str(exe),
-                    os.path.join(HERE, "q8k_rounding_exhaustive.c"), "-lm"], check=True)
+                    os.path.join(HERE, "act_rounding_exhaustive.c"), "-lm"], check=True)
     env = dict(os.environ, OMP_NUM_THREADS=str(min(8, os.cpu_count() or 1)))
     r = subprocess.run([str(exe)], capture_output=True, text=True, env=env, timeout=600)
     assert r.returncode == 0, r.stdout + r.stderr

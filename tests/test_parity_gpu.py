@@ -76,6 +76,10 @@ def test_q8k_activation_bit_exact(k, rows):
 @pytest.mark.parametrize("k,rows", [(32, 1), (2880, 1), (4096, 5), (14336, 2)])
 def test_q8_0_activation_bit_exact(k, rows):
     x = act_inputs(k, rows, 2)
+    x[-1, 5] = np.nan  # never the block's largest; `as i8` of NaN is 0
+    if k >= 96:
+        x[-1, 32 + 3] = np.inf  # amax inf: d inf, id 0, inf * 0 is NaN (code 0)
+        x[-1, 64 + 7] = -np.inf
     buf = quantize_act(upload(x), _lib.ACT_Q8_0)
     codes, scales, sums = (t.cpu().numpy() for t in act_planes(buf, _lib.ACT_Q8_0, k, rows))
     for r in range(rows):
