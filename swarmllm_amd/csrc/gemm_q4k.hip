@@ -153,27 +153,42 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
   const uint32_t alast = (uint32_t)((M - 1) * K);
   const uint32_t kstep4 = (uint32_t)(4 * K);
 
-  auto issue = [&](int sb, uint8_t* sw, int8_t* sa) {
-    uint32_t lane0 = (uint32_t)lane;
-    asm volatile("" : "+v"(lane0));  // the offsets are recomputed per super-block, not held across it
+  // A wave's copies of one super-block: kWCopies of the weight tile, then
+  // kACopies of the activation tile. They are issued one per K-step of the
+  // super-block before (all of a CU's copies issued at once queue in the
+  // memory pipeline and hold up every wave's next instruction).
+  constexpr int kWCopies = (kWInstr + kWaves - 1) / kWaves, kACopies = kAInstr / kWaves;
+  constexpr int kCopies = kWCopies + kACopies;
+  static_assert(kCopies <= 16, "one copy a K-step");
+  // Each copy's per-lane byte offset, for super-block 0 (the super-block
+  // advances the scalar base address instead).
+  uint32_t coff[kCopies];
 #pragma unroll
-    for (int u = 0; u < (kWInstr + kWaves - 1) / kWaves; u++) {
-      const int i = wv + kWaves * u;
-      if (i < kWInstr) {
-        const uint32_t f = 64u * (uint32_t)i + lane0;
-        const uint32_t r = (f * 7282u) >> 16;  // f / 9 for f < 2^14
-        const uint32_t row = (uint32_t)(n0 + r) * rowbytes;
-        const uint32_t off = (row < wlast ? row : wlast) + 16u * (f - 9u * r) + 144u * (uint32_t)sb;
-        dma16(W, off, lds_addr(sw + 1024 * i));
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kAInstr / kWaves; u++) {
-      const int i = wv + kWaves * u;
+  for (int j = 0; j < kCopies; j++) {
+    if (j < kWCopies) {
+      const uint32_t i = (uint32_t)(wv + kWaves * j);
+      const uint32_t f = 64u * i + (uint32_t)lane;
+      const uint32_t r = (f * 7282u) >> 16;  // f / 9 for f < 2^14
+      const uint32_t row = (uint32_t)(n0 + r) * rowbytes;
+      coff[j] = (row < wlast ? row : wlast) + 16u * (f - 9u * r);
+    } else {
+      const int i = wv + kWaves * (j - kWCopies);
       const uint32_t row = arow0 + (uint32_t)(4 * i) * (kstep4 / 4);
-      const uint32_t off = (row < alast ? row : alast) + 16u * (lp ^ (4u * (uint32_t)(i & 3) + lq)) + 256u * (uint32_t)sb;
-      dma16(yq, off, lds_addr(sa + 1024 * i));
+      coff[j] = (row < alast ? row : alast) + 16u * (lp ^ (4u * (uint32_t)(i & 3) + lq));
     }
+  }
+  auto issue_one = [&](int sb, int j, uint8_t* sw, int8_t* sa) {
+    if (j < kWCopies) {
+      const int i = wv + kWaves * j;
+      if (i < kWInstr) dma16(W + 144 * sb, coff[j], lds_addr(sw + 1024 * i));
+    } else {
+      const int i = wv + kWaves * (j - kWCopies);
+      dma16(yq + 256 * sb, coff[j], lds_addr(sa + 1024 * i));
+    }
+  };
+  auto issue = [&](int sb, uint8_t* sw, int8_t* sa) {
+#pragma unroll
+    for (int j = 0; j < kCopies; j++) issue_one(sb, j, sw, sa);
   };
 
   // per-super-block activation scales: thread t < 256 takes row t/2, sub-blocks 4(t%2)..+3
@@ -254,10 +269,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
   // copies into the other half
   auto step = [&](int sb, const uint8_t* sw, const int8_t* sa, uint8_t* nw, int8_t* na) {
     const bool more = sb + 1 < nsb;
-    if (more) {
-      load_s(sb + 1);
-      issue(sb + 1, nw, na);
-    }
+    if (more) load_s(sb + 1);
 
     WRaw cur;
     {
@@ -283,11 +295,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
     const int xh = (r32 & 15) >> 1;
     const int8_t* at = sa + r32 * 256 + 16 * (h ^ (r32 & 1));
     // The B operand of K-chunk kc of pass p: this lane's 16 code bytes of
-    // chunk kc/2 (low nibbles for even kc, high for odd) times sh or sl.
+    // chunk kc/2 (low nibbles for even kc, high for odd) times sh or sl,
+    // the factor byte placed in both 16-bit halves by one byte permute.
+    const uint32_t sh03 = (s03 >> 3) & 0x07070707u, sl03 = s03 & 0x07070707u;
+    const uint32_t sh47 = (s47 >> 3) & 0x07070707u, sl47 = s47 & 0x07070707u;
     auto make_b = [&](int pass, int kc) {
-      const uint32_t sw = kc < 4 ? s03 : s47;
-      const uint32_t scv = (sw >> (8 * (kc & 3))) & 0xFF;
-      const uint32_t f = dup16(pass == 0 ? scv >> 3 : scv & 7);
+      const uint32_t sw = pass == 0 ? (kc < 4 ? sh03 : sh47) : (kc < 4 ? sl03 : sl47);
+      const uint32_t k = (uint32_t)(kc & 3);
+      const uint32_t f = __builtin_amdgcn_perm(0u, sw, 0x0C000C00u | (k << 16) | k);
       const uint4& ch = chunk(cur, kc >> 1);
       i4v b;
 #pragma unroll
@@ -301,35 +316,48 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
 #pragma unroll
       for (int t = 0; t < 4; t++) a[t] = *(const i4v*)(at + 32 * t * 256 + 32 * (kc ^ xh));
     };
-    // Software-pipelined by one K-chunk: each block issues its four MFMAs,
-    // then builds the next chunk's B operand and reads its A fragments, work
-    // that runs while the matrix unit is busy with the MFMAs before it.
+    // Software-pipelined by one K-chunk, tile by tile: tile t's A fragment
+    // of the next chunk is read right after tile t's MFMA has taken the
+    // current one (three MFMAs before it is needed), the next chunk's B
+    // operand is built under the MFMAs, and at the start of the second pass
+    // each tile is shifted just before its first MFMA of that pass.
+    const int8_t* const at_t[4] = {at, at + 32 * 256, at + 64 * 256, at + 96 * 256};
     i4v bq = make_b(0, 0);
     i4v af[4];
     load_a(0, af);
 #pragma unroll
     for (int step = 0; step < 16; step++) {
-      const int pass = step >> 3, kc = step & 7;
+      const int ns = step + 1;
+      i4v bn = bq;
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        const i16v zero = {};
-        c[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[t], bq, step == 0 ? zero : c[t], 0, 0, 0);
-      }
-      if (step + 1 < 16) {
-        bq = make_b((step + 1) >> 3, (step + 1) & 7);
-        load_a((step + 1) & 7, af);
-      }
-      if (step == 7) {
-#pragma unroll
-        for (int t = 0; t < 4; t++)
+        if (step == 8) {
 #pragma unroll
           for (int i = 0; i < 16; i++) c[t][i] <<= 3;
+        }
+        const i16v zero = {};
+        c[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[t], bq, step == 0 ? zero : c[t], 0, 0, 0);
+        if (ns < 16) af[t] = *(const i4v*)(at_t[t] + 32 * ((ns & 7) ^ xh));
+        if (t == 1 && ns < 16) bn = make_b(ns >> 3, ns & 7);
+      }
+      // The copies of super-block sb + 1 (at the last super-block, the last
+      // one's again, into the half no wave reads any more: no branch in the
+      // chunk's block).
+      if (step < kCopies) issue_one(more ? sb + 1 : sb, step, nw, na);
+      bq = bn;
+      // The order within the chunk: each MFMA, then its tile's next
+      // fragment read; the next B operand after the second MFMA; the
+      // second pass's shifts each before their tile's MFMA.
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        if (step == 8) __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (ns < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (t == 1 && ns < 16) __builtin_amdgcn_sched_group_barrier(0x002, 13, 0);
       }
       // keep each K-chunk's work in its block (hoisting the operand loads of
       // every chunk would hold 64 fragments in registers)
       __builtin_amdgcn_sched_barrier(0);
-      (void)pass;
-      (void)kc;
     }
 
     epilogue(c, sb, dw, dmin, m03, m47);
@@ -346,6 +374,8 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
     step(sb, s_w0, s_a0, s_w1, s_a1);
     if (sb + 1 < nsb) step(sb + 1, s_w1, s_a1, s_w0, s_a0);
   }
+  // the last super-block's repeated copies land before the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0);
 
   const int64_t col = n0 + 32 * wv + r32;
   if (col < N) {
