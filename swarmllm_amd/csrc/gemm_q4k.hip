@@ -322,6 +322,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
     // operand is built under the MFMAs, and at the start of the second pass
     // each tile is shifted just before its first MFMA of that pass.
     const int8_t* const at_t[4] = {at, at + 32 * 256, at + 64 * 256, at + 96 * 256};
+    // The matrix loop runs at a higher issue priority than the epilogue:
+    // while one wave of a SIMD is in its f32 epilogue, the other's MFMAs and
+    // operand work go first and keep the matrix unit fed.
+    __builtin_amdgcn_s_setprio(1);
     i4v bq = make_b(0, 0);
     i4v af[4];
     load_a(0, af);
@@ -360,6 +364,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q4k_kernel(const uint8_t*
       __builtin_amdgcn_sched_barrier(0);
     }
 
+    __builtin_amdgcn_s_setprio(0);
     epilogue(c, sb, dw, dmin, m03, m47);
 
     if (more) {
