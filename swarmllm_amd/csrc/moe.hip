@@ -13,11 +13,13 @@
 // (Q8_0, the VecDotType of these formats). An entry whose expert or pair is
 // out of range writes nothing, as in the reference.
 //
-// Shape of the work: a pre-pass (moe_runs_kernel, one workgroup) cuts the
-// routing into runs of consecutive entries with the same expert — with ids
-// sorted by expert, one run per touched expert — so the products of a run
-// read the expert's weights once: a wave stages each weight row's blocks in
-// LDS and applies them to up to 8 of the run's activation rows at a time.
+// Shape of the work: the routing is cut into runs of consecutive entries
+// with the same expert — with ids sorted by expert, one run per touched
+// expert — so the products of a run read the expert's weights once: a wave
+// stages each weight row's blocks in LDS and applies them to up to 8 of the
+// run's activation rows at a time. The run table (moe_runs.h) is written by
+// one extra workgroup of the launch that quantizes the activation
+// (launch_act_quantize_moe), so a product is two launches.
 // The per-unit arithmetic and the reduction are the decode kernel's
 // (b32_common.h, wave_sum_dpp), so each pair's result is bit-identical to
 // the same product through qmm_forward (times its scale): the reference's
@@ -31,43 +33,8 @@ namespace {
 constexpr int kMoeWaves = 4;   // waves per workgroup
 constexpr int kMoePairs = 8;   // activation rows a wave applies a staged row to
 
-// runs[0] = number of runs; run r at runs[1 + 3r]: first entry, length, expert.
-__global__ __launch_bounds__(1024) void moe_runs_kernel(const int32_t* __restrict__ expert_ids, int size_m,
-                                                        int32_t* __restrict__ runs) {
-  __shared__ int32_t scan[1024];
-  __shared__ int32_t base;
-  const int t = threadIdx.x;
-  if (t == 0) base = 0;
-  __syncthreads();
-  for (int c0 = 0; c0 < size_m; c0 += 1024) {
-    const int i = c0 + t;
-    const int e = i < size_m ? expert_ids[i] : 0;
-    const int f = (i < size_m && (i == 0 || expert_ids[i - 1] != e)) ? 1 : 0;
-    scan[t] = f;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {  // inclusive scan of the run-start flags
-      const int v = t >= d ? scan[t - d] : 0;
-      __syncthreads();
-      scan[t] += v;
-      __syncthreads();
-    }
-    if (f) {
-      const int r = base + scan[t] - 1;
-      runs[1 + 3 * r] = i;
-      runs[3 + 3 * r] = e;
-    }
-    __syncthreads();
-    if (t == 0) base += scan[1023];
-    __syncthreads();
-  }
-  const int nr = base;
-  for (int r = t; r < nr; r += 1024) {
-    const int s = runs[1 + 3 * r];
-    const int s2 = r + 1 < nr ? runs[1 + 3 * (r + 1)] : size_m;
-    runs[2 + 3 * r] = s2 - s;
-  }
-  if (t == 0) runs[0] = nr;
-}
+// runs[0] = number of runs; run r at runs[1 + 3r]: first entry, length, expert
+// (written by moe_runs_block, moe_runs.h).
 
 template <int FMT, int RPW>
 __global__ __launch_bounds__(64 * kMoeWaves) void moe_b32_kernel(
@@ -205,17 +172,6 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint8_t* const buf = smem + ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)wv * Span::kStage;
 
-  // The run: its count and its (first entry, length, expert) are read
-  // together (the runs buffer holds 1 + 3 size_m ints and run < gridDim.y <=
-  // size_m); each lookup below is one batch of independent scalar loads.
-  const int run = blockIdx.y;
-  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
-  const int start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
-  const int len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
-  const int e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
-  if (run >= nruns) return;  // the whole workgroup: before any barrier
-  if (e < 0 || e >= num_experts) return;
-  const uint8_t* We = W + (int64_t)e * estride;
   const int64_t rb = (int64_t)nb * F::B;
   const int nspan = (nb + 127) / 128;
   const int64_t r0 = ((int64_t)blockIdx.x * kMoeSWaves + wv) * rpw;
@@ -225,161 +181,176 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
   const uint32_t t0 = lut.t0, t1 = lut.t1, t2 = lut.t2, t3 = lut.t3;
   const int bl = 2 * lane;
 
-  for (int c0 = 0; c0 < len; c0 += kMoePairs) {
-    const int cnt = len - c0 < kMoePairs ? len - c0 : kMoePairs;
-    // The wave's weight rows: the loads run kMoeRing spans ahead of the
-    // arithmetic; past the wave's last span they read the first bytes of the
-    // quantized activation (cached, never used). Every step issues one span's
-    // loads and writes all of its pieces, so the compiler counts the loads
-    // in flight exactly and waits for the oldest span only. The first spans
-    // go out before the entries are looked up.
-    int64_t lr = r0;
-    int lsp = 0;
-    auto load_next = [&](Span& sp) {
-      const bool real = lr < r0 + nrows;
-      const int b0 = lsp * 128;
-      const int blen = real ? (nb - b0 < 128 ? nb - b0 : 128) : 1;
-      const uint8_t* pp = real ? We + lr * rb + (int64_t)b0 * F::B : (const uint8_t*)yq;
-      sp.off = (int)((uintptr_t)pp & 15);
-      sp.len = blen;
-      const uint8_t* a0 = pp - sp.off;
-      const int pieces = (sp.off + blen * F::B + 15) >> 4;
-#pragma unroll
-      for (int c = 0; c < Span::kLoads; c++) {
-        const int pc = lane + 64 * c;
-        sp.p[c] = ld_stream16(a0 + 16u * (uint32_t)(pc < pieces ? pc : pieces - 1));
-      }
-      if (++lsp == nspan) {
-        lsp = 0;
-        lr++;
-      }
-    };
-    Span ring[kMoeRing];
-#pragma unroll
-    for (int j = 0; j < kMoeRing; j++) load_next(ring[j]);
+  // Runs blockIdx.y, blockIdx.y + gridDim.y, ...: with entries grouped by
+  // expert there are at most as many runs as experts and each workgroup
+  // takes one; entries in any order are still all computed. The loop and
+  // its barriers are uniform over the workgroup.
+  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  for (int run = blockIdx.y; run < nruns; run += gridDim.y) {
+    // its (first entry, length, expert), one batch of scalar loads
+    const int start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
+    const int len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
+    const int e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+    if (e < 0 || e >= num_experts) continue;
+    const uint8_t* We = W + (int64_t)e * estride;
 
-    // the chunk's entries: their pair indices (indices clamped into the run),
-    // then their routing weights, each one batch
-    int pr[kMoePairs];
-#pragma unroll
-    for (int p = 0; p < kMoePairs; p++) pr[p] = __builtin_amdgcn_readfirstlane(ids[start + c0 + (p < cnt ? p : cnt - 1)]);
-    int64_t out_row[kMoePairs];
-    float scale[kMoePairs];
-    bool use[kMoePairs];
-    int64_t in_row[kMoePairs];
-#pragma unroll
-    for (int p = 0; p < kMoePairs; p++) {
-      use[p] = p < cnt && pr[p] >= 0 && pr[p] < size_m;
-      out_row[p] = use[p] ? pr[p] : 0;
-      in_row[p] = use[p] ? (topk_w ? pr[p] : pr[p] / topk) : 0;
-    }
-#pragma unroll
-    for (int p = 0; p < kMoePairs; p++) scale[p] = topk_w ? topk_w[use[p] ? pr[p] : 0] : 1.0f;
-    // The chunk's activation rows into LDS (after the previous chunk's
-    // reads): entry p is copied by wave p, each lane loading a fixed number
-    // of 16-byte code pieces and scales (addresses clamped to the row;
-    // k <= 4096, the launcher checks).
-    __syncthreads();
-    const int cp = wv;  // the entry this wave copies (uniform)
-    const int ct = lane;
-    const bool cuse = cp < kMoePairs && use[cp < kMoePairs ? cp : 0];
-    const int8_t* crow = yq + (cuse ? in_row[cp] * k : 0);
-    const float* cdrow = yd + (cuse ? in_row[cp] * nb : 0);
-    const int npc = k / 16;
-    auto ld_piece = [&](int j) {
-      const int i = ct + 64 * j;
-      return *(const uint4*)(crow + 16 * (i < npc ? i : npc - 1));
-    };
-    auto ld_scale = [&](int j) {
-      const int i = ct + 64 * j;
-      return cdrow[i < nb ? i : nb - 1];
-    };
-    // named registers (an array here was kept in scratch memory)
-    const uint4 cv0 = ld_piece(0), cv1 = ld_piece(1), cv2 = ld_piece(2), cv3 = ld_piece(3);
-    const float cd0 = ld_scale(0), cd1 = ld_scale(1);
-    if (cuse) {
-      auto st_piece = [&](int j, const uint4& v) {
-        const int i = ct + 64 * j;
-        if (i < npc) *(uint4*)(acodes + cp * k + 16 * i) = v;
-      };
-      auto st_scale = [&](int j, float v) {
-        const int i = ct + 64 * j;
-        if (i < nb) ad[cp * nb + i] = v;
-      };
-      st_piece(0, cv0);
-      st_piece(1, cv1);
-      st_piece(2, cv2);
-      st_piece(3, cv3);
-      st_scale(0, cd0);
-      st_scale(1, cd1);
-    }
-    __syncthreads();
-    int64_t R = r0;
-    int sp = 0;
-    float acc[kMoePairs];
-#pragma unroll
-    for (int p = 0; p < kMoePairs; p++) acc[p] = 0.0f;
-    auto step = [&](Span& cur, int64_t sigma) {
-      wave_lds_sync();
-#pragma unroll
-      for (int c = 0; c < Span::kLoads; c++) {
-        const int pc = lane + 64 * c;
-        *(uint4*)(buf + 16 * (pc < Span::kPieces ? pc : Span::kPieces - 1)) = cur.p[c];
-      }
-      wave_lds_sync();
-      const int off = cur.off, blen = cur.len;
-      load_next(cur);
-      if (sigma >= S) return;
-      if (bl < blen) {
-        const bool two = bl + 1 < blen;
-        uint32_t q0[8], q1[8];
-        float dx0, dx1;
-        F::decode(buf, off + bl * F::B, q0, dx0, t0, t1, t2, t3);
-        if (two) {
-          F::decode(buf, off + (bl + 1) * F::B, q1, dx1, t0, t1, t2, t3);
-        } else {
-#pragma unroll
-          for (int t = 0; t < 8; t++) q1[t] = 0;
-          dx1 = 0.0f;
+    for (int c0 = 0; c0 < len; c0 += kMoePairs) {
+      const int cnt = len - c0 < kMoePairs ? len - c0 : kMoePairs;
+      // The wave's weight rows: the loads run kMoeRing spans ahead of the
+      // arithmetic; past the wave's last span they read the first bytes of the
+      // quantized activation (cached, never used). Every step issues one span's
+      // loads and writes all of its pieces, so the compiler counts the loads
+      // in flight exactly and waits for the oldest span only. The first spans
+      // go out before the entries are looked up.
+      int64_t lr = r0;
+      int lsp = 0;
+      auto load_next = [&](Span& sp) {
+        const bool real = lr < r0 + nrows;
+        const int b0 = lsp * 128;
+        const int blen = real ? (nb - b0 < 128 ? nb - b0 : 128) : 1;
+        const uint8_t* pp = real ? We + lr * rb + (int64_t)b0 * F::B : (const uint8_t*)yq;
+        sp.off = (int)((uintptr_t)pp & 15);
+        sp.len = blen;
+        const uint8_t* a0 = pp - sp.off;
+        const int pieces = (sp.off + blen * F::B + 15) >> 4;
+  #pragma unroll
+        for (int c = 0; c < Span::kLoads; c++) {
+          const int pc = lane + 64 * c;
+          sp.p[c] = ld_stream16(a0 + 16u * (uint32_t)(pc < pieces ? pc : pieces - 1));
         }
-        const int gb = sp * 128 + bl;
-#pragma unroll
-        for (int p = 0; p < kMoePairs; p++) {
-          if (!use[p]) continue;
-          Act64 a;
-          const int4* yp = (const int4*)(acodes + p * k + gb * 32);
-          const int4 a0 = yp[0], a1 = yp[1];
-          a.y[0][0] = a0.x; a.y[0][1] = a0.y; a.y[0][2] = a0.z; a.y[0][3] = a0.w;
-          a.y[0][4] = a1.x; a.y[0][5] = a1.y; a.y[0][6] = a1.z; a.y[0][7] = a1.w;
-          a.dy[0] = ad[p * nb + gb];
+        if (++lsp == nspan) {
+          lsp = 0;
+          lr++;
+        }
+      };
+      Span ring[kMoeRing];
+  #pragma unroll
+      for (int j = 0; j < kMoeRing; j++) load_next(ring[j]);
+
+      // the chunk's entries: their pair indices (indices clamped into the run),
+      // then their routing weights, each one batch
+      int pr[kMoePairs];
+  #pragma unroll
+      for (int p = 0; p < kMoePairs; p++)
+        pr[p] = __builtin_amdgcn_readfirstlane(ids[start + c0 + (p < cnt ? p : cnt - 1)]);
+      int64_t out_row[kMoePairs];
+      float scale[kMoePairs];
+      bool use[kMoePairs];
+      int64_t in_row[kMoePairs];
+  #pragma unroll
+      for (int p = 0; p < kMoePairs; p++) {
+        use[p] = p < cnt && pr[p] >= 0 && pr[p] < size_m;
+        out_row[p] = use[p] ? pr[p] : 0;
+        in_row[p] = use[p] ? (topk_w ? pr[p] : pr[p] / topk) : 0;
+      }
+  #pragma unroll
+      for (int p = 0; p < kMoePairs; p++) scale[p] = topk_w ? topk_w[use[p] ? pr[p] : 0] : 1.0f;
+      // The chunk's activation rows into LDS (after the previous chunk's
+      // reads): entry p is copied by wave p, each lane loading a fixed number
+      // of 16-byte code pieces and scales (addresses clamped to the row;
+      // k <= 4096, the launcher checks).
+      __syncthreads();
+      const int cp = wv;  // the entry this wave copies (uniform)
+      const int ct = lane;
+      const bool cuse = cp < kMoePairs && use[cp < kMoePairs ? cp : 0];
+      const int8_t* crow = yq + (cuse ? in_row[cp] * k : 0);
+      const float* cdrow = yd + (cuse ? in_row[cp] * nb : 0);
+      const int npc = k / 16;
+      auto ld_piece = [&](int j) {
+        const int i = ct + 64 * j;
+        return *(const uint4*)(crow + 16 * (i < npc ? i : npc - 1));
+      };
+      auto ld_scale = [&](int j) {
+        const int i = ct + 64 * j;
+        return cdrow[i < nb ? i : nb - 1];
+      };
+      // named registers (an array here was kept in scratch memory)
+      const uint4 cv0 = ld_piece(0), cv1 = ld_piece(1), cv2 = ld_piece(2), cv3 = ld_piece(3);
+      const float cd0 = ld_scale(0), cd1 = ld_scale(1);
+      if (cuse) {
+        auto st_piece = [&](int j, const uint4& v) {
+          const int i = ct + 64 * j;
+          if (i < npc) *(uint4*)(acodes + cp * k + 16 * i) = v;
+        };
+        auto st_scale = [&](int j, float v) {
+          const int i = ct + 64 * j;
+          if (i < nb) ad[cp * nb + i] = v;
+        };
+        st_piece(0, cv0);
+        st_piece(1, cv1);
+        st_piece(2, cv2);
+        st_piece(3, cv3);
+        st_scale(0, cd0);
+        st_scale(1, cd1);
+      }
+      __syncthreads();
+      int64_t R = r0;
+      int sp = 0;
+      float acc[kMoePairs];
+  #pragma unroll
+      for (int p = 0; p < kMoePairs; p++) acc[p] = 0.0f;
+      auto step = [&](Span& cur, int64_t sigma) {
+        wave_lds_sync();
+  #pragma unroll
+        for (int c = 0; c < Span::kLoads; c++) {
+          const int pc = lane + 64 * c;
+          *(uint4*)(buf + 16 * (pc < Span::kPieces ? pc : Span::kPieces - 1)) = cur.p[c];
+        }
+        wave_lds_sync();
+        const int off = cur.off, blen = cur.len;
+        load_next(cur);
+        if (sigma >= S) return;
+        if (bl < blen) {
+          const bool two = bl + 1 < blen;
+          uint32_t q0[8], q1[8];
+          float dx0, dx1;
+          F::decode(buf, off + bl * F::B, q0, dx0, t0, t1, t2, t3);
           if (two) {
-            const int4 b0 = yp[2], b1 = yp[3];
-            a.y[1][0] = b0.x; a.y[1][1] = b0.y; a.y[1][2] = b0.z; a.y[1][3] = b0.w;
-            a.y[1][4] = b1.x; a.y[1][5] = b1.y; a.y[1][6] = b1.z; a.y[1][7] = b1.w;
-            a.dy[1] = ad[p * nb + gb + 1];
+            F::decode(buf, off + (bl + 1) * F::B, q1, dx1, t0, t1, t2, t3);
           } else {
-#pragma unroll
-            for (int t = 0; t < 8; t++) a.y[1][t] = 0;
-            a.dy[1] = 0.0f;
+  #pragma unroll
+            for (int t = 0; t < 8; t++) q1[t] = 0;
+            dx1 = 0.0f;
           }
-          acc[p] = b32_unit(q0, q1, dx0, dx1, a, acc[p]);
+          const int gb = sp * 128 + bl;
+  #pragma unroll
+          for (int p = 0; p < kMoePairs; p++) {
+            if (!use[p]) continue;
+            Act64 a;
+            const int4* yp = (const int4*)(acodes + p * k + gb * 32);
+            const int4 a0 = yp[0], a1 = yp[1];
+            a.y[0][0] = a0.x; a.y[0][1] = a0.y; a.y[0][2] = a0.z; a.y[0][3] = a0.w;
+            a.y[0][4] = a1.x; a.y[0][5] = a1.y; a.y[0][6] = a1.z; a.y[0][7] = a1.w;
+            a.dy[0] = ad[p * nb + gb];
+            if (two) {
+              const int4 b0 = yp[2], b1 = yp[3];
+              a.y[1][0] = b0.x; a.y[1][1] = b0.y; a.y[1][2] = b0.z; a.y[1][3] = b0.w;
+              a.y[1][4] = b1.x; a.y[1][5] = b1.y; a.y[1][6] = b1.z; a.y[1][7] = b1.w;
+              a.dy[1] = ad[p * nb + gb + 1];
+            } else {
+  #pragma unroll
+              for (int t = 0; t < 8; t++) a.y[1][t] = 0;
+              a.dy[1] = 0.0f;
+            }
+            acc[p] = b32_unit(q0, q1, dx0, dx1, a, acc[p]);
+          }
         }
-      }
-      if (++sp == nspan) {
-#pragma unroll
-        for (int p = 0; p < kMoePairs; p++) {
-          if (!use[p]) continue;
-          const float v = wave_sum_dpp(acc[p]);
-          if (lane == 0) dst[out_row[p] * ldd + R] = __fmul_rn(v, scale[p]);
-          acc[p] = 0.0f;
+        if (++sp == nspan) {
+  #pragma unroll
+          for (int p = 0; p < kMoePairs; p++) {
+            if (!use[p]) continue;
+            const float v = wave_sum_dpp(acc[p]);
+            if (lane == 0) dst[out_row[p] * ldd + R] = __fmul_rn(v, scale[p]);
+            acc[p] = 0.0f;
+          }
+          sp = 0;
+          R++;
         }
-        sp = 0;
-        R++;
+      };
+      for (int64_t sigma = 0; sigma < S; sigma += kMoeRing) {
+  #pragma unroll
+        for (int j = 0; j < kMoeRing; j++) step(ring[j], sigma + j);
       }
-    };
-    for (int64_t sigma = 0; sigma < S; sigma += kMoeRing) {
-#pragma unroll
-      for (int j = 0; j < kMoeRing; j++) step(ring[j], sigma + j);
     }
   }
 }
@@ -435,11 +406,8 @@ bool moe_supported(int type) { return type == T_Q8_0 || type == T_IQ4_NL || type
 size_t moe_runs_bytes(int64_t size_m) { return (size_t)(1 + 3 * size_m) * sizeof(int32_t); }
 
 hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
-                      int32_t* runs, const int32_t* ids, const int32_t* expert_ids, const float* topk_w, int topk,
-                      int64_t size_m, float* dst, int64_t ldd, int cus, hipStream_t st) {
-  moe_runs_kernel<<<1, 1024, 0, st>>>(expert_ids, (int)size_m, runs);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+                      const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
+                      float* dst, int64_t ldd, int cus, hipStream_t st) {
   if (moe_stream_fits(k)) {
     switch (type) {
       case T_Q8_0: return launch_moe_s<T_Q8_0>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);

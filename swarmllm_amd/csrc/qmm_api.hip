@@ -402,11 +402,12 @@ int qmm_moe_forward(int type, const void* w, int num_experts, const float* x, in
   if (!w || !x || !dst || !sorted_ids || !expert_ids) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
-  if (qmm::launch_act_quantize(qmm::ACT_Q8_0, x, x_stride, k, in_rows, workspace, q8k_scale(), st) != hipSuccess)
+  // the activation's Q8_0 planes and the run table, one launch; then the grouped kernel
+  int32_t* runs = (int32_t*)((char*)workspace + act);
+  if (qmm::launch_act_quantize_moe(x, x_stride, k, in_rows, workspace, expert_ids, size_m, runs, st) != hipSuccess)
     return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(qmm::ACT_Q8_0, workspace, k, in_rows);
-  int32_t* runs = (int32_t*)((char*)workspace + act);
-  if (qmm::launch_moe(type, w, num_experts, n, k, p, runs, sorted_ids, expert_ids, topk_w, topk, size_m, dst, ldd,
+  if (qmm::launch_moe(type, w, num_experts, n, k, p, runs, sorted_ids, topk_w, topk, size_m, dst, ldd,
                       (int)cu_count(), st) != hipSuccess)
     return QMM_DEVICE_ERROR;
   g_moe_launches.fetch_add(1, std::memory_order_relaxed);

@@ -36,6 +36,10 @@ ActPlanes act_planes(int layout, void* base, int64_t k, int64_t rows);
 // ---- launchers (return hipSuccess or the launch error) ---------------------
 hipError_t launch_act_quantize(int layout, const float* x, int64_t stride, int64_t k, int64_t rows,
                                void* out, float q8k_scale, hipStream_t s);
+// ACT_Q8_0 quantization for a grouped expert product, which also writes
+// its run table (1 + 3 size_m ints) from expert_ids in the same launch.
+hipError_t launch_act_quantize_moe(const float* x, int64_t stride, int64_t k, int64_t rows, void* out,
+                                   const int32_t* expert_ids, int64_t size_m, int32_t* runs, hipStream_t s);
 hipError_t launch_weight_quantize(int type, const float* x, void* w, int64_t nelem, void* scratch,
                                   hipStream_t s);
 size_t weight_quantize_scratch_bytes(int type, int64_t nelem);
@@ -97,13 +101,14 @@ hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, 
 // dst = x · Wᵀ for a Q4_K weight from the Q8_K activation planes of `rows`
 // rows (qmm_quantize_act ACT_Q8K); used from gemm_q4k_min_rows() rows up.
 // Grouped expert products (moe.hip): types it covers, bytes of the run table
-// for size_m routing entries, and the launch (run pre-pass + grouped kernel)
-// from an activation already quantized in Q8_0 planes.
+// for size_m routing entries, and the grouped kernel's launch from an
+// activation already quantized in Q8_0 planes and its run table
+// (launch_act_quantize_moe).
 bool moe_supported(int type);
 size_t moe_runs_bytes(int64_t size_m);
 hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
-                      int32_t* runs, const int32_t* ids, const int32_t* expert_ids, const float* topk_w, int topk,
-                      int64_t size_m, float* dst, int64_t ldd, int cus, hipStream_t st);
+                      const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
+                      float* dst, int64_t ldd, int cus, hipStream_t st);
 
 // Q4_K products of a few rows (gemm_q4k_skinny.hip): up to
 // gemm_q4k_skinny_max_rows() activation rows, targets as the stream kernels.

@@ -15,6 +15,7 @@
 //   to_float per type      Q/k_quants.rs:1222 (Q8_0), 2238 (Q4_K), 2810 (Q6_K), 465 (MXFP4), 709 (IQ4_NL)
 #include "qmm_device.h"
 #include "qmm_launch.h"
+#include "moe_runs.h"
 
 namespace qmm {
 
@@ -103,11 +104,20 @@ __global__ __launch_bounds__(256) void act_q8k_kernel(const float* __restrict__ 
 // Q8_0 activation (per 32), planes: 8 lanes per block, 4 values per lane.
 // Also the GGUF-layout Q8_0 weight quantizer (the same from_float).
 // ===========================================================================
-template <bool kVec, bool kGguf>
+// kRuns: the last workgroup of the grid writes a grouped expert product's
+// run table instead (moe_runs.h), so that product needs no launch of its own
+// before the grouped kernel.
+template <bool kVec, bool kGguf, bool kRuns = false>
 __global__ __launch_bounds__(256) void q8_0_kernel(const float* __restrict__ x, int64_t stride, int64_t k,
                                                    int64_t rows, int8_t* __restrict__ codes,
                                                    float* __restrict__ dout, int32_t* __restrict__ sout,
-                                                   uint8_t* __restrict__ gguf) {
+                                                   uint8_t* __restrict__ gguf,
+                                                   const int32_t* __restrict__ expert_ids = nullptr,
+                                                   int size_m = 0, int32_t* __restrict__ runs = nullptr) {
+  if (kRuns && blockIdx.x == gridDim.x - 1) {
+    moe_runs_block<256>(expert_ids, size_m, runs);
+    return;
+  }
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int sub = (int)(gid & 7);
   const int64_t blk = gid >> 3;
@@ -152,6 +162,21 @@ __global__ __launch_bounds__(256) void q8_0_kernel(const float* __restrict__ x, 
       sout[r * nb + b] = s;
     }
   }
+}
+
+hipError_t launch_act_quantize_moe(const float* x, int64_t stride, int64_t k, int64_t rows, void* out,
+                                   const int32_t* expert_ids, int64_t size_m, int32_t* runs, hipStream_t st) {
+  const ActPlanes p = act_planes(ACT_Q8_0, out, k, rows);
+  const bool vec = ((uintptr_t)x % 16 == 0) && (stride % 4 == 0);
+  const int64_t threads = rows * (k / 32) * 8;
+  const dim3 grid((unsigned)((threads + 255) / 256 + 1));  // + the run table's workgroup
+  if (vec)
+    q8_0_kernel<true, false, true><<<grid, 256, 0, st>>>(x, stride, k, rows, p.codes, p.d, (int32_t*)p.sums, nullptr,
+                                                         expert_ids, (int)size_m, runs);
+  else
+    q8_0_kernel<false, false, true><<<grid, 256, 0, st>>>(x, stride, k, rows, p.codes, p.d, (int32_t*)p.sums, nullptr,
+                                                          expert_ids, (int)size_m, runs);
+  return hipGetLastError();
 }
 
 hipError_t launch_act_quantize(int layout, const float* x, int64_t stride, int64_t k, int64_t rows, void* out,

@@ -116,15 +116,83 @@ def test_moe_c4_gpt_oss_shapes():
     assert lib().qmm_moe_launches() >= before + 2
 
 
+def moe_into(stack, xs, x_stride, sorted_ids, expert_ids, topk_w, topk, rows_out, fill=float("nan")):
+    """qmm_moe_forward through the C ABI into an output prefilled with `fill`
+    (rows the routing does not reach keep it)."""
+    L = lib()
+    e, n, k = stack.shape
+    size_m = len(sorted_ids)
+    out = torch.full((rows_out, n), fill, dtype=torch.float32, device=DEV)
+    sid, eid = t32(sorted_ids), t32(expert_ids)
+    tw = t32(topk_w) if topk_w is not None else None
+    need = ctypes.c_size_t(0)
+    args = (int(stack.dtype), stack.data_.data_ptr(), e, xs.data_ptr(), x_stride, sid.data_ptr(), eid.data_ptr(),
+            tw.data_ptr() if tw is not None else None, topk, out.data_ptr(), n)
+    assert L.qmm_moe_forward(*args, None, 0, ctypes.byref(need), k, n, size_m, 0, 0) == 0
+    ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=DEV)
+    assert L.qmm_moe_forward(*args, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, size_m, 1, 0) == 0
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
 def test_moe_order_of_entries_does_not_change_results():
+    """Any order of the routing entries gives the same bits; out of expert
+    order there are more runs than experts, and every one is computed (the
+    output starts as NaN, so a run left out shows)."""
     qtype, E, n, k, tokens, topk = 39, 6, 64, 256, 5, 2
     sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, 7)
     stack = expert_stack(qtype, E, n, k, 77)
-    x = np.random.default_rng(7).standard_normal((tokens, k)).astype(np.float32)
-    ref = moe_forward(t32(x), stack, t32(sorted_ids), t32(expert_ids), None, topk).cpu().numpy()
+    xs = t32(np.random.default_rng(7).standard_normal((tokens, k)).astype(np.float32))
+    ref = moe_into(stack, xs, k, sorted_ids, expert_ids, None, topk, tokens * topk)
+    assert not np.isnan(ref).any()
     perm = np.random.default_rng(8).permutation(len(sorted_ids))
-    got = moe_forward(t32(x), stack, t32(sorted_ids[perm]), t32(expert_ids[perm]), None, topk).cpu().numpy()
+    runs = 1 + int(np.count_nonzero(np.diff(expert_ids[perm])))
+    assert runs > E
+    got = moe_into(stack, xs, k, sorted_ids[perm], expert_ids[perm], None, topk, tokens * topk)
     assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
+
+
+def test_moe_more_runs_than_experts():
+    """Entries alternating between two experts: six runs over two experts."""
+    qtype, E, n, k, topk = 8, 2, 48, 128, 1
+    stack = expert_stack(qtype, E, n, k, 13)
+    x = np.random.default_rng(13).standard_normal((6, k)).astype(np.float32)
+    xs = t32(x)
+    sorted_ids = np.arange(6, dtype=np.int32)
+    expert_ids = np.array([0, 1, 0, 1, 0, 1], np.int32)
+    got = moe_into(stack, xs, k, sorted_ids, expert_ids, None, topk, 6)
+    check_against_oracle(qtype, stack, x, got, sorted_ids, expert_ids, None, topk)
+    check_against_forward(stack, xs, got, sorted_ids, expert_ids, None, topk)
+
+
+@pytest.mark.parametrize("name", ["MXFP4", "Q8_0"])
+def test_moe_prepass_form_matches_one_launch_form(name):
+    """Routings above a decode step's size, and inputs whose rows are not
+    16-byte aligned, take the runs pre-pass and the standalone quantizer;
+    both forms give the same bits, and the large routing matches the oracle
+    and qmm_forward."""
+    qtype = MOE_TYPES[name]
+    E, n, k, topk = 8, 64, 256, 4
+    tokens = 80  # 320 routing entries
+    sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, 21)
+    stack = expert_stack(qtype, E, n, k, 21)
+    x = np.random.default_rng(21).standard_normal((tokens * topk, k)).astype(np.float32)
+    xs = t32(x)
+    big = moe_into(stack, xs, k, sorted_ids, expert_ids, topk_w, topk, tokens * topk)
+    assert not np.isnan(big).any()
+    check_against_forward(stack, xs, big, sorted_ids, expert_ids, topk_w, topk)
+    sel = slice(0, len(sorted_ids), 7)
+    check_against_oracle(qtype, stack, x, big, sorted_ids[sel], expert_ids[sel], topk_w, topk)
+    # a decode-sized routing: the one-launch form, then the same inputs at a
+    # row stride of k + 1 floats (rows not 16-byte aligned): the pre-pass form
+    sid, eid, tw = routing(6, E, topk, 22)
+    x6 = np.random.default_rng(22).standard_normal((6 * topk, k)).astype(np.float32)
+    one = moe_into(stack, t32(x6), k, sid, eid, tw, topk, 6 * topk)
+    padded = np.zeros((6 * topk, k + 1), np.float32)
+    padded[:, :k] = x6
+    two = moe_into(stack, t32(padded), k + 1, sid, eid, tw, topk, 6 * topk)
+    assert not np.isnan(one).any()
+    assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
 
 
 def test_moe_out_of_range_entries_write_nothing():
