@@ -126,11 +126,16 @@ bool stream_supported(int type, int64_t k, int64_t rows) {
 // workgroups (one activation fill per 16 waves): a row per wave up to 16
 // waves a CU; beyond that, about 1.5 rows per wave up to 32 waves a CU, the
 // next row's loads in flight whenever a wave has more than one row.
-qmm::MvShape stream_shape(int64_t n_total) {
+qmm::MvShape stream_shape(int64_t n_total, int64_t k) {
   const int64_t cus = cu_count();
   // a row per wave while the rows fit one 16-wave workgroup a CU (o, 4096
   // rows: 5.5 us against 6.2 us for 2736 waves with the next row in flight)
   if (n_total <= cus * 16) return qmm::MvShape{(n_total + 15) / 16 * 16, 16, false};
+  // Rows of more than 4096 values hold twice the registers: one 16-wave
+  // workgroup a CU is resident, so the grid is one round of cus * 16 waves
+  // with the rows spread over it (8192 rows of 8192: two a wave; 5472 waves
+  // ran as 256 workgroups and then 86 on a third of the GPU).
+  if (k > 4096) return qmm::MvShape{cus * 16, 16, true};
   int64_t waves = n_total * 2 / 3;
   if (waves < 1024) waves = 1024;
   if (waves > cus * 32) waves = cus * 32;
@@ -154,7 +159,7 @@ hipError_t launch_stream_targets(int type, int count, const void* const* w, cons
   t.count = count;
   if (type == qmm::T_Q6_K) return qmm::launch_mv_q6k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), (int)cu_count(), st);
   if (type != qmm::T_Q4_K) return qmm::launch_mv_b32_rows(type, t, k, rows, x, x_stride, pre, (int)cu_count(), st);
-  return qmm::launch_mv_q4k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), stream_shape(end), st);
+  return qmm::launch_mv_q4k_rows(t, k, rows, x, x_stride, pre, q8k_scale(), stream_shape(end, k), st);
 }
 
 }  // namespace
