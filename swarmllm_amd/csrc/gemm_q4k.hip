@@ -87,8 +87,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-__device__ __forceinline__ uint32_t dup16(uint32_t v) { return v | (v << 16); }
-
 __device__ __forceinline__ uint32_t pkmul(uint32_t a, uint32_t s2) {
   const u16x2 x = __builtin_bit_cast(u16x2, a);
   const u16x2 y = __builtin_bit_cast(u16x2, s2);
