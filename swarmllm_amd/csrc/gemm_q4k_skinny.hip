@@ -235,13 +235,18 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q4k_skinny_kernel(MvTargets 
     if (sb0 + 1 < sb1) load_w(pb, sb0 + 1);
     load_a(aa, sb0);
   }
+  // The matrix work runs at a raised wave priority: while the other wave of
+  // a SIMD stages and issues loads, this one's MFMAs and operand work go
+  // first (C5 at 8 rows: 7.27-7.31 -> 7.18 ms a forward).
   auto step_full = [&](Pieces& pc, SkAct<MT>& cur, SkAct<MT>& nxt, int sb) {
     wave_lds_sync();  // the previous super-block's reads are done
     stage_w(pc);
     load_w(pc, sb + 2);
     load_a(nxt, sb + 1);
     wave_lds_sync();
+    __builtin_amdgcn_s_setprio(1);
     compute(cur);
+    __builtin_amdgcn_s_setprio(0);
   };
   auto step_tail = [&](Pieces& pc, SkAct<MT>& cur, SkAct<MT>& nxt, int sb) {
     wave_lds_sync();

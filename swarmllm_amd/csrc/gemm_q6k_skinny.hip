@@ -221,13 +221,16 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
   // it then issues unconditionally (a load issued on one path and not
   // another makes the compiler wait for every load in flight); the last
   // steps follow it, loading only what remains.
+  // the matrix work at a raised wave priority, as in gemm_q4k_skinny.hip
   auto step_full = [&](Pieces& pc, Q6Act<MT>& cur, Q6Act<MT>& nxt, int sb) {
     wave_lds_sync();
     stage_w(pc);
     load_w(pc, sb + 2);
     load_a(nxt, sb + 1);
     wave_lds_sync();
+    __builtin_amdgcn_s_setprio(1);
     compute(cur, sb);
+    __builtin_amdgcn_s_setprio(0);
   };
   auto step_tail = [&](Pieces& pc, Q6Act<MT>& cur, Q6Act<MT>& nxt, int sb) {
     wave_lds_sync();
