@@ -289,7 +289,11 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
       float acc[kMoePairs];
   #pragma unroll
       for (int p = 0; p < kMoePairs; p++) acc[p] = 0.0f;
+      // Staging and the next span's load issue run at a raised wave priority,
+      // the unit arithmetic at the default: a wave's requests go out ahead of
+      // the other waves' vector work (C4's grouped launches 1-2% faster).
       auto step = [&](Span& cur, int64_t sigma) {
+        __builtin_amdgcn_s_setprio(1);
         wave_lds_sync();
   #pragma unroll
         for (int c = 0; c < Span::kLoads; c++) {
@@ -299,6 +303,7 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
         wave_lds_sync();
         const int off = cur.off, blen = cur.len;
         load_next(cur);
+        __builtin_amdgcn_s_setprio(0);
         if (sigma >= S) return;
         if (bl < blen) {
           const bool two = bl + 1 < blen;
