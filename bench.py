@@ -165,14 +165,27 @@ class Replayer:
             self.graphs[count] = capture(fn, self.stream)
         return self.graphs[count]
 
+    def prepare(self, steps: int) -> None:
+        """Capture every graph run(steps) replays, so that no capture (and
+        none of the synchronisation capture does) falls inside a timed
+        region."""
+        C = len(self.layers)
+        full, rem = divmod(steps, C)
+        if full:
+            self.graph(C)
+        if rem:
+            self.graph(rem)
+
     def run(self, steps: int) -> None:
         C = len(self.layers)
         full, rem = divmod(steps, C)
-        g = self.graph(C) if full else None
+        if (full and C not in self.graphs) or (rem and rem not in self.graphs):
+            raise RuntimeError("Replayer.run: call prepare(steps) first (no capture inside a timed run)")
+        g = self.graphs[C] if full else None
         for _ in range(full):
             g.replay()
         if rem:
-            self.graph(rem).replay()
+            self.graphs[rem].replay()
 
 
 def time_gpu(fn, stream) -> float:
@@ -188,6 +201,42 @@ def time_gpu(fn, stream) -> float:
         b.record(stream)
     torch.cuda.synchronize()
     return a.elapsed_time(b)
+
+
+def single_matvec(layers, stream, reps: int) -> dict:
+    """The product BASELINE.json's target names: ONE Q4_K 14336x4096 matvec
+    at M = 1 (the gate projection alone, qmm_forward: one launch that
+    quantizes the activation in LDS), back to back over the layer copies'
+    gate weights in one graph, timed with HIP events on the stream it runs
+    on. Algorithmic bytes = the weight + the f32 activation + the f32 output."""
+    import torch
+
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    x, ws = layers[0].acts["ffn_in"]
+    n, k = 14336, 4096
+    out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    per_graph = 4 * len(layers)
+    need = ctypes.c_size_t(0)
+
+    def fn(st):
+        for i in range(per_graph):
+            lay = layers[i % len(layers)]
+            check("qmm_forward", L.qmm_forward(Q4K, lay.w["gate"].data_.data_ptr(), x.data_ptr(), k, out.data_ptr(),
+                                               n, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 1, 1, st))
+
+    g = capture(fn, stream)
+    kernel = L.qmm_last_kernel().decode()
+    for _ in range(3):
+        g.replay()
+    ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+    launches = reps * per_graph
+    us = ms * 1e3 / launches
+    alg = 14336 * 16 * 144 + 4 * 4096 + 4 * 14336
+    gbs = alg / (us * 1e-6) / 1e9
+    return {"kernel": f"mv_q4k_stream_kernel, one Q4_K 14336x4096 at M=1 ({kernel})", "us": us, "launches": launches,
+            "alg_bytes": alg, "gbs": gbs}
 
 
 def dominant_kernel(layers, outs, stream, reps: int) -> dict:
@@ -288,34 +337,48 @@ def cpu_baseline(layers, budget_s: float) -> dict:
 
     from oracle import qref
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    usable = len(os.sched_getaffinity(0))
+    logical, physical = usable, physical_cores(usable)
     wbs = [{name: np.frombuffer(lay.w[name].data(), np.uint8) for name, _, _, _ in LAYER} for lay in layers]
     xs = {g: layers[0].acts[g][0].cpu().numpy() for g, _, _ in GROUPS}
     shape = {name: (t, n, k) for name, t, n, k in LAYER}
-
-    def one_layer(wb):
-        for g, _, names in GROUPS:
-            for name in names:
-                t, n, _ = shape[name]
-                qref.matmul(t, xs[g], wb[name], n, threads=threads)
-
-    def rotation():
-        for wb in wbs:
-            one_layer(wb)
-
-    rotation()  # warm
-    best, t_end, trials = float("inf"), time.perf_counter() + budget_s, 0
-    while trials < 3 or (time.perf_counter() < t_end and trials < 100):
-        t0 = time.perf_counter()
-        rotation()
-        best = min(best, (time.perf_counter() - t0) / len(wbs))
-        trials += 1
     alg = layer_bytes()["total"]
-    return {"value": round(alg / best / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+
+    def timed(threads: int, seconds: float):
+        def rotation():
+            for wb in wbs:
+                for g, _, names in GROUPS:
+                    for name in names:
+                        t, n, _ = shape[name]
+                        qref.matmul(t, xs[g], wb[name], n, threads=threads)
+
+        rotation()  # warm
+        best, t_end, trials = float("inf"), time.perf_counter() + seconds, 0
+        while trials < 2 or (time.perf_counter() < t_end and trials < 100):
+            t0 = time.perf_counter()
+            rotation()
+            best = min(best, (time.perf_counter() - t0) / len(wbs))
+            trials += 1
+        return best, trials
+
+    # the reference shows decode peaking below the full core count
+    # (src/inference/cpu_pools.rs:3-25): 1, 4, physical/2 and physical threads
+    counts = sorted({c for c in (1, 4, max(1, physical // 2), physical) if c <= usable})
+    sweep = {}
+    for c in counts:
+        if c == physical:
+            continue
+        best, trials = timed(c, budget_s / 4)
+        sweep[str(c)] = {"gbs": round(alg / best / 1e9, 3), "ms_per_layer": round(best * 1e3, 4), "trials": trials}
+    best, trials = timed(physical, budget_s)
+    sweep[str(physical)] = {"gbs": round(alg / best / 1e9, 3), "ms_per_layer": round(best * 1e3, 4), "trials": trials}
+    return {"value": round(alg / best / 1e9, 3), "unit": "GB/s", "cores": physical, "kind": "port",
             "sample": f"C2 decode layer at M=1 (7 products, 138.1 MB of Q4_K/Q6_K weights) rotated over "
                       f"{len(wbs)} copies, oracle/ restatement of candle k_quants::matmul with its AVX2 vec_dot "
-                      f"kernels, {threads} threads, min of {trials} rotations: {best * 1e3:.3f} ms/layer",
-            "cpu": cpu_name(), "logical_cpus": os.cpu_count()}
+                      f"kernels, {physical} threads (one per physical core of the {logical} logical CPUs this "
+                      f"process may use), min of {trials} rotations: {best * 1e3:.3f} ms/layer",
+            "cpu": cpu_name(), "logical_cpus_usable": logical, "physical_cores_usable": physical,
+            "logical_cpus_host": os.cpu_count(), "threads_sweep": sweep}
 
 
 # BASELINE C5: one peer's shard of a Llama-3.3-70B-shaped model, 40 layers
@@ -504,6 +567,18 @@ def profile_only(which: str, layers, outs, stream, reps: int) -> None:
         torch.cuda.synchronize()
         log(f"profile copy: {reps} copies of {COPY_BYTES} bytes")
         return
+    if which == "single":
+        x, ws = layers[0].acts["ffn_in"]
+        n, k = 14336, 4096
+        need = ctypes.c_size_t(0)
+        out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        for i in range(reps):
+            lay = layers[i % len(layers)]
+            check("qmm_forward", L.qmm_forward(Q4K, lay.w["gate"].data_.data_ptr(), x.data_ptr(), k, out.data_ptr(),
+                                               n, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 1, 1, s))
+        torch.cuda.synchronize()
+        log(f"profile single: {reps} Q4_K 14336x4096 M=1 launches over {len(layers)} copies")
+        return
     if which == "dominant":
         x, ws = layers[0].acts["ffn_in"]
         n, k = 14336, 4096
@@ -544,6 +619,27 @@ def measured_traffic(kernel_key: str):
     return None
 
 
+def physical_cores(usable: int) -> int:
+    """Physical cores among the CPUs this process may run on: distinct
+    (package, core) pairs of /proc/cpuinfo over the affinity set, or the
+    usable count when the file does not say."""
+    try:
+        allowed = os.sched_getaffinity(0)
+        cores, cur = set(), {}
+        with open("/proc/cpuinfo") as f:
+            for line in list(f) + [""]:
+                if not line.strip():
+                    if cur.get("processor") is not None and int(cur["processor"]) in allowed and "core id" in cur:
+                        cores.add((cur.get("physical id", "0"), cur["core id"]))
+                    cur = {}
+                    continue
+                key, _, val = line.partition(":")
+                cur[key.strip()] = val.strip()
+        return max(1, min(len(cores), usable)) if cores else usable
+    except (OSError, ValueError):
+        return usable
+
+
 def cpu_name() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -565,7 +661,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="skip the C1 / C4 / C5 sections")
-    ap.add_argument("--profile", choices=["dominant", "prefill", "copy"],
+    ap.add_argument("--profile", choices=["single", "dominant", "prefill", "copy"],
                     help="launch only this kernel --steps times (for rocprofv3 counter passes), print no JSON")
     args = ap.parse_args()
 
@@ -603,20 +699,25 @@ def main() -> int:
         return 0
 
     rep = Replayer(layers, outs, stream)
+    rep.prepare(args.warmup)
+    rep.prepare(args.steps)
     with torch.cuda.stream(stream):
         rep.run(args.warmup)
     torch.cuda.synchronize()
-    log(f"warmup {args.warmup} steps done")
+    log(f"warmup {args.warmup} steps done (graphs for {sorted(rep.graphs)} steps captured before timing)")
 
     wall0 = time.perf_counter()
     ms = time_gpu(lambda: rep.run(args.steps), stream)
     wall = time.perf_counter() - wall0
     ms_per_step = ms / args.steps
     value = lb["total"] / (ms_per_step * 1e-3) / 1e9
-    log(f"timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step (wall {wall * 1e3 / args.steps:.2f} us/step)")
+    log(f"timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step "
+        f"(host wall clock around the timed region {wall * 1e6 / args.steps:.2f} us/step)")
 
-    dk = dominant_kernel(layers, outs, stream, args.kernel_reps)
-    log(f"dominant kernel: {dk['us']:.3f} us/launch, {dk['gbs']:.1f} GB/s")
+    dk = single_matvec(layers, stream, args.kernel_reps)
+    log(f"roofline kernel (one Q4_K 14336x4096 matvec): {dk['us']:.3f} us/launch, {dk['gbs']:.1f} GB/s")
+    gu = dominant_kernel(layers, outs, stream, args.kernel_reps)
+    log(f"gate+up launch: {gu['us']:.3f} us/launch, {gu['gbs']:.1f} GB/s")
 
     pre = prefill_gemm(layers, stream, max(2, args.kernel_reps // 5))
     log(f"prefill GEMM: {pre['us_per_launch']:.2f} us/launch, {pre['tops']:.1f} TOP/s")
@@ -649,9 +750,12 @@ def main() -> int:
                    "rows": 1, "layer_bytes": lb["total"], "weight_copies": args.copies,
                    "percent_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(dk["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gate_up"),
+                     "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic("gate"),
                      "kernel": dk["kernel"], "us_per_launch": round(dk["us"], 4),
                      "alg_bytes_per_launch": dk["alg_bytes"]},
+        "gate_up": {"kernel": gu["kernel"], "us_per_launch": round(gu["us"], 4), "alg_bytes_per_launch": gu["alg_bytes"],
+                    "gbs": round(gu["gbs"], 2), "frac": round(gu["gbs"] / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic("gate_up")},
         "cpu_baseline": cpu,
         "prefill": pre,
         **extra,

@@ -195,6 +195,12 @@ uint64_t qmm_matvec_launches(void);
 uint64_t qmm_gemm_launches(void);
 uint64_t qmm_moe_launches(void);
 
+/* The launcher of the last kernel this library enqueued, with its template
+ * arguments (a static string, "" before any launch): which instantiation
+ * served a product, as the reference's tests read mmq_mma_products
+ * (quantized/cuda.rs:937-945). Process-wide; the last writer wins. */
+const char *qmm_last_kernel(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,7 @@ SIGNATURES = {
     "qmm_matvec_launches": (_U64, []),
     "qmm_gemm_launches": (_U64, []),
     "qmm_moe_launches": (_U64, []),
+    "qmm_last_kernel": (ctypes.c_char_p, []),
 }
 
 _lib = None

@@ -405,6 +405,7 @@ bool gemm_q4k_fits(int64_t n, int64_t k, int64_t rows) {
 
 hipError_t launch_gemm_q4k(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
                            int64_t ldd, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
   // 256-column tiles where they give the grid at least one workgroup per
   // CU-sized share, 128-column tiles otherwise
   const int64_t mt = (rows + BM - 1) / BM;

@@ -302,6 +302,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q4k_skinny_kernel(MvTargets 
 
 template <int MT, int NB, int W>
 hipError_t launch_sk(const MvTargets& t, int nsb, const ActPlanes& p, int64_t rows, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
   const int64_t n_total = t.row_end[t.count - 1];
   const dim3 grid((unsigned)((n_total + 16 * NB - 1) / (16 * NB)));
   gemm_q4k_skinny_kernel<MT, NB, W><<<grid, 64 * W, 0, st>>>(t, nsb, p.codes, p.d, (int)rows);

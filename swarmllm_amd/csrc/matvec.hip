@@ -254,6 +254,7 @@ int matvec_max_rows() { return 8; }
 template <int NR>
 static hipError_t launch_nr(int type, const void* w, int64_t n, int64_t k, const ActPlanes& p, float* dst,
                             int64_t ldd, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
   const uint8_t* W = (const uint8_t*)w;
   if (type == T_Q4_K || type == T_Q6_K) {
     const int nsb = (int)(k / 256);

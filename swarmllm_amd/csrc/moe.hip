@@ -364,6 +364,7 @@ template <int FMT>
 hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                         const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                         float* dst, int64_t ldd, int cus, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
   const int nb = (int)(k / 32);
   const int64_t estride = n * nb * Fmt32<FMT>::B;
   const int64_t gy = size_m < num_experts ? size_m : num_experts;
@@ -393,6 +394,7 @@ template <int FMT>
 hipError_t launch_moe_fmt(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                           const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                           float* dst, int64_t ldd, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
   constexpr int RPW = 2;
   const int nb = (int)(k / 32);
   const int64_t estride = n * nb * Fmt32<FMT>::B;

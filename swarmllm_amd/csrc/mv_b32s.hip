@@ -245,6 +245,7 @@ __global__ __launch_bounds__(1024) void mv_b32_stream_kernel(MvTargets tg, int n
 template <int FMT, int NR>
 hipError_t launch_b32s(const MvTargets& t, int nb, const float* x, int64_t xstride, const ActPlanes* pre, int cus,
                        hipStream_t st) {
+  QMM_NOTE_LAUNCH();
   const int64_t n_total = t.row_end[t.count - 1];
   int64_t waves = (int64_t)cus * 16;
   // every wave the same number of rows (the last ones one fewer)

@@ -240,6 +240,7 @@ inline bool q4k_xchg(int nsb) { return nsb <= 16; }
 template <int NR, int T, int WPG, bool PF, bool XCHG>
 hipError_t launch_stream_x(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
                            float qmax, int64_t waves, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
   const size_t lds = act_lds_bytes(NR, nsb) + (XCHG ? (size_t)WPG * 144 * nsb : 0);
   const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
   if (pre) {

@@ -231,6 +231,7 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
 template <int NR>
 hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xstride, const ActPlanes* pre,
                          float qmax, int cus, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
   const int64_t n_total = t.row_end[t.count - 1];
   if (n_total >= ((int64_t)1 << 30)) return hipErrorInvalidValue;  // row numbers are ints in the kernel
   int waves = cus * 16;

@@ -164,7 +164,16 @@ hipError_t launch_stream_targets(int type, int count, const void* const* w, cons
 
 }  // namespace
 
+namespace qmm {
+namespace {
+std::atomic<const char*> g_last_kernel{""};
+}
+void note_launch(const char* what) { g_last_kernel.store(what, std::memory_order_relaxed); }
+}  // namespace qmm
+
 extern "C" {
+
+const char* qmm_last_kernel(void) { return qmm::g_last_kernel.load(std::memory_order_relaxed); }
 
 int qmm_available(void) {
   static std::mutex mu;

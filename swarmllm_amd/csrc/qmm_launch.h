@@ -8,6 +8,12 @@
 
 namespace qmm {
 
+// The name of the last kernel launcher this library ran (its signature with
+// template arguments), read by qmm_last_kernel: the evidence of which kernel
+// instantiation served a product.
+void note_launch(const char* what);
+#define QMM_NOTE_LAUNCH() ::qmm::note_launch(__PRETTY_FUNCTION__)
+
 // ---- activation layouts on the device --------------------------------------
 // The codes, scales and sums are bit-for-bit those of candle's BlockQ8K /
 // BlockQ8_0 from_float; only their placement differs: planes, 16-B aligned.
