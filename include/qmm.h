@@ -121,6 +121,19 @@ int qmm_forward(int type, const void *w, const float *x, int64_t x_stride, float
                 void *workspace, size_t workspace_bytes, size_t *need, int64_t k, int64_t n, int64_t rows,
                 int launch, int64_t stream);
 
+/* qmm_forward without a workspace: the activation scratch is a 16 MiB
+ * device array the library holds per GPU until the process ends
+ * (qmm_forward_noalloc_max_bytes()). No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); the entry
+ * point itself allocates nothing. Products whose planned workspace exceeds
+ * the scratch return QMM_WORKSPACE_TOO_SMALL with nothing enqueued. All
+ * calls on one GPU share the scratch: calls that overlap on one GPU (other
+ * streams, other threads) race on it. Results equal qmm_forward's bit for bit. */
+int qmm_forward_noalloc(int type, const void *w, const float *x, int64_t x_stride, float *dst, int64_t ldd,
+                        int64_t k, int64_t n, int64_t rows, int64_t stream);
+size_t qmm_forward_noalloc_max_bytes(void);
+
 /* dst[i] = x · W[i]ᵀ for `count` weights of one type and the same k that
  * share the activation x (rows x k f32, `x_stride` floats apart): the
  * activation is quantized once for all of them. Weight i has n[i] rows and

@@ -51,6 +51,8 @@ SIGNATURES = {
     "qmm_gemm_launches": (_U64, []),
     "qmm_moe_launches": (_U64, []),
     "qmm_last_kernel": (ctypes.c_char_p, []),
+    "qmm_forward_noalloc": (_I, [_I, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64]),
+    "qmm_forward_noalloc_max_bytes": (_SZ, []),
 }
 
 _lib = None
