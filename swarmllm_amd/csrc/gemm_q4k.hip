@@ -44,6 +44,7 @@
 //     workgroup's threads and written to LDS (2.5 KB).
 // Rows past M or N are read as the last row (valid memory); their outputs
 // are never stored.
+#include "lds_copy.h"
 #include "qmm_device.h"
 #include "qmm_launch.h"
 
@@ -60,32 +61,6 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int BM = 128;  // rows of a workgroup tile
-
-// One global-to-LDS copy of 16 bytes a lane (global_load_lds_dwordx4): lane
-// L's 16 bytes at base + off[L] land at LDS byte lds + 16 L (lds uniform,
-// through M0, which is restored). Written as inline assembly: the compiler
-// counts its own form of this load among the LDS operations, in a way it
-// cannot order against them, and then waits for every LDS read with
-// lgkmcnt(0) for the rest of the super-block (the A fragments read a step
-// ahead were waited for at once). The kernel waits for the copies itself
-// (vmcnt(0) before the barrier that ends the super-block); the copies write
-// only the buffer half no wave reads until then.
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(off), "s"(base), "s"(lds)
-      : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
 
 __device__ __forceinline__ uint32_t pkmul(uint32_t a, uint32_t s2) {
   const u16x2 x = __builtin_bit_cast(u16x2, a);

@@ -1,0 +1,409 @@
+// gemm_q4k_sp.hip — Q4_K prefill GEMM in ONE int8 matrix-core pass (gfx950).
+//
+// dst[m][n] = sum over super-blocks of  d_n dy_m sum_j sc_nj sum_{i in j} q_ni y_mi
+//                                      - dmin_n dy_m sum_j m_nj S_mj
+// is candle's Q4_K x Q8_K vec_dot (vendor/candle/candle-core/src/quantized/
+// k_quants.rs:2031-2111) against the activation quantized as the reference
+// quantizes it for Q4_K (BlockQ8K::from_float, :2882-2927): per-256 scale
+// dy_m, int8 codes y, S_mj the code sum of 32-value sub-block j.
+//
+// One pass instead of two. sc*q needs 10 bits and an int8 operand holds 8,
+// so the weight enters the matrix cores as
+//     w8 = floor((sc (q - 8) + 2) / 4)   in [-126, 110],
+// sc (q - 8) rounded to a multiple of 4. Then
+//     sum_j sc_j sum q y  ~=  4 sum w8 y  +  8 sum_j sc_j S_j ,
+// where the second sum (the -8 offset) is exact and joins the min term in
+// one f16 product per super-block:
+//     sum_j S_j * (8 d sc_j - dmin m_j)   (A = dy S_j, B = 8 d sc_j - dmin m_j).
+// The rounding of sc (q - 8) (|error| <= 2 of a code step of 4) is the
+// kernel's one approximation beyond the f16 operands of that product; the
+// normalised error |y - y_ref| / (||w|| ||x||) stays near 4e-4 at most on C3
+// with its outlier channels, inside the 2e-3 bound of the GEMM.
+//
+// Integer accumulators start at the bits of 1.5 * 2^23, so after a
+// super-block's eight MFMAs each holds the f32 1.5 * 2^23 + T exactly
+// (|T| < 2^22); the epilogue folds it with one fma, acc += (1.5 2^23 + T) s,
+// and the same f16 product that carries the min term subtracts
+// 1.5 * 2^23 * s (its spare K slots, s = 4 d dy as two f16 halves x d).
+//
+// Each row's activation scales are divided by a power of two 2^e_m (the
+// largest |dy| of the row in [0.5, 1)), which keeps the f16 operands of the
+// per-super-block product in range for activations of any size; the output
+// is multiplied back by 2^e_m (exact).
+//
+// Data movement (workgroup: 8 waves, 256 rows x 128 weight rows, each wave
+// 64 x 64 as 2 x 2 tiles of v_mfma_i32_32x32x32_i8):
+//   - K is staged 128 values (half a super-block) at a time. The activation
+//     codes of the stage (256 rows x 128 B) and the raw Q4_K bytes of the
+//     super-block (128 rows x 144 B) reach LDS by direct global-to-LDS copies,
+//     one stage ahead into the other half of double buffers.
+//   - The workgroup's 512 threads turn the next stage's raw nibbles into int8
+//     w8 in LDS (each thread 32 values: four packed 16-bit multiply-adds per
+//     8 values, then a byte permute), beside the current stage's MFMAs. The
+//     weights are expanded once per 256 activation rows.
+//   - The f16 product operands, dy and d of a super-block are written to LDS
+//     by the threads during its first half and read by its epilogue.
+// Rows past M and weight rows past N are read as the last row (valid
+// memory); their outputs are never stored.
+#include "lds_copy.h"
+#include "qmm_device.h"
+#include "qmm_launch.h"
+
+namespace qmm {
+
+namespace {
+
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i16v __attribute__((ext_vector_type(16)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kBM = 256, kBN = 128;  // workgroup tile: activation rows x weight rows
+constexpr int kThreads = 512;        // 8 waves: 4 (rows) x 2 (weight rows), 64 x 64 each
+constexpr int kStage = 128;          // K values a stage (half a super-block)
+constexpr uint32_t kMagic = 0x4B400000u;  // bits of 1.5 * 2^23
+constexpr float kMagicF = 12582912.0f;
+// exponent shift of the f16 operands: A carries 2^-8, B 2^8
+constexpr float kToA = 1.0f / 256.0f, kToB = 256.0f;
+
+__device__ __forceinline__ uint32_t pkmad(uint32_t a, uint32_t b, uint32_t c) {
+  const u16x2 x = __builtin_bit_cast(u16x2, a), y = __builtin_bit_cast(u16x2, b), z = __builtin_bit_cast(u16x2, c);
+  return __builtin_bit_cast(uint32_t, x * y + z);
+}
+
+__device__ __forceinline__ uint32_t word(const uint4& c, int e) {
+  return e == 0 ? c.x : e == 1 ? c.y : e == 2 ? c.z : c.w;
+}
+
+// A staged tile keeps 128 bytes a row; its 16-byte piece p of row r sits at
+// piece p ^ swz(r), so the 16 rows one 16-lane group of an MFMA operand read
+// (rows r0 .. r0+15, one piece each) cover the 64 LDS banks once.
+__device__ __forceinline__ uint32_t swz(uint32_t r) { return (r >> 1) & 7u; }
+
+// 2^-e with |v| in [2^(e-1), 2^e) for the largest |v| of a row: the factor
+// that brings the row's scales into [0.5, 1); 1 for a zero or non-finite row.
+__device__ __forceinline__ float row_factor(float maxabs) {
+  const uint32_t E = (__builtin_bit_cast(uint32_t, maxabs) >> 23) & 0xFFu;
+  if (maxabs == 0.0f || E == 0xFFu) return 1.0f;
+  const int fe = 253 - (int)E;  // biased exponent of 2^(126 - E)
+  return __builtin_bit_cast(float, (uint32_t)(fe < 1 ? 1 : (fe > 254 ? 254 : fe)) << 23);
+}
+
+__global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const uint8_t* __restrict__ W, int64_t N, int nsb,
+                                                                  const int8_t* __restrict__ yq,
+                                                                  const float* __restrict__ yd,
+                                                                  const int16_t* __restrict__ ybs, int64_t M,
+                                                                  float* __restrict__ dst, int64_t ldd, int mtiles,
+                                                                  int remap) {
+  // Each half of each double buffer is its own object and the stage loop is
+  // unrolled over two super-blocks, so every access names its buffer
+  // statically (the compiler can tell reads of one half from writes of the other).
+  __shared__ __attribute__((aligned(16))) int8_t s_a0[kBM * kStage], s_a1[kBM * kStage];
+  __shared__ __attribute__((aligned(16))) int8_t s_b0[kBN * kStage], s_b1[kBN * kStage];
+  __shared__ __attribute__((aligned(16))) uint8_t s_w0[kBN * 144], s_w1[kBN * 144];
+  __shared__ __attribute__((aligned(16))) _Float16 s_rop[kBM][16];  // f16 product A operands of a super-block
+  __shared__ __attribute__((aligned(16))) _Float16 s_cop[kBN][16];  // and B operands
+  __shared__ __attribute__((aligned(16))) float s_dy[kBM];          // dy_m 2^-e_m
+  __shared__ __attribute__((aligned(16))) float s_d4[kBN];          // 4 d_n
+  __shared__ __attribute__((aligned(16))) float s_rf[kBM];          // 2^-e_m
+  // a super-block's activation sums (bsums) and scales, copied one stage
+  // ahead of the stage that turns them into the f16 operands
+  __shared__ __attribute__((aligned(16))) int16_t s_bsr[kBM * 16];
+  __shared__ __attribute__((aligned(16))) float s_ydr[kBM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv & 3, wn = wv >> 2;
+  const int h = lane >> 5, r32 = lane & 31;
+
+  // workgroup -> tile; the row tiles of one weight tile on one XCD (its L2)
+  const int total = (int)gridDim.x;
+  const int b = (int)blockIdx.x;
+  const int idx = remap ? (b & 7) * (total >> 3) + (b >> 3) : b;
+  const int64_t m0 = (int64_t)(idx % mtiles) * kBM;
+  const int64_t n0 = (int64_t)(idx / mtiles) * kBN;
+
+  const int64_t K = (int64_t)nsb * 256;
+  const uint32_t rowbytes = (uint32_t)nsb * 144;
+
+  // ---- per-lane byte offsets of the copies (stage 0 / super-block 0) ----
+  // activation: 32 copies a stage, 8 rows each; wave wv takes copies wv + 8u
+  // Copy u of this wave moves rows 64u + 8wv .. +7; lane L row 64u + 8wv +
+  // L/8 (the swizzle of a row is the same 64 rows on), clamped to M - 1.
+  const uint32_t arow_l = 8u * (uint32_t)wv + ((uint32_t)lane >> 3);
+  const uint32_t a_rowk = (uint32_t)((m0 + arow_l) * K);  // < 2^31: rows + 256 rows of k
+  const uint32_t a_lastk = (uint32_t)((M - 1) * K);
+  const uint32_t a_piece = 16u * (((uint32_t)lane & 7u) ^ swz(arow_l));
+  auto aoff = [&](int u) -> uint32_t {
+    const uint32_t rk = a_rowk + (uint32_t)(64 * u) * (uint32_t)K;
+    return (rk < a_lastk ? rk : a_lastk) + a_piece;
+  };
+  // weights: 18 copies a super-block (128 rows x 9 pieces), copy i = wv + 8u
+  uint32_t woff[3];
+#pragma unroll
+  for (int u = 0; u < 3; u++) {
+    const uint32_t i = (uint32_t)(wv + 8 * u);
+    const uint32_t f = 64u * (i < 18u ? i : 17u) + (uint32_t)lane;
+    const uint32_t col = (f * 7282u) >> 16;  // f / 9 for f < 2^14
+    const int64_t gc = n0 + col < N ? n0 + col : N - 1;
+    woff[u] = (uint32_t)gc * rowbytes + 16u * (f - 9u * col);
+  }
+  // the per-super-block row inputs: bsums (32 bytes a row, 8 copies, one a
+  // wave) and dy (4 bytes a row, 4 dword copies, waves 0-3)
+  const uint32_t bsr = 32u * (uint32_t)wv + ((uint32_t)lane >> 1);
+  const int64_t bsrow = m0 + bsr < M ? m0 + bsr : M - 1;
+  const uint32_t bsoff = (uint32_t)(bsrow * (K / 16) * 2) + 16u * ((uint32_t)lane & 1u);
+  const uint32_t ydr = 64u * (uint32_t)(wv & 3) + (uint32_t)lane;
+  const int64_t ydrow = m0 + ydr < M ? m0 + ydr : M - 1;
+  const uint32_t ydoff = (uint32_t)(ydrow * nsb) * 4u;
+  auto dma_a1 = [&](int g, int8_t* sa, int u) {
+    dma16(yq + 128 * (int64_t)g, aoff(u), lds_addr(sa + 1024 * (wv + 8 * u)));
+  };
+  auto dma_w1 = [&](int sb, uint8_t* sw, int u) {
+    if (wv + 8 * u < 18) dma16(W + 144 * (int64_t)sb, woff[u], lds_addr(sw + 1024 * (wv + 8 * u)));
+  };
+  auto dma_rows = [&](int sb, int part) {
+    if (part == 0)
+      dma16((const uint8_t*)ybs + 32 * (int64_t)sb, bsoff, lds_addr((uint8_t*)s_bsr + 1024 * wv));
+    else if (wv < 4)
+      dma4(yd + sb, ydoff, lds_addr(s_ydr + 64 * wv));
+  };
+
+  // ---- expansion of a stage's weights: thread -> (weight row, piece) ----
+  const int bn = tid & (kBN - 1), bpi = tid >> 7;  // 16 consecutive lanes: 16 rows, one piece
+  auto build = [&](const uint8_t* sw, int half, int8_t* sbt) {
+    const uint8_t* wr = sw + bn * 144;
+    const uint4 hdr = *(const uint4*)wr;
+    const uint4 raw = *(const uint4*)(wr + 16 * (1 + 4 * half + bpi));
+    // 6-bit scales of sub-blocks 4 half + 2 (bpi >> 1) and the next
+    // (get_scale_min_k4, vendor/candle/candle-core/src/quantized/utils.rs:50-60)
+    const uint32_t scw = half == 0 ? (hdr.y & 0x3f3f3f3fu)
+                                   : ((hdr.w & 0x0f0f0f0fu) | (((hdr.y >> 6) & 0x03030303u) << 4));
+    const uint32_t sw2 = scw >> (16 * (bpi >> 1));
+    const uint32_t sc0 = sw2 & 0xFFu, sc1 = (sw2 >> 8) & 0xFFu;
+    // per 16-bit lane: 64 sc (q - 8) + 128, whose high byte is w8
+    const uint32_t mlo = (64u * sc0) * 0x10001u, blo = ((128u - 512u * sc0) & 0xFFFFu) * 0x10001u;
+    const uint32_t mhi = (4u * sc1) * 0x10001u, bhi = ((128u - 512u * sc1) & 0xFFFFu) * 0x10001u;
+    uint4 olo, ohi;
+    uint32_t* lo = (uint32_t*)&olo;
+    uint32_t* hi = (uint32_t*)&ohi;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t D = word(raw, e), D8 = D >> 8;
+      const uint32_t el = pkmad(D & 0x000F000Fu, mlo, blo), ol = pkmad(D8 & 0x000F000Fu, mlo, blo);
+      const uint32_t eh = pkmad(D & 0x00F000F0u, mhi, bhi), oh = pkmad(D8 & 0x00F000F0u, mhi, bhi);
+      lo[e] = __builtin_amdgcn_perm(ol, el, 0x07030501u);
+      hi[e] = __builtin_amdgcn_perm(oh, eh, 0x07030501u);
+    }
+    const uint32_t plo = 4u * ((uint32_t)bpi >> 1) + ((uint32_t)bpi & 1u);
+    int8_t* rowp = sbt + bn * kStage;
+    *(uint4*)(rowp + 16 * (plo ^ swz(bn))) = olo;
+    *(uint4*)(rowp + 16 * ((plo + 2u) ^ swz(bn))) = ohi;
+  };
+
+  // ---- per-super-block scales: rows (threads 0-255), weight rows (256-383) ----
+  const int64_t prow = m0 + (tid & 255) < M ? m0 + (tid & 255) : M - 1;
+  auto prep = [&](const uint8_t* sw) {
+    if (tid < 256) {
+      const float dy = s_ydr[tid] * s_rf[tid];
+      const uint4 pbs0 = *(const uint4*)&s_bsr[16 * tid], pbs1 = *(const uint4*)&s_bsr[16 * tid + 8];
+      h8 a, c = {};
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint32_t wd = word(j < 4 ? pbs0 : pbs1, j & 3);
+        const int s = (int)(int16_t)(wd & 0xFFFFu) + (int)(int16_t)(wd >> 16);
+        a[j] = (_Float16)(dy * (float)s * kToA);
+      }
+      const float v = -kMagicF * dy * kToA;
+      const _Float16 vh = (_Float16)v;
+      c[0] = vh;
+      c[1] = (_Float16)(v - (float)vh);
+      *(h8*)&s_rop[tid][0] = a;
+      *(h8*)&s_rop[tid][8] = c;
+      s_dy[tid] = dy;
+    } else if (tid < 256 + kBN) {
+      const int n = tid - 256;
+      const uint4 hdr = *(const uint4*)(sw + n * 144);
+      const uint32_t u0 = hdr.y, u1 = hdr.z, u2 = hdr.w;
+      const uint32_t s03 = u0 & 0x3f3f3f3fu, m03 = u1 & 0x3f3f3f3fu;
+      const uint32_t s47 = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+      const uint32_t m47 = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+      const float d = h2f((uint16_t)(hdr.x & 0xFFFFu)), dmin = h2f((uint16_t)(hdr.x >> 16));
+      h8 bq, c = {};
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint32_t sc = ((j < 4 ? s03 : s47) >> (8 * (j & 3))) & 0xFFu;
+        const uint32_t mn = ((j < 4 ? m03 : m47) >> (8 * (j & 3))) & 0xFFu;
+        bq[j] = (_Float16)((8.0f * d * (float)sc - dmin * (float)mn) * kToB);
+      }
+      const _Float16 d4 = (_Float16)(4.0f * d * kToB);  // exact: 4 d 2^8 of an f16 d
+      c[0] = d4;
+      c[1] = d4;
+      *(h8*)&s_cop[n][0] = bq;
+      *(h8*)&s_cop[n][8] = c;
+      s_d4[n] = 4.0f * d;
+    }
+  };
+
+  // ---- accumulators ----
+  i16v T[2][2];
+  f16v acc[2][2];
+  i16v magic;
+#pragma unroll
+  for (int i = 0; i < 16; i++) magic[i] = (int)kMagic;
+#pragma unroll
+  for (int a = 0; a < 2; a++)
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[a][c][i] = 0.0f;
+
+  // the lane's operand rows within the staged tiles
+  const int arow0 = 64 * wm + r32, arow1 = arow0 + 32;
+  const int bcol0 = 64 * wn + r32, bcol1 = bcol0 + 32;
+  auto frag = [&](const int8_t* base, int row, int ks) -> i4v {
+    return *(const i4v*)(base + row * kStage + 16 * ((uint32_t)(2 * ks + h) ^ swz(row)));
+  };
+
+  // ---- prologue: row factors, stage 0 ----
+#pragma unroll
+  for (int u = 0; u < 4; u++) dma_a1(0, s_a0, u);
+#pragma unroll
+  for (int u = 0; u < 3; u++) dma_w1(0, s_w0, u);
+  dma_rows(0, 0);
+  dma_rows(0, 1);
+  if (tid < 256) {
+    float mx = 0.0f;
+    for (int sb = 0; sb < nsb; sb++) mx = fmaxf(mx, fabsf(yd[prow * nsb + sb]));
+    s_rf[tid] = row_factor(mx);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  build(s_w0, 0, s_b0);
+  __syncthreads();
+
+  // One stage: MFMAs on (sa, sbt); the next stage's weights expanded into
+  // nbt from nw (half nhalf) and its activation copied into na; on the first
+  // half of a super-block, the next super-block's raw weights copied into
+  // wnext and this super-block's scales prepared from wcur; on the second
+  // half, the epilogue.
+  auto stage = [&](int sb, int half, const int8_t* sa, const int8_t* sbt, int8_t* na, int8_t* nbt,
+                   const uint8_t* nw, int nhalf, const uint8_t* wcur, uint8_t* wnext) {
+    const int g = 2 * sb + half;
+    const bool more = g + 1 < 2 * nsb;
+    const bool wmore = half == 0 && sb + 1 < nsb;  // the next super-block's raw weights
+    const bool rmore = half == 1 && sb + 1 < nsb;  // the next super-block's row inputs
+    i4v a0 = frag(sa, arow0, 0), a1 = frag(sa, arow1, 0);
+    i4v b0 = frag(sbt, bcol0, 0), b1 = frag(sbt, bcol1, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+      const bool first = half == 0 && ks == 0;
+      T[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, first ? magic : T[0][0], 0, 0, 0);
+      T[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, first ? magic : T[0][1], 0, 0, 0);
+      T[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, first ? magic : T[1][0], 0, 0, 0);
+      T[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, first ? magic : T[1][1], 0, 0, 0);
+      // The next K-step's fragments into the same registers: an MFMA reads
+      // its operands when it issues, so the reads overlap the four MFMAs
+      // without a second register set.
+      if (ks < 3) {
+        a0 = frag(sa, arow0, ks + 1);
+        a1 = frag(sa, arow1, ks + 1);
+        b0 = frag(sbt, bcol0, ks + 1);
+        b1 = frag(sbt, bcol1, ks + 1);
+      }
+      // this K-step's share of the next stage's copies
+      if (more) dma_a1(g + 1, na, ks);
+      if (wmore && ks < 3) dma_w1(sb + 1, wnext, ks);
+      if (rmore && ks < 2) dma_rows(sb + 1, ks);
+      if (ks == 1 && more) build(nw, nhalf, nbt);
+    }
+    if (half == 0) {
+      prep(wcur);
+    } else {
+      // epilogue of super-block sb: the f16 product (min term, offset, and
+      // the magic correction), then acc += (1.5 2^23 + T) * 4 d dy
+      const h8 ra0 = *(const h8*)&s_rop[arow0][8 * h], ra1 = *(const h8*)&s_rop[arow1][8 * h];
+      const h8 cb0 = *(const h8*)&s_cop[bcol0][8 * h], cb1 = *(const h8*)&s_cop[bcol1][8 * h];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra0, cb0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra0, cb1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra1, cb0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra1, cb1, acc[1][1], 0, 0, 0);
+      const float d40 = s_d4[bcol0], d41 = s_d4[bcol1];
+#pragma unroll
+      for (int tm = 0; tm < 2; tm++) {
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) {
+          const float4 dy4 = *(const float4*)&s_dy[64 * wm + 32 * tm + 8 * gq + 4 * h];
+          const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            // the element by value: __builtin_bit_cast of a vector element
+            // reads element 0 for every index (clang, ROCm 7.2)
+            const int i = 4 * gq + e;
+            const int t0 = T[tm][0][i], t1 = T[tm][1][i];
+            acc[tm][0][i] = __builtin_fmaf(__int_as_float(t0), dyv[e] * d40, acc[tm][0][i]);
+            acc[tm][1][i] = __builtin_fmaf(__int_as_float(t1), dyv[e] * d41, acc[tm][1][i]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  };
+
+  for (int sb = 0; sb < nsb; sb += 2) {
+    stage(sb, 0, s_a0, s_b0, s_a1, s_b1, s_w0, 1, s_w0, s_w1);
+    stage(sb, 1, s_a1, s_b1, s_a0, s_b0, s_w1, 0, s_w0, s_w1);
+    if (sb + 1 < nsb) {
+      stage(sb + 1, 0, s_a0, s_b0, s_a1, s_b1, s_w1, 1, s_w1, s_w0);
+      stage(sb + 1, 1, s_a1, s_b1, s_a0, s_b0, s_w0, 0, s_w1, s_w0);
+    }
+  }
+
+  // ---- store, the row factor undone (exact powers of two) ----
+#pragma unroll
+  for (int tn = 0; tn < 2; tn++) {
+    const int64_t col = n0 + 64 * wn + 32 * tn + r32;
+    if (col >= N) continue;
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int lr = 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
+        const int64_t row = m0 + lr;
+        if (row < M) dst[row * ldd + col] = acc[tm][tn][i] / s_rf[lr];
+      }
+  }
+}
+
+}  // namespace
+
+constexpr int64_t kSpMinK = 2048;
+
+int gemm_q4k_sp_min_rows() { return 129; }
+
+bool gemm_q4k_sp_fits(int64_t n, int64_t k, int64_t rows) {
+  // The rounding of sc (q - 8) adds an error that shrinks as 1/sqrt(k)
+  // relative to ||w|| ||x||: from k = 2048 it stays within half the 2e-3
+  // bound; shorter rows keep the exact two-pass kernel. 32-bit byte offsets
+  // inside the kernel.
+  return k % 256 == 0 && k >= kSpMinK && n * (k / 256) * 144 < ((int64_t)1 << 31) &&
+         (rows + kBM) * k < ((int64_t)1 << 31) && rows < ((int64_t)1 << 24);
+}
+
+hipError_t launch_gemm_q4k_sp(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
+                              int64_t ldd, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  const int mt = (int)((rows + kBM - 1) / kBM);
+  const int64_t nt = (n + kBN - 1) / kBN;
+  const int64_t total = nt * mt;
+  if (total >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  const int remap = total % 8 == 0 ? 1 : 0;
+  gemm_q4k_sp_kernel<<<dim3((unsigned)total), kThreads, 0, st>>>((const uint8_t*)w, n, (int)(k / 256), p.codes, p.d,
+                                                                 (const int16_t*)p.sums, rows, dst, ldd, mt, remap);
+  return hipGetLastError();
+}
+
+}  // namespace qmm

@@ -114,6 +114,15 @@ bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, i
          qmm::gemm_q4k_fits(n, k, rows);
 }
 
+// From 129 rows the single-pass GEMM (256-row tiles); 33-128 rows keep the
+// exact two-pass kernel, whose 128-row tiles waste less on short batches.
+hipError_t launch_gemm(const void* w, int64_t n, int64_t k, const qmm::ActPlanes& p, int64_t rows, float* dst,
+                       int64_t ldd, hipStream_t st) {
+  if (rows >= qmm::gemm_q4k_sp_min_rows() && qmm::gemm_q4k_sp_fits(n, k, rows))
+    return qmm::launch_gemm_q4k_sp(w, n, k, p, rows, dst, ldd, st);
+  return qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st);
+}
+
 // The streaming decode kernels (Q4_K, Q6_K at 1-2 activation rows).
 bool stream_supported(int type, int64_t k, int64_t rows) {
   if (qmm::mv_b32_rows_supported(type, k, rows)) return true;
@@ -258,7 +267,7 @@ int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd,
 int launch_product(int type, const void* w, int64_t n, int64_t k, const void* xq, const qmm::ActPlanes& p,
                    int layout, int64_t rows, float* dst, int64_t ldd, hipStream_t st) {
   if (gemm_takes(type, w, xq, n, k, rows)) {
-    if (qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
+    if (launch_gemm(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
   }

@@ -129,6 +129,13 @@ bool gemm_q6k_skinny_fits(int64_t k, int64_t rows);
 hipError_t launch_gemm_q6k_skinny(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, int cus,
                                   hipStream_t st);
 
+// The single-pass Q4_K GEMM (gemm_q4k_sp.hip), from gemm_q4k_sp_min_rows()
+// rows: weights rounded into one int8 operand, 256-row tiles.
+int gemm_q4k_sp_min_rows();
+bool gemm_q4k_sp_fits(int64_t n, int64_t k, int64_t rows);
+hipError_t launch_gemm_q4k_sp(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
+                              int64_t ldd, hipStream_t s);
+
 int gemm_q4k_min_rows();
 // The GEMM indexes with 32-bit byte offsets: the weight below 2 GiB and
 // (rows + 128) * k below 2^31.
