@@ -192,6 +192,21 @@ int qmm_quantize_weights(int type, const float *x, void *w, int64_t nelem, void 
 size_t qmm_type_bytes(int type, int64_t nelem);
 int qmm_block_size(int type);
 
+/* The Q8_0 hidden-state wire codec: the bytes in which a layer split sends
+ * activations between the peers holding consecutive layers. Per 32 values
+ * [f16 scale][32 x i8], a partial trailing group zero-padded; the block
+ * maximum skips non-finite values and codes are clamped to [-127, 127].
+ * Bit-exact to the reference's codec.
+ * qmm_wire_bytes: ceil(n / 32) * 34, or 0 when n < 0 or the size would not
+ * fit (q8_0_byte_len_checked, src/inference/quant.rs:98-104).
+ * qmm_wire_encode: replaces quantize_q8_0 (src/inference/quant.rs:24-60);
+ * `out` holds qmm_wire_bytes(n) bytes.
+ * qmm_wire_decode: replaces dequantize_q8_0 (src/inference/quant.rs:65-92);
+ * QMM_UNSUPPORTED (nothing enqueued) when in_bytes != qmm_wire_bytes(n). */
+size_t qmm_wire_bytes(int64_t n);
+int qmm_wire_encode(const float *x, int64_t n, void *out, int64_t stream);
+int qmm_wire_decode(const void *in, size_t in_bytes, int64_t n, float *out, int64_t stream);
+
 /* Fault injection, host side (the reference's fail_the_next_mmq_allocation,
  * quantized/cuda.rs:972-991): the next qmm_forward launch returns
  * QMM_NO_ROOM without enqueuing anything, once. */

@@ -96,6 +96,13 @@ int qref_matmul_upstream(int type, int64_t m, int64_t k, int64_t n, const float 
 /* The activation quantization step of the driver (VecDotType from_float per row). */
 int qref_quantize_rows(int type, int64_t m, int64_t k, const float *x, void *xq, int threads);
 
+/* Q8_0 hidden-state wire codec (src/inference/quant.rs:1-107), qref_wire.c:
+ * bytes of n values (ceil(n/32)*34, -1 if it overflows), encode, decode
+ * (-1 when nbytes is not qref_wire_bytes(n)). */
+int64_t qref_wire_bytes(int64_t n);
+void qref_wire_encode(const float *values, int64_t n, uint8_t *out);
+int qref_wire_decode(const uint8_t *bytes, int64_t nbytes, int64_t n, float *out);
+
 #ifdef __cplusplus
 }
 #endif

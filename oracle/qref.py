@@ -53,6 +53,9 @@ def lib():
         L.qref_matmul_prequantized.restype = I
         L.qref_matmul_upstream.argtypes, L.qref_matmul_upstream.restype = [I, I64, I64, I64, P, P, P], I
         L.qref_quantize_rows.argtypes, L.qref_quantize_rows.restype = [I, I64, I64, P, P, I], I
+        L.qref_wire_bytes.argtypes, L.qref_wire_bytes.restype = [I64], I64
+        L.qref_wire_encode.argtypes, L.qref_wire_encode.restype = [P, I64, P], None
+        L.qref_wire_decode.argtypes, L.qref_wire_decode.restype = [P, I64, I64, P], I
         _lib = L
     return _lib
 
@@ -141,3 +144,26 @@ def f32_to_f16_bits(x: float) -> int:
 
 def f16_bits_to_f32(h: int) -> float:
     return float(lib().qref_f16_to_f32(int(h)))
+
+
+def wire_bytes(n: int) -> int:
+    """q8_0_byte_len_checked (src/inference/quant.rs:98-104): -1 on overflow."""
+    return int(lib().qref_wire_bytes(n))
+
+
+def wire_encode(x: np.ndarray) -> np.ndarray:
+    """quantize_q8_0 (src/inference/quant.rs:24-60): the wire bytes of ``x``."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.zeros(max(wire_bytes(x.size), 0), dtype=np.uint8)
+    if x.size:
+        lib().qref_wire_encode(_p(x), x.size, _p(out))
+    return out
+
+
+def wire_decode(b: np.ndarray, n: int) -> np.ndarray:
+    """dequantize_q8_0 (src/inference/quant.rs:65-92); ValueError on a length mismatch."""
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    if lib().qref_wire_decode(_p(b) if b.size else 0, b.size, n, _p(out) if n else 0) != 0:
+        raise ValueError(f"wire_decode: {b.size} bytes for {n} values")
+    return out

@@ -53,6 +53,9 @@ SIGNATURES = {
     "qmm_last_kernel": (ctypes.c_char_p, []),
     "qmm_forward_noalloc": (_I, [_I, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64]),
     "qmm_forward_noalloc_max_bytes": (_SZ, []),
+    "qmm_wire_bytes": (_SZ, [_I64]),
+    "qmm_wire_encode": (_I, [_P, _I64, _P, _I64]),
+    "qmm_wire_decode": (_I, [_P, _SZ, _I64, _P, _I64]),
 }
 
 _lib = None

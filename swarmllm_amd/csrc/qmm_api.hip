@@ -439,6 +439,28 @@ int qmm_moe_forward(int type, const void* w, int num_experts, const float* x, in
 
 uint64_t qmm_moe_launches(void) { return g_moe_launches.load(std::memory_order_relaxed); }
 
+size_t qmm_wire_bytes(int64_t n) {
+  const int64_t b = qmm::wire_bytes(n);
+  return b < 0 ? 0 : (size_t)b;
+}
+
+int qmm_wire_encode(const float* x, int64_t n, void* out, int64_t stream) {
+  if (n < 0 || qmm::wire_bytes(n) < 0 || (n > 0 && (!x || !out))) return QMM_UNSUPPORTED;
+  if (n == 0) return QMM_OK;
+  clear_stale_error();
+  return status_of(qmm::launch_wire_encode(x, n, out, (hipStream_t)stream));
+}
+
+int qmm_wire_decode(const void* in, size_t in_bytes, int64_t n, float* out, int64_t stream) {
+  // the reference rejects a payload whose length is not the one n values take
+  // (dequantize_q8_0, src/inference/quant.rs:65-77)
+  const int64_t want = qmm::wire_bytes(n);
+  if (want < 0 || (int64_t)in_bytes != want || (n > 0 && (!in || !out))) return QMM_UNSUPPORTED;
+  if (n == 0) return QMM_OK;
+  clear_stale_error();
+  return status_of(qmm::launch_wire_decode(in, n, out, (hipStream_t)stream));
+}
+
 void qmm_fail_next_launch(void) { g_fail_next.store(true); }
 
 int qmm_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float std, int64_t stream) {

@@ -129,6 +129,12 @@ bool gemm_q6k_skinny_fits(int64_t k, int64_t rows);
 hipError_t launch_gemm_q6k_skinny(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, int cus,
                                   hipStream_t st);
 
+// The Q8_0 hidden-state wire codec (wire.hip): bytes of n values (-1 when
+// they would not fit an int64), encode, decode.
+int64_t wire_bytes(int64_t n);
+hipError_t launch_wire_encode(const float* x, int64_t n, void* out, hipStream_t st);
+hipError_t launch_wire_decode(const void* in, int64_t n, float* out, hipStream_t st);
+
 // The single-pass Q4_K GEMM (gemm_q4k_sp.hip), from gemm_q4k_sp_min_rows()
 // rows: weights rounded into one int8 operand, 256-row tiles.
 int gemm_q4k_sp_min_rows();
