@@ -294,38 +294,79 @@ def prefill_inputs(M: int, n: int, k: int):
     return xq, out
 
 
-def prefill_gemm(layers, stream, reps: int) -> dict:
-    """BASELINE C3's headline product: the Q4_K gate projection 14336x4096 at
-    M = 512 (activations N(0,1) with 1% of channels scaled x20), the activation
+def prefill_gemm(layers, stream, reps: int, name: str = "gate") -> dict:
+    """One product of BASELINE C3 alone: the Q4_K gate projection 14336x4096
+    (C3's headline) or the Q6_K down projection 4096x14336 at M = 512
+    (activations N(0,1) with 1% of channels scaled x20), the activation
     quantized once (qmm_quantize_act), then the int8 matrix-core GEMM alone
-    (qmm_matmul) back to back over the layer copies' gate weights in one
-    graph, timed with HIP events on its stream. ops = 2*M*N*K per launch."""
+    (qmm_matmul) back to back over the layer copies' weights in one graph,
+    timed with HIP events on its stream. ops = 2*M*N*K per launch."""
     from swarmllm_amd._lib import check, lib
 
     L = lib()
-    M, n, k = 512, 14336, 4096
+    t, n, k = {nm: (tt, nn, kk) for nm, tt, nn, kk in LAYER}[name]
+    M = 512
     xq, out = prefill_inputs(M, n, k)
     before = L.qmm_gemm_launches()
 
     def fn(st):
         for lay in layers:
-            check("qmm_matmul", L.qmm_matmul(Q4K, lay.w["gate"].data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k,
+            check("qmm_matmul", L.qmm_matmul(t, lay.w[name].data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k,
                                              n, M, st))
 
     graph = capture(fn, stream)
     if L.qmm_gemm_launches() <= before:
         raise RuntimeError("the prefill product did not run the GEMM")
+    kernel = L.qmm_last_kernel().decode()
     for _ in range(2):
         graph.replay()
     ms = time_gpu(lambda: [graph.replay() for _ in range(reps)], stream)
     us = ms * 1e3 / (reps * len(layers))
     ops = 2.0 * M * n * k
     tops = ops / (us * 1e-6) / 1e12
-    return {"workload": "C3: Q4_K gate 14336x4096 at M=512, int8 MFMA GEMM (activation quantized once, Q8_K)",
+    tname = "Q4_K" if t == Q4K else "Q6_K"
+    return {"workload": f"C3: {tname} {name} {n}x{k} at M=512, int8 MFMA GEMM (activation quantized once, Q8_K)",
             "us_per_launch": round(us, 3), "ops_per_launch": int(ops), "tops": round(tops, 2),
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": 5000.0, "unit": "TOP/s",
-                         "frac": round(tops / 5000.0, 4), "kernel": "gemm_q4k_kernel",
-                         "traffic": measured_traffic("prefill_gemm")}}
+                         "frac": round(tops / 5000.0, 4), "kernel": kernel,
+                         "traffic": measured_traffic("prefill_gemm" if name == "gate" else f"prefill_{name}")}}
+
+
+def prefill_layer(layers, stream, reps: int) -> dict:
+    """BASELINE C3 as a whole layer: the C2 layer's 7 products at M = 512
+    (activations N(0,1), 1% of channels x20), launched as a decode step
+    launches them (each shared activation quantized once: qmm_forward_shared
+    for q/k/v and gate/up, qmm_forward for o and down), over the layer copies
+    in one graph, timed with HIP events on its stream.
+    ops = 2 * 512 * sum(n * k) = 223.3 G per layer."""
+    import types
+
+    import torch
+
+    M = 512
+    acts, outs = make_acts(rows=M, config_seed=3)
+    g = torch.Generator().manual_seed(3)
+    for x, _ in acts.values():
+        k = x.shape[1]
+        ch = torch.randperm(k, generator=g)[: k // 100].to(x.device)
+        x[:, ch] *= 20.0
+    views = [types.SimpleNamespace(spec=lay.spec, w=lay.w, acts=acts) for lay in layers]
+
+    def fn(st):
+        for v in views:
+            enqueue_step(v, outs, st, rows=M)
+
+    graph = capture(fn, stream)
+    for _ in range(2):
+        graph.replay()
+    ms = time_gpu(lambda: [graph.replay() for _ in range(reps)], stream)
+    us = ms * 1e3 / (reps * len(layers))
+    ops = 2.0 * M * sum(n * k for _, _, n, k in LAYER)
+    tops = ops / (us * 1e-6) / 1e12
+    return {"workload": "C3: the Llama-3-8B layer's 7 products at M=512 (q/k/v/o/gate/up Q4_K, down Q6_K), "
+                        "activations quantized once per shared input (Q8_K), int8 MFMA GEMMs",
+            "us_per_layer": round(us, 2), "ops_per_layer": int(ops), "tops": round(tops, 2),
+            "frac_of_int8_peak": round(tops / 5000.0, 4)}
 
 
 def cpu_baseline(layers, budget_s: float) -> dict:
@@ -720,7 +761,11 @@ def main() -> int:
     log(f"gate+up launch: {gu['us']:.3f} us/launch, {gu['gbs']:.1f} GB/s")
 
     pre = prefill_gemm(layers, stream, max(2, args.kernel_reps // 5))
-    log(f"prefill GEMM: {pre['us_per_launch']:.2f} us/launch, {pre['tops']:.1f} TOP/s")
+    log(f"prefill GEMM (gate): {pre['us_per_launch']:.2f} us/launch, {pre['tops']:.1f} TOP/s")
+    pre_down = prefill_gemm(layers, stream, max(2, args.kernel_reps // 5), name="down")
+    log(f"prefill GEMM (down): {pre_down['us_per_launch']:.2f} us/launch, {pre_down['tops']:.1f} TOP/s")
+    pre_layer = prefill_layer(layers, stream, max(2, args.kernel_reps // 10))
+    log(f"prefill layer: {pre_layer['us_per_layer']:.2f} us/layer, {pre_layer['tops']:.1f} TOP/s")
 
     extra = {}
     if not args.no_extra:
@@ -758,6 +803,8 @@ def main() -> int:
                     "traffic": measured_traffic("gate_up")},
         "cpu_baseline": cpu,
         "prefill": pre,
+        "prefill_down": pre_down,
+        "prefill_layer": pre_layer,
         **extra,
     }
     print(json.dumps(line), flush=True)

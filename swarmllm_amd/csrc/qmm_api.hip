@@ -106,18 +106,21 @@ hipError_t launch_skinny(int type, const qmm::MvTargets& t, int64_t k, const qmm
   return qmm::launch_gemm_q4k_skinny(t, k, p, rows, (int)cu_count(), st);
 }
 
-// The tiled int8 matrix-core GEMM: Q4_K past the skinny kernel's rows,
-// weight and quantized activation 16-byte aligned (its 16-byte copies),
-// sizes inside its 32-bit offsets.
+// The tiled int8 matrix-core GEMMs: Q4_K and Q6_K past the skinny kernels'
+// rows, weight and quantized activation 16-byte aligned (their 16-byte
+// copies), sizes inside their 32-bit offsets.
 bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows) {
-  return type == qmm::T_Q4_K && rows >= qmm::gemm_q4k_min_rows() && aligned16(w) && aligned16(xq) &&
-         qmm::gemm_q4k_fits(n, k, rows);
+  if (!aligned16(w) || !aligned16(xq)) return false;
+  if (type == qmm::T_Q4_K) return rows >= qmm::gemm_q4k_min_rows() && qmm::gemm_q4k_fits(n, k, rows);
+  if (type == qmm::T_Q6_K) return rows >= qmm::gemm_q6k_min_rows() && qmm::gemm_q6k_fits(n, k, rows);
+  return false;
 }
 
-// From 129 rows the single-pass GEMM (256-row tiles); 33-128 rows keep the
-// exact two-pass kernel, whose 128-row tiles waste less on short batches.
-hipError_t launch_gemm(const void* w, int64_t n, int64_t k, const qmm::ActPlanes& p, int64_t rows, float* dst,
-                       int64_t ldd, hipStream_t st) {
+// Q4_K: from 129 rows the single-pass GEMM (256-row tiles); 33-128 rows keep
+// the exact two-pass kernel, whose 128-row tiles waste less on short batches.
+hipError_t launch_gemm(int type, const void* w, int64_t n, int64_t k, const qmm::ActPlanes& p, int64_t rows,
+                       float* dst, int64_t ldd, hipStream_t st) {
+  if (type == qmm::T_Q6_K) return qmm::launch_gemm_q6k(w, n, k, p, rows, dst, ldd, st);
   if (rows >= qmm::gemm_q4k_sp_min_rows() && qmm::gemm_q4k_sp_fits(n, k, rows))
     return qmm::launch_gemm_q4k_sp(w, n, k, p, rows, dst, ldd, st);
   return qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st);
@@ -267,7 +270,7 @@ int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd,
 int launch_product(int type, const void* w, int64_t n, int64_t k, const void* xq, const qmm::ActPlanes& p,
                    int layout, int64_t rows, float* dst, int64_t ldd, hipStream_t st) {
   if (gemm_takes(type, w, xq, n, k, rows)) {
-    if (launch_gemm(w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
+    if (launch_gemm(type, w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
   }

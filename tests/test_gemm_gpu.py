@@ -1,5 +1,7 @@
-"""The prefill GEMM (int8 matrix cores) against the CPU oracle, through the
-C ABI: qmm_forward at 9 rows and more runs it for Q4_K weights.
+"""The prefill GEMMs (int8 matrix cores) against the CPU oracle, through the
+C ABI: qmm_forward runs them for Q4_K weights from 33 rows (the two-pass
+kernel to 128 rows, the single-pass kernel from 129 rows at k >= 2048) and
+for Q6_K weights from 33 rows; the few-row kernels below 33.
 
 Tolerance (for the MFMA GEMM): max
 |y_gpu - y_cpu| / (||w_j|| * ||x_r||) <= 2e-3. The GEMM multiplies the same
@@ -310,3 +312,83 @@ def test_q6k_skinny_shared_activation_equals_forward():
     shared = QMatMul.forward_shared(x, mats)
     for m, y in zip(mats, shared):
         assert torch.equal(y, m.forward(x))
+
+
+# ---------------------------------------------------------------------------
+# the Q6_K GEMM (from 33 rows): 256 T_h + T_l is four times the reference's
+# exact int32 super-block sum, so the gap to the oracle is again only the
+# order of the f32 scaling
+# ---------------------------------------------------------------------------
+Q6K_GEMM_SHAPES = [  # (k, n, rows): one and many super-blocks; rows of 3, 5, 12 super-blocks (blocks at
+    # every even offset of their windows) and of 8 and 56 (the same offset in every row); row and
+    # weight-row tails; 4- and 8-wave tiles; the XCD remap (tiles % 8 == 0) and without it
+    (256, 70, 33), (768, 300, 40), (1280, 129, 97), (2048, 64, 200), (3072, 4100, 129),
+    (4096, 1000, 300), (14336, 256, 64), (2048, 2048, 512),
+]
+
+
+@pytest.mark.parametrize("k,n,rows", Q6K_GEMM_SHAPES)
+def test_q6k_gemm_parity(k, n, rows):
+    rng = np.random.default_rng(zlib.crc32(f"q6gemm-{k}-{n}-{rows}".encode()))
+    w = weights(rng, n, k)
+    x = activations(rng, rows, k, outliers=True)
+    qt, wq = q6k(w)
+    L = lib()
+    before = L.qmm_gemm_launches()
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert L.qmm_gemm_launches() == before + 1, "the MFMA GEMM did not run"
+    assert "launch_gemm_q6k(" in L.qmm_last_kernel().decode()
+    want = qref.matmul(qref.Q6_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q6_K, wq, n * k).reshape(n, k)
+    err = normalised_error(y, want, wdeq, x)
+    assert err <= TOL_GEMM, f"k={k} n={n} rows={rows}: {err}"
+    assert err <= TIGHT_Q6K, f"k={k} n={n} rows={rows}: {err}"
+
+
+def test_q6k_gemm_special_activation_rows():
+    """The quantizer's edge-case rows (zeros, a constant, one outlier, ties,
+    subnormal values, one-signed runs, near powers of two), rows scaled by
+    1e-30 and 1e30, against extreme group scales (a weight row with one
+    large value per group)."""
+    from helpers import special_rows
+
+    k, n, rows = 2048, 96, 48
+    rng = np.random.default_rng(92)
+    w = weights(rng, n, k)
+    w[5, ::16] = 3.0  # each group's scale -128 or 127 next to small codes
+    w[6] = 0.0
+    qt, wq = q6k(w)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    sp = special_rows(k)
+    x[: len(sp)] = sp
+    x[len(sp)] *= np.float32(1e-30)
+    x[len(sp) + 1] *= np.float32(1e30)
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert "launch_gemm_q6k(" in lib().qmm_last_kernel().decode()
+    assert np.all(y[0] == 0.0) and np.all(y[:, 6] == 0.0)
+    want = qref.matmul(qref.Q6_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q6_K, wq, n * k).reshape(n, k)
+    assert normalised_error(y, want, wdeq, x) <= TIGHT_Q6K
+
+
+def test_q6k_gemm_shared_activation_and_prequantized_equal_forward():
+    """forward_shared over Q6_K weights and qmm_matmul from a quantized
+    activation give each weight's own forward bit for bit at 64 rows."""
+    from swarmllm_amd import _lib
+    from swarmllm_amd.qtensor import quantize_act
+
+    rng = np.random.default_rng(93)
+    k = 1024
+    mats = [QMatMul(q6k(weights(rng, n, k))[0]) for n in (300, 64, 1000)]
+    x = upload(activations(rng, 64, k))
+    shared = QMatMul.forward_shared(x, mats)
+    for m, y in zip(mats, shared):
+        assert torch.equal(y, m.forward(x))
+    xq = quantize_act(x, _lib.ACT_Q8K)
+    n = 300
+    out = torch.empty((64, n), dtype=torch.float32, device=DEV)
+    st = lib().qmm_matmul(qref.Q6_K, mats[0].qtensor.data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k, n, 64,
+                          torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    assert "launch_gemm_q6k(" in lib().qmm_last_kernel().decode()
+    assert torch.equal(out, shared[0])
