@@ -590,7 +590,7 @@ COPY_BYTES = 512 << 20  # the calibration copy: 512 MiB read + 512 MiB written
 def profile_only(which: str, layers, outs, stream, reps: int) -> None:
     """Launch one kind of kernel alone, `reps` times, outside any graph, for
     rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE): the dominant decode
-    launch rotating over the layer copies, the prefill GEMM, or a plain
+    launch rotating over the layer copies, a prefill GEMM (gate or down), or a plain
     device copy of COPY_BYTES whose counters calibrate the other two."""
     import torch
 
@@ -634,14 +634,16 @@ def profile_only(which: str, layers, outs, stream, reps: int) -> None:
         torch.cuda.synchronize()
         log(f"profile dominant: {reps} gate+up launches over {len(layers)} copies")
         return
-    M, n, k = 512, 14336, 4096
+    name = "down" if which == "prefill_down" else "gate"
+    t, n, k = {nm: (tt, nn, kk) for nm, tt, nn, kk in LAYER}[name]
+    M = 512
     xq, out = prefill_inputs(M, n, k)
     for i in range(reps):
         lay = layers[i % len(layers)]
-        check("qmm_matmul", L.qmm_matmul(Q4K, lay.w["gate"].data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k,
+        check("qmm_matmul", L.qmm_matmul(t, lay.w[name].data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k,
                                          n, M, s))
     torch.cuda.synchronize()
-    log(f"profile prefill: {reps} GEMM launches over {len(layers)} copies")
+    log(f"profile {which}: {reps} GEMM launches over {len(layers)} copies")
 
 
 def measured_traffic(kernel_key: str):
@@ -702,7 +704,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="skip the C1 / C4 / C5 sections")
-    ap.add_argument("--profile", choices=["single", "dominant", "prefill", "copy"],
+    ap.add_argument("--profile", choices=["single", "dominant", "prefill", "prefill_down", "copy"],
                     help="launch only this kernel --steps times (for rocprofv3 counter passes), print no JSON")
     args = ap.parse_args()
 

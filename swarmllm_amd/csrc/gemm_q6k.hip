@@ -40,6 +40,8 @@
 //     the weight bytes are read from HBM about once.
 // Rows past M and weight rows past N are read as the last row (valid
 // memory); their outputs are never stored.
+#include <type_traits>
+
 #include "lds_copy.h"
 #include "mv_common.h"
 #include "qmm_device.h"
@@ -79,7 +81,11 @@ __device__ __forceinline__ void q6_operands(const uint32_t (&ql)[4], const uint3
   }
 }
 
-template <int kWaves>
+// s_waitcnt that waits for all but the newest n vector-memory operations
+// (global loads and global-to-LDS copies) and for nothing else.
+constexpr int vmcnt_below(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+template <int kWaves, int kBuf>
 __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q6k_kernel(const uint8_t* __restrict__ W, int64_t N, int nsb,
                                                                    const int8_t* __restrict__ yq,
                                                                    const float* __restrict__ yd, int64_t M,
@@ -92,12 +98,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q6k_kernel(const uint8_t*
   constexpr int kCopies = kWCopies + kACopies;
   constexpr int kPerChunk = (kCopies + 3) / 4;
   static_assert(BN * 14 % 64 == 0 && kAInstr % kWaves == 0, "copy shapes");
-  // Each half of each double buffer is its own object and the super-block
-  // loop is unrolled by two, so every access names its buffer statically
-  // (the compiler then tells reads of one half from copies into the other).
-  __shared__ __attribute__((aligned(16))) int8_t s_a0[BM * 256], s_a1[BM * 256];
+  static_assert(kBuf == 2 || kBuf == 3, "double or triple buffers");
+  // kBuf stages of the activation tile and the weight windows: the copies of
+  // super-block sb + kBuf - 1 are issued while sb is computed. The loop is
+  // unrolled by kBuf so every access names its stage statically (the
+  // compiler then tells reads of one stage from copies into another).
+  __shared__ __attribute__((aligned(16))) int8_t s_a[kBuf][BM * 256];
   // 16 spare bytes: a row's last dword read may pass its window by two
-  __shared__ __attribute__((aligned(16))) uint8_t s_w0[BN * kWin + 16], s_w1[BN * kWin + 16];
+  __shared__ __attribute__((aligned(16))) uint8_t s_w[kBuf][BN * kWin + 16];
   __shared__ __attribute__((aligned(16))) float s_dy[2][BM];
 
   const int tid = threadIdx.x;
@@ -119,45 +127,45 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q6k_kernel(const uint8_t*
   // (L%16) ^ (row & 15). Rows past M read the last row: the host keeps
   // (M + BM) * K below 2^31.
   const uint32_t lp = lane & 15, lq = lane >> 4;
-  uint32_t coff[kCopies];
+  // Every wave issues kCopies copies a super-block, without branches: a wave
+  // whose last weight copy index passes kWInstr repeats its previous copy
+  // (the same bytes to the same place).
+  uint32_t coff[kCopies], cpiece[kWCopies];
+  int cidx[kCopies];
 #pragma unroll
   for (int j = 0; j < kCopies; j++) {
     if (j < kWCopies) {
-      const uint32_t i = (uint32_t)(wv + kWaves * j);
-      const uint32_t f = 64u * i + (uint32_t)lane;
+      int i = wv + kWaves * j;
+      i = i < kWInstr ? i : i - kWaves;
+      cidx[j] = i;
+      const uint32_t f = 64u * (uint32_t)i + (uint32_t)lane;
       const int64_t r = n0 + f / 14u < N ? n0 + f / 14u : N - 1;
-      coff[j] = (uint32_t)r * rowbytes;  // the piece is added per super-block
+      coff[j] = (uint32_t)r * rowbytes;  // the super-block is added per step
+      cpiece[j] = 16u * (f % 14u);
     } else {
-      const uint32_t i = (uint32_t)(wv + kWaves * (j - kWCopies));
-      const uint32_t tr = 4u * i + lq;
+      const int i = wv + kWaves * (j - kWCopies);
+      cidx[j] = i;
+      const uint32_t tr = 4u * (uint32_t)i + lq;
       const int64_t r = m0 + tr < M ? m0 + tr : M - 1;
       coff[j] = (uint32_t)(r * K) + 16u * (lp ^ (tr & 15u));
     }
   }
   auto issue_one = [&](int sbi, int j, uint8_t* sw, int8_t* sa) {
     const int sb = __builtin_amdgcn_readfirstlane(sbi);
-    if (j < kWCopies) {
-      const int i = wv + kWaves * j;
-      if (i < kWInstr) {
-        const uint32_t f = 64u * (uint32_t)i + (uint32_t)lane;
-        const uint32_t off = ((coff[j] + (uint32_t)(kBlock * sb)) & ~15u) + 16u * (f % 14u);
-        dma16(W, off, lds_addr(sw + 1024 * i));
-      }
-    } else {
-      const int i = wv + kWaves * (j - kWCopies);
+    const int i = __builtin_amdgcn_readfirstlane(cidx[j]);
+    if (j < kWCopies)
+      dma16(W, ((coff[j] + (uint32_t)(kBlock * sb)) & ~15u) + cpiece[j], lds_addr(sw + 1024 * i));
+    else
       dma16(yq + 256 * sb, coff[j], lds_addr(sa + 1024 * i));
-    }
   };
 
-  // dy of the tile's rows, one super-block ahead
+  // dy of the tile's rows, one super-block ahead. Every thread loads and
+  // stores the dy of row tid % BM (threads of one row store the same value),
+  // so a step has no branch and is scheduled as one block.
   const int64_t srow = m0 + (tid & (BM - 1)) < M ? m0 + (tid & (BM - 1)) : M - 1;
   float sdy = 0.0f;
-  auto load_dy = [&](int sb) {
-    if (tid < BM) sdy = yd[srow * nsb + sb];
-  };
-  auto store_dy = [&](int sb) {
-    if (tid < BM) s_dy[sb & 1][tid] = sdy;
-  };
+  auto load_dy = [&](int sb) { sdy = yd[srow * nsb + sb]; };
+  auto store_dy = [&](int sb) { s_dy[sb & 1][tid & (BM - 1)] = sdy; };
 
   float acc[8][4];
 #pragma unroll
@@ -172,17 +180,29 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q6k_kernel(const uint8_t*
   const uint32_t xr = (uint32_t)r16 >> 2, xl = ((uint32_t)kq ^ (uint32_t)r16) & 3u;
 
 #pragma unroll
-  for (int j = 0; j < kCopies; j++) issue_one(0, j, s_w0, s_a0);
+  for (int s = 0; s + 1 < kBuf; s++) {
+    if (s < nsb) {
+#pragma unroll
+      for (int j = 0; j < kCopies; j++) issue_one(s, j, s_w[s], s_a[s]);
+    }
+  }
   load_dy(0);
   __builtin_amdgcn_s_waitcnt(0);
   store_dy(0);
   __syncthreads();
 
-  auto step = [&](int sb, const uint8_t* sw, const int8_t* sa, uint8_t* nw, int8_t* na) {
-    const bool more = sb + 1 < nsb;
-    if (more) load_dy(sb + 1);
+  // Step sb: this lane's raw weight bytes and the A fragments of chunk 0,
+  // then the four K-chunks, software-pipelined tile by tile: each tile's two
+  // MFMAs, then its A fragment of the next chunk read into the same
+  // registers, with the next chunk's B operands built under the first
+  // tiles' MFMAs; in the last chunk the f32 epilogue of tile m - 1 runs
+  // under tile m's MFMAs. The copies of sb + kBuf - 1 follow each chunk.
+  auto step = [&](auto stage, int sb) {
+    constexpr int cur = decltype(stage)::value;
+    constexpr int nxt = (cur + kBuf - 1) % kBuf;
+    load_dy(sb + 1 < nsb ? sb + 1 : sb);  // past the last super-block, the last one's again
 
-    const uint8_t* win = sw + wrow * kWin;
+    const uint8_t* win = s_w[cur] + wrow * kWin;
     const int o = (int)((wbase + (uint32_t)(kBlock * sb)) & 15u);
     uint32_t ql[2][4], qh[2][4], scw[4];
     lds_words<4>(win, o + 16 * kq, ql[0]);
@@ -191,58 +211,94 @@ __global__ __launch_bounds__(64 * kWaves, 1) void gemm_q6k_kernel(const uint8_t*
     lds_words<4>(win, o + 160 + 16 * (kq & 1), qh[1]);
     lds_words<4>(win, o + 192, scw);
     const float dw4 = 0.25f * h2f((uint16_t)lds_u16(win, o + 208));
-
-    const int8_t* at = sa + r16 * 256;
-    i4v th[8], tl[8];
-    const i4v zero = {0, 0, 0, 0};
+    const int8_t* at = s_a[cur] + r16 * 256;
+    auto afrag = [&](int c, int m) -> i4v {
+      return *(const i4v*)(at + 16 * 256 * m + 16 * ((((uint32_t)c ^ xr) << 2) | xl));
+    };
+    i4v af[8];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
+    for (int m = 0; m < 8; m++) af[m] = afrag(0, m);
+    const float* sdyl = s_dy[sb & 1];
+
+    // the copies of super-block sb + kBuf - 1 (past the last super-block,
+    // the last one's again, into the stage no wave reads any more)
+    const int sbc = sb + kBuf - 1 < nsb ? sb + kBuf - 1 : nsb - 1;
+    const i4v zero = {0, 0, 0, 0};
+    auto build = [&](int c, i4v& bh, i4v& bl) {
       // group 4c + kq: scale byte kq of scale word c, codes from ql half c/2
       // (low nibbles for even c) and qh bits 4 (c%2) + 2 (kq/2)
       const int sc = (int)(int8_t)(scw[c] >> (8 * kq));
       const uint32_t sc4 = ((uint32_t)(4 * sc) & 0xFFFFu) * 0x10001u;
       const uint32_t kb = ((uint32_t)(128 - 128 * sc) & 0xFFFFu) * 0x10001u;
-      i4v bh, bl;
       q6_operands(ql[c >> 1], qh[c >> 1], 4 * (c & 1), 4 * (c & 1) + 2 * (kq >> 1), sc4, kb, bh, bl);
-      const uint32_t apiece = 16u * ((((uint32_t)c ^ xr) << 2) | xl);
-#pragma unroll
-      for (int m = 0; m < 8; m++) {
-        const i4v a = *(const i4v*)(at + 16 * 256 * m + apiece);
-        th[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bh, c == 0 ? zero : th[m], 0, 0, 0);
-        tl[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bl, c == 0 ? zero : tl[m], 0, 0, 0);
-      }
-      // the copies of super-block sb + 1 (at the last super-block, the last
-      // one's again, into the half no wave reads any more)
-#pragma unroll
-      for (int j = kPerChunk * c; j < kPerChunk * (c + 1) && j < kCopies; j++)
-        issue_one(more ? sb + 1 : sb, j, nw, na);
-    }
-
-    const float* sdyl = s_dy[sb & 1];
-#pragma unroll
-    for (int m = 0; m < 8; m++) {
-      const float4 dy4 = *(const float4*)&sdyl[16 * m + 4 * kq];
+    };
+    i4v th[8], tl[8];
+    // acc += (dy_m d_n / 4) (256 T_h + T_l) for tile m
+    auto epi_tile = [&](int m, const float4& dy4) {
       const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int t = (int)(((uint32_t)th[m][i] << 8) + (uint32_t)tl[m][i]);
         acc[m][i] = __builtin_fmaf(dyv[i] * dw4, (float)t, acc[m][i]);
       }
+    };
+    i4v bh, bl;
+    build(0, bh, bl);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      i4v nh = bh, nl = bl;
+      float4 dy4[8];
+#pragma unroll
+      for (int m = 0; m < 8; m++) {
+        th[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[m], bh, c == 0 ? zero : th[m], 0, 0, 0);
+        tl[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[m], bl, c == 0 ? zero : tl[m], 0, 0, 0);
+        if (c < 3) af[m] = afrag(c + 1, m);
+        if (c == 3) dy4[m] = *(const float4*)&sdyl[16 * m + 4 * kq];
+        if (c < 3 && m == 0) build(c + 1, nh, nl);
+        if (c == 3 && m > 0) epi_tile(m - 1, dy4[m - 1]);
+      }
+      if (c == 3) epi_tile(7, dy4[7]);
+      // the order within the chunk: each tile's MFMAs, then its next A
+      // fragment (or, in the last chunk, its dy) and a share of the vector
+      // work (the next chunk's B operands, or the previous tile's epilogue)
+#pragma unroll
+      for (int m = 0; m < 8; m++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (c < 3)
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        else
+          __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = kPerChunk * c; j < kPerChunk * (c + 1) && j < kCopies; j++)
+        issue_one(sbc, j, s_w[nxt], s_a[nxt]);
+      bh = nh;
+      bl = nl;
     }
+    // the accumulators are consumed here, so the epilogue stays under the
+    // last chunk's MFMAs (the compiler would otherwise sink it past the
+    // barrier into the next step, as one block of vector work)
+#pragma unroll
+    for (int m = 0; m < 8; m++) asm volatile("" ::"v"(acc[m][0]), "v"(acc[m][1]), "v"(acc[m][2]), "v"(acc[m][3]));
 
-    if (more) {
-      // the next super-block's tiles and scales have landed
-      __builtin_amdgcn_s_waitcnt(0);
-      store_dy(sb + 1);
-    }
-    // every wave is done with this buffer, and the next one is complete
+    // super-block sb + 1's stage and dy have landed (with three stages, the
+    // copies of sb + 2, issued after them, may still be in flight); after the
+    // last super-block this stores a dy no step reads
+    __builtin_amdgcn_s_waitcnt(kBuf == 3 ? vmcnt_below(kCopies) : 0);
+    store_dy(sb + 1);
+    // every wave is done with this stage, and the next one is complete
     __syncthreads();
   };
-  for (int sb = 0; sb < nsb; sb += 2) {
-    step(sb, s_w0, s_a0, s_w1, s_a1);
-    if (sb + 1 < nsb) step(sb + 1, s_w1, s_a1, s_w0, s_a0);
+  for (int sb = 0; sb < nsb; sb += kBuf) {
+    step(std::integral_constant<int, 0>{}, sb);
+    if (sb + 1 < nsb) step(std::integral_constant<int, 1>{}, sb + 1);
+    if constexpr (kBuf == 3) {
+      if (sb + 2 < nsb) step(std::integral_constant<int, 2>{}, sb + 2);
+    }
   }
-  // the last super-block's repeated copies land before the workgroup ends
+  // the repeated copies past the last super-block land before the workgroup ends
   __builtin_amdgcn_s_waitcnt(0);
 
   const int64_t col = n0 + wrow;
@@ -277,12 +333,14 @@ hipError_t launch_gemm_q6k(const void* w, int64_t n, int64_t k, const ActPlanes&
   const int64_t total = ((n + (wide ? 127 : 63)) / (wide ? 128 : 64)) * mt;
   if (total >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   const int remap = total % 8 == 0;
+  // the 4-wave tiles (one wave a SIMD) run three stages deep, the 8-wave ones
+  // (whose second wave a SIMD hides the copies' latency) two
   if (wide)
-    gemm_q6k_kernel<8><<<dim3((unsigned)total), 512, 0, st>>>((const uint8_t*)w, n, nsb, p.codes, p.d, rows, dst,
-                                                             ldd, (int)mt, remap);
+    gemm_q6k_kernel<8, 2><<<dim3((unsigned)total), 512, 0, st>>>((const uint8_t*)w, n, nsb, p.codes, p.d, rows,
+                                                                dst, ldd, (int)mt, remap);
   else
-    gemm_q6k_kernel<4><<<dim3((unsigned)total), 256, 0, st>>>((const uint8_t*)w, n, nsb, p.codes, p.d, rows, dst,
-                                                             ldd, (int)mt, remap);
+    gemm_q6k_kernel<4, 3><<<dim3((unsigned)total), 256, 0, st>>>((const uint8_t*)w, n, nsb, p.codes, p.d, rows,
+                                                                dst, ldd, (int)mt, remap);
   return hipGetLastError();
 }
 
