@@ -584,6 +584,42 @@ def c1_q8_0(stream, reps: int = 50, copies: int = 16) -> dict:
             "percent_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
 
 
+def prefill_b32(stream, reps: int = 10, copies: int = 4) -> dict:
+    """The 32-value block GEMM (Q8_0 and MXFP4, 4096 x 4096 at M = 512,
+    activation quantized once to Q8_0 planes, then qmm_matmul alone), rotated
+    over `copies` weights in one graph: no BASELINE config runs these types
+    at prompt size; the line shows their matrix-core path's rate."""
+    import torch
+
+    from swarmllm_amd import GgmlDType, QTensor, fill_normal
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    M, n, k = 512, 4096, 4096
+    x = fill_normal(M * k, seed=(1 << 32) | 5).reshape(M, k)
+    xq = torch.empty(L.qmm_act_bytes(1, k, M), dtype=torch.uint8, device="cuda")
+    check("qmm_quantize_act", L.qmm_quantize_act(x.data_ptr(), xq.data_ptr(), 1, k, M, k,
+                                                 torch.cuda.current_stream().cuda_stream))
+    out = torch.empty((M, n), dtype=torch.float32, device="cuda")
+    res = {}
+    for t, name in ((8, "Q8_0"), (39, "MXFP4")):
+        ws = [QTensor.quantize(fill_normal(n * k, seed=c, std=0.02).reshape(n, k), GgmlDType(t)) for c in range(copies)]
+
+        def fn(s, ws=ws, t=t):
+            for w in ws:
+                check("qmm_matmul", L.qmm_matmul(t, w.data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k, n, M, s))
+
+        g = capture(fn, stream)
+        for _ in range(2):
+            g.replay()
+        ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+        us = ms * 1e3 / (reps * copies)
+        tops = 2.0 * M * n * k / (us * 1e-6) / 1e12
+        log(f"{name} GEMM 4096x4096 at M=512: {us:.2f} us, {tops:.1f} TOP/s")
+        res[name] = {"us_per_launch": round(us, 3), "tops": round(tops, 2)}
+    return {"workload": "Q8_0 / MXFP4 4096x4096 at M=512, int8 MFMA GEMM (activation quantized once, Q8_0)", **res}
+
+
 COPY_BYTES = 512 << 20  # the calibration copy: 512 MiB read + 512 MiB written
 
 
@@ -774,6 +810,7 @@ def main() -> int:
         extra["c1"] = c1_q8_0(stream)
         extra["c4"] = c4_moe(stream)
         extra["c5"] = c5_shard(stream)
+        extra["prefill_b32"] = prefill_b32(stream)
 
     cpu = None
     if not args.no_cpu:

@@ -107,13 +107,14 @@ hipError_t launch_skinny(int type, const qmm::MvTargets& t, int64_t k, const qmm
 }
 
 // The tiled int8 matrix-core GEMMs: Q4_K and Q6_K past the skinny kernels'
-// rows, weight and quantized activation 16-byte aligned (their 16-byte
-// copies), sizes inside their 32-bit offsets.
+// rows, Q8_0 / IQ4_NL / MXFP4 past the decode kernels' rows; weight and
+// quantized activation 16-byte aligned (their 16-byte copies), sizes inside
+// their 32-bit offsets.
 bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows) {
   if (!aligned16(w) || !aligned16(xq)) return false;
   if (type == qmm::T_Q4_K) return rows >= qmm::gemm_q4k_min_rows() && qmm::gemm_q4k_fits(n, k, rows);
   if (type == qmm::T_Q6_K) return rows >= qmm::gemm_q6k_min_rows() && qmm::gemm_q6k_fits(n, k, rows);
-  return false;
+  return rows >= qmm::gemm_b32_min_rows() && qmm::gemm_b32_fits(type, n, k, rows);
 }
 
 // Q4_K: from 129 rows the single-pass GEMM (256-row tiles); 33-128 rows keep
@@ -121,6 +122,7 @@ bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, i
 hipError_t launch_gemm(int type, const void* w, int64_t n, int64_t k, const qmm::ActPlanes& p, int64_t rows,
                        float* dst, int64_t ldd, hipStream_t st) {
   if (type == qmm::T_Q6_K) return qmm::launch_gemm_q6k(w, n, k, p, rows, dst, ldd, st);
+  if (type != qmm::T_Q4_K) return qmm::launch_gemm_b32(type, w, n, k, p, rows, dst, ldd, st);
   if (rows >= qmm::gemm_q4k_sp_min_rows() && qmm::gemm_q4k_sp_fits(n, k, rows))
     return qmm::launch_gemm_q4k_sp(w, n, k, p, rows, dst, ldd, st);
   return qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st);

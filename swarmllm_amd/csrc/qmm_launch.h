@@ -149,6 +149,13 @@ bool gemm_q4k_fits(int64_t n, int64_t k, int64_t rows);
 hipError_t launch_gemm_q4k(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
                            int64_t ldd, hipStream_t s);
 
+// The Q8_0 / IQ4_NL / MXFP4 GEMM (gemm_b32.hip), from gemm_b32_min_rows()
+// rows: exact int32 block sums, f32 scaling per block.
+int gemm_b32_min_rows();
+bool gemm_b32_fits(int type, int64_t n, int64_t k, int64_t rows);
+hipError_t launch_gemm_b32(int type, const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows,
+                           float* dst, int64_t ldd, hipStream_t s);
+
 // The Q6_K GEMM (gemm_q6k.hip), from gemm_q6k_min_rows() rows, exact int32
 // super-block sums; the same 32-bit offset limits.
 int gemm_q6k_min_rows();

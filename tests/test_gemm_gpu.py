@@ -392,3 +392,93 @@ def test_q6k_gemm_shared_activation_and_prequantized_equal_forward():
     assert st == 0
     assert "launch_gemm_q6k(" in lib().qmm_last_kernel().decode()
     assert torch.equal(out, shared[0])
+
+
+# ---------------------------------------------------------------------------
+# the 32-value block formats (Q8_0, IQ4_NL, MXFP4) from 9 rows: one exact int32
+# sum per block and output, scaled in f32 per block as the reference does
+# ---------------------------------------------------------------------------
+B32 = {"Q8_0": qref.Q8_0, "IQ4_NL": qref.IQ4_NL, "MXFP4": qref.MXFP4}
+B32_SHAPES = [  # (k, n, rows): one block; a partial stage of 3 blocks; C4's 2880 (90 blocks, a partial last
+    # stage); 4096; 129 blocks; row and weight-row tails; 4- and 8-wave tiles
+    (32, 70, 9), (96, 33, 16), (2880, 300, 40), (4096, 1000, 129), (4128, 64, 200), (1024, 2048, 512),
+]
+
+
+def b32_weight(qtype, w: np.ndarray):
+    wq = qref.from_float(qtype, w)
+    return QTensor.from_data(wq.tobytes(), w.shape, GgmlDType(qtype), device=DEV), wq
+
+
+@pytest.mark.parametrize("name", list(B32))
+@pytest.mark.parametrize("k,n,rows", B32_SHAPES)
+def test_b32_gemm_parity(name, k, n, rows):
+    qtype = B32[name]
+    rng = np.random.default_rng(zlib.crc32(f"b32gemm-{name}-{k}-{n}-{rows}".encode()))
+    w = weights(rng, n, k)
+    x = activations(rng, rows, k, outliers=True)
+    qt, wq = b32_weight(qtype, w)
+    L = lib()
+    before = L.qmm_gemm_launches()
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert L.qmm_gemm_launches() == before + 1, "the MFMA GEMM did not run"
+    assert "launch_gemm_b32(" in L.qmm_last_kernel().decode()
+    want = qref.matmul(qtype, x, wq, n)
+    wdeq = qref.to_float(qtype, wq, n * k).reshape(n, k)
+    err = normalised_error(y, want, wdeq, x)
+    assert err <= TOL_GEMM, f"{name} k={k} n={n} rows={rows}: {err}"
+    assert err <= TIGHT_Q6K, f"{name} k={k} n={n} rows={rows}: {err}"  # exact block sums, f32 scaling
+
+
+@pytest.mark.parametrize("name", list(B32))
+def test_b32_gemm_special_rows(name):
+    """The quantizer's edge-case activation rows, rows scaled by 1e-30 and
+    1e5 (the f16 block scale of the activation overflows past about 8e6, in
+    the reference as here), against a zero weight row and rows of large and
+    tiny scales."""
+    from helpers import special_rows
+
+    qtype = B32[name]
+    k, n, rows = 1024, 48, 24
+    rng = np.random.default_rng(94)
+    w = weights(rng, n, k)
+    w[3] = 0.0
+    w[4] *= np.float32(300.0)
+    w[5] *= np.float32(1e-3)
+    qt, wq = b32_weight(qtype, w)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    sp = special_rows(k)
+    x[: len(sp)] = sp
+    x[len(sp)] *= np.float32(1e-30)
+    x[len(sp) + 1] *= np.float32(1e5)
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert "launch_gemm_b32(" in lib().qmm_last_kernel().decode()
+    assert np.all(y[0] == 0.0) and np.all(y[:, 3] == 0.0)
+    want = qref.matmul(qtype, x, wq, n)
+    wdeq = qref.to_float(qtype, wq, n * k).reshape(n, k)
+    assert normalised_error(y, want, wdeq, x) <= TIGHT_Q6K
+
+
+@pytest.mark.parametrize("name", list(B32))
+def test_b32_gemm_shared_activation_and_prequantized_equal_forward(name):
+    """forward_shared over 32-value weights and qmm_matmul from a quantized
+    activation give each weight's own forward bit for bit at 20 rows."""
+    from swarmllm_amd import _lib
+    from swarmllm_amd.qtensor import quantize_act
+
+    qtype = B32[name]
+    rng = np.random.default_rng(95)
+    k = 2880
+    mats = [QMatMul(b32_weight(qtype, weights(rng, n, k))[0]) for n in (300, 64, 1000)]
+    x = upload(activations(rng, 20, k))
+    shared = QMatMul.forward_shared(x, mats)
+    for m, y in zip(mats, shared):
+        assert torch.equal(y, m.forward(x))
+    xq = quantize_act(x, _lib.ACT_Q8_0)
+    n = 300
+    out = torch.empty((20, n), dtype=torch.float32, device=DEV)
+    st = lib().qmm_matmul(qtype, mats[0].qtensor.data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k, n, 20,
+                          torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    assert "launch_gemm_b32(" in lib().qmm_last_kernel().decode()
+    assert torch.equal(out, shared[0])

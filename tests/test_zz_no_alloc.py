@@ -4,10 +4,9 @@ qmm_forward with a caller-owned workspace, through the C ABI.
 
 Bit-identical outputs on two calls in a row, the second with a smaller
 input (the array keeps the first call's contents), on products whose
-planned workspace is used: the matrix-core GEMM (Q4_K, 64 rows), the
-few-row kernels (Q6_K, 12 rows) and the decode kernels in 8-row chunks
-(Q8_0, 11 rows). A product whose workspace exceeds the array is rejected
-with nothing enqueued.
+planned workspace is used: the matrix-core GEMMs (Q4_K, 64 rows; Q8_0,
+11 rows) and the few-row kernels (Q6_K, 12 rows). A product whose
+workspace exceeds the array is rejected with nothing enqueued.
 """
 import ctypes
 
@@ -46,7 +45,7 @@ CASES = [  # (type, (n, k, rows) first call, (n, k, rows) second, smaller call)
 ]
 
 
-@pytest.mark.parametrize("t,first,second", CASES, ids=["q4k_gemm", "q6k_few_rows", "q8_0_chunks"])
+@pytest.mark.parametrize("t,first,second", CASES, ids=["q4k_gemm", "q6k_few_rows", "q8_0_gemm"])
 def test_noalloc_equals_forward_on_two_calls(t, first, second):
     L = lib()
     for i, (n, k, rows) in enumerate((first, second)):
