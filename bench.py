@@ -273,6 +273,45 @@ def dominant_kernel(layers, outs, stream, reps: int) -> dict:
             "us": us, "launches": launches, "alg_bytes": alg, "gbs": gbs}
 
 
+def gate_up_glu(layers, stream, reps: int) -> dict:
+    """The gate+up+GLU launch (qmm_forward_glu, SiLU): the gate+up products of
+    the C2 layer at M = 1 and silu(gate) * up written once, back to back over
+    the copies in one graph, timed with HIP events on its stream. Algorithmic
+    bytes: the two weights, the f32 activation and the n f32 outputs."""
+    import torch
+
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    x, ws = layers[0].acts["ffn_in"]
+    n, k = 14336, 4096
+    out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    per_graph = 4 * len(layers)
+    need = ctypes.c_size_t(0)
+    check("qmm_forward_glu", L.qmm_forward_glu(Q4K, 0, None, None, None, k, None, n, None, 0, ctypes.byref(need), k,
+                                               n, 1, 0, 0))
+    buf = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+
+    def fn(st):
+        for i in range(per_graph):
+            lay = layers[i % len(layers)]
+            check("qmm_forward_glu", L.qmm_forward_glu(Q4K, 0, lay.w["gate"].data_.data_ptr(),
+                                                       lay.w["up"].data_.data_ptr(), x.data_ptr(), k, out.data_ptr(),
+                                                       n, buf.data_ptr(), buf.numel(), ctypes.byref(need), k, n, 1,
+                                                       1, st))
+
+    g = capture(fn, stream)
+    kernel = L.qmm_last_kernel().decode()
+    for _ in range(3):
+        g.replay()
+    ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+    us = ms * 1e3 / (reps * per_graph)
+    alg = 2 * 14336 * 16 * 144 + 4 * 4096 + 4 * 14336
+    gbs = alg / (us * 1e-6) / 1e9
+    return {"kernel": kernel, "us_per_launch": round(us, 4), "alg_bytes_per_launch": alg, "gbs": round(gbs, 2),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def prefill_inputs(M: int, n: int, k: int):
     """C3's activation (N(0,1), 1% of channels x20) quantized once to Q8_K
     planes, and the output buffer."""
@@ -797,6 +836,8 @@ def main() -> int:
     log(f"roofline kernel (one Q4_K 14336x4096 matvec): {dk['us']:.3f} us/launch, {dk['gbs']:.1f} GB/s")
     gu = dominant_kernel(layers, outs, stream, args.kernel_reps)
     log(f"gate+up launch: {gu['us']:.3f} us/launch, {gu['gbs']:.1f} GB/s")
+    gl = gate_up_glu(layers, stream, args.kernel_reps)
+    log(f"gate+up+GLU launch: {gl['us_per_launch']:.3f} us/launch, {gl['gbs']:.1f} GB/s")
 
     pre = prefill_gemm(layers, stream, max(2, args.kernel_reps // 5))
     log(f"prefill GEMM (gate): {pre['us_per_launch']:.2f} us/launch, {pre['tops']:.1f} TOP/s")
@@ -840,6 +881,7 @@ def main() -> int:
         "gate_up": {"kernel": gu["kernel"], "us_per_launch": round(gu["us"], 4), "alg_bytes_per_launch": gu["alg_bytes"],
                     "gbs": round(gu["gbs"], 2), "frac": round(gu["gbs"] / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic("gate_up")},
+        "gate_up_glu": gl,
         "cpu_baseline": cpu,
         "prefill": pre,
         "prefill_down": pre_down,

@@ -103,10 +103,10 @@ int qmm_matvec(int type, const void *w, const void *xq, float *dst, int64_t ldd,
  * reference's few-rows policy (quantized/cuda.rs:775-839): the decode
  * kernels up to qmm_matvec_max_rows() rows; for Q4_K and Q6_K the few-row
  * int8 matrix-core kernels from 4 rows on weights of 2 MiB or more and for
- * 9-32 rows, and for Q4_K the int8 matrix-core GEMM from 33 rows; the other
- * types run the decode kernels 8 rows at a time. Nothing is allocated. Replaces swarm_mmq_matmul's launch step
- * (mmq_entry.cu:162-203), which multiplies the activation swarm_mmq_quantize
- * produced. */
+ * 9-32 rows, then the int8 matrix-core GEMMs from 33 rows; for Q8_0, IQ4_NL
+ * and MXFP4 the int8 matrix-core GEMM from 9 rows. Nothing is allocated.
+ * Replaces swarm_mmq_matmul's launch step (mmq_entry.cu:162-203), which
+ * multiplies the activation swarm_mmq_quantize produced. */
 int qmm_matmul(int type, const void *w, const void *xq, float *dst, int64_t ldd, int64_t k, int64_t n,
                int64_t rows, int64_t stream);
 
@@ -149,6 +149,34 @@ int qmm_forward_shared(int type, int count, const void *const *w, const int64_t 
                        const int64_t *ldd, const float *x, int64_t x_stride, void *workspace,
                        size_t workspace_bytes, size_t *need, int64_t k, int64_t rows, int launch,
                        int64_t stream);
+
+/* Gated activations of an MLP: act(gate) * up. */
+enum qmm_glu_act_id {
+  QMM_GLU_SILU = 0,       /* gate / (1 + exp(-gate)) * up (fast_math.rs:48-60) */
+  QMM_GLU_SWIGLU_OAI = 1, /* min(gate, 7) sharpened by 1.702, times clamp(up, -7, 7) + 1 (fast_math.rs:84-104) */
+  QMM_GLU_GELU = 2        /* tanh-form GELU of gate, times up (fast_math.rs:62-76) */
+};
+
+/* dst[r][j] = act(x_r · gate_j) * (x_r · up_j): an MLP's gate and up
+ * products (two weights of one type, n x k each) sharing one quantized
+ * activation, and the gated activation between them, written once. For Q4_K
+ * at 1-2 rows and k <= 8192 with a 16-byte aligned activation this is ONE
+ * launch (each wave computes gate row j and up row j and writes the product;
+ * the activation quantized in LDS); otherwise the two products run as
+ * qmm_forward_shared into the workspace, followed by the elementwise GLU.
+ * Either way the results equal qmm_forward_shared followed by qmm_glu bit for
+ * bit. Plan (launch == 0) and launch as qmm_forward. Replaces the
+ * reference's forward_shared of ffn_up and ffn_gate followed by silu_mul /
+ * swiglu_oai_mul / the GELU product (src/inference/layers/mod.rs:583-632). */
+int qmm_forward_glu(int type, int act, const void *w_gate, const void *w_up, const float *x, int64_t x_stride,
+                    float *dst, int64_t ldd, void *workspace, size_t workspace_bytes, size_t *need, int64_t k,
+                    int64_t n, int64_t rows, int launch, int64_t stream);
+
+/* out[i] = act(gate[i]) * up[i] for n values (f32, on the device). Replaces
+ * the reference's fused elementwise ops silu_mul / swiglu_oai_mul
+ * (src/inference/fast_math.rs:48-130, their card kernels in
+ * kernels/fused_decode.cu). */
+int qmm_glu(int act, const float *gate, const float *up, float *out, int64_t n, int64_t stream);
 
 /* Grouped expert products (mixture-of-experts layers). Routing entry i
  * (i < size_m) pairs sorted_ids[i] (a token's k-th choice, numbered

@@ -103,6 +103,11 @@ int64_t qref_wire_bytes(int64_t n);
 void qref_wire_encode(const float *values, int64_t n, uint8_t *out);
 int qref_wire_decode(const uint8_t *bytes, int64_t nbytes, int64_t n, float *out);
 
+/* gated activations act(gate) * up (qref_glu.c) */
+void qref_silu_mul(const float *gate, const float *up, float *out, int64_t n);
+void qref_swiglu_oai_mul(const float *gate, const float *up, float *out, int64_t n);
+void qref_gelu_mul(const float *gate, const float *up, float *out, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

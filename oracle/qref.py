@@ -56,6 +56,8 @@ def lib():
         L.qref_wire_bytes.argtypes, L.qref_wire_bytes.restype = [I64], I64
         L.qref_wire_encode.argtypes, L.qref_wire_encode.restype = [P, I64, P], None
         L.qref_wire_decode.argtypes, L.qref_wire_decode.restype = [P, I64, I64, P], I
+        for f in ("qref_silu_mul", "qref_swiglu_oai_mul", "qref_gelu_mul"):
+            getattr(L, f).argtypes, getattr(L, f).restype = [P, P, P, I64], None
         _lib = L
     return _lib
 
@@ -166,4 +168,19 @@ def wire_decode(b: np.ndarray, n: int) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
     if lib().qref_wire_decode(_p(b) if b.size else 0, b.size, n, _p(out) if n else 0) != 0:
         raise ValueError(f"wire_decode: {b.size} bytes for {n} values")
+    return out
+
+
+def glu(activation: str, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """act(gate) * up in f32 as the reference's CPU path evaluates it
+    (src/inference/fast_math.rs: silu_mul_into :48-60, swiglu_oai_mul_into
+    :84-104, gelu_mul_into :62-76), elementwise over arrays of one shape."""
+    fn = {"silu": "qref_silu_mul", "swiglu_oai": "qref_swiglu_oai_mul", "gelu": "qref_gelu_mul"}[activation]
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    if g.shape != u.shape:
+        raise ValueError("glu: gate and up must have one shape")
+    out = np.empty_like(g)
+    if g.size:
+        getattr(lib(), fn)(_p(g), _p(u), _p(out), g.size)
     return out

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libqmm.so")
 QMM_OK, QMM_UNSUPPORTED, QMM_WORKSPACE_TOO_SMALL, QMM_DEVICE_ERROR, QMM_NO_TILE, QMM_NO_ROOM = range(6)
 STATUS_NAMES = {0: "OK", 1: "UNSUPPORTED", 2: "WORKSPACE_TOO_SMALL", 3: "DEVICE_ERROR", 4: "NO_TILE", 5: "NO_ROOM"}
 ACT_Q8K, ACT_Q8_0 = 0, 1
+GLU_SILU, GLU_SWIGLU_OAI, GLU_GELU = 0, 1, 2
 
 
 class QmmError(RuntimeError):
@@ -56,6 +57,9 @@ SIGNATURES = {
     "qmm_wire_bytes": (_SZ, [_I64]),
     "qmm_wire_encode": (_I, [_P, _I64, _P, _I64]),
     "qmm_wire_decode": (_I, [_P, _SZ, _I64, _P, _I64]),
+    "qmm_forward_glu": (_I, [_I, _I, _P, _P, _P, _I64, _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64, _I64, _I64,
+                             _I, _I64]),
+    "qmm_glu": (_I, [_I, _P, _P, _P, _I64, _I64]),
 }
 
 _lib = None

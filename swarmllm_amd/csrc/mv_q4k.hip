@@ -25,6 +25,7 @@
 // One launch may cover up to kMaxTargets weights of the same k that share
 // the activation (QMatMul::forward_shared, quantized/mod.rs:1221-1263): the
 // rows of the targets are numbered one after another.
+#include "glu_act.h"
 #include "mv_common.h"
 
 namespace qmm {
@@ -272,6 +273,156 @@ hipError_t launch_shape(const MvTargets& t, int nsb, const float* x, int64_t xst
                      : launch_stream<NR, T, 4, false>(t, nsb, x, xstride, pre, qmax, sh.waves, st);
 }
 
+// The gate and up products of an MLP and the GLU between them in one
+// launch (the reference's forward_shared of ffn_up and ffn_gate followed by
+// silu_mul / swiglu_oai_mul / gelu, src/inference/layers/mod.rs:583-632):
+// the stream kernel above with a unit of two weight rows, gate row j and up
+// row j, which one wave computes against the shared activation before lane 0
+// writes act(g) * u. Both rows are unpacked through the wave's LDS slot in
+// turn; with PF the next pair's loads are in flight under the current pair.
+template <int NR, int T, bool FUSED, int kWaves, bool PF, int ACT>
+__global__ __launch_bounds__(64 * kWaves) void mv_q4k_glu_kernel(const uint8_t* __restrict__ wg,
+                                                                 const uint8_t* __restrict__ wu, int64_t n, int nsb,
+                                                                 const float* __restrict__ x, int64_t xstride,
+                                                                 const int8_t* __restrict__ yq,
+                                                                 const float* __restrict__ yd,
+                                                                 const int16_t* __restrict__ ybs, float qmax,
+                                                                 float* __restrict__ dst, int64_t ldd) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const ActLds s = act_lds(smem, NR, nsb);
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 3, sbl = lane >> 2;
+  const int k = nsb * 256;
+  const int64_t rowbytes = (int64_t)nsb * 144;
+  const int64_t W = (int64_t)gridDim.x * kWaves;
+  const int64_t gw = (int64_t)blockIdx.x * kWaves + wv;
+  uint8_t* slot = smem + act_lds_bytes(NR, nsb) + (size_t)wv * 144 * nsb;
+
+  ActBatch<NR, FUSED, kWaves> act;
+  act.load(nsb, x, xstride, yq, yd, ybs);
+  RowRaw<T> cg, cu;
+  if (gw < n) {
+    load_raw<T>(cg, wg + gw * rowbytes, nsb, lane);
+    load_raw<T>(cu, wu + gw * rowbytes, nsb, lane);
+  }
+  act.store(s, nsb, x, xstride, yq, yd, ybs, qmax);
+  __syncthreads();
+  ActRegs<T> a[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const int sb = sbl + 16 * t;
+      if (sb < nsb) {
+        const int4* yp = (const int4*)(s.codes + r * k + sb * 256 + 64 * j);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int4 v = yp[q];
+          a[r].y[t][4 * q] = v.x; a[r].y[t][4 * q + 1] = v.y; a[r].y[t][4 * q + 2] = v.z; a[r].y[t][4 * q + 3] = v.w;
+        }
+        a[r].dy[t] = s.dy[r * nsb + sb];
+        const int32_t* g = s.s16 + (r * nsb + sb) * 16 + 4 * j;
+        a[r].p0[t] = g[0] + g[1];
+        a[r].p1[t] = g[2] + g[3];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 16; q++) a[r].y[t][q] = 0;
+        a[r].dy[t] = 0.0f;
+        a[r].p0[t] = a[r].p1[t] = 0;
+      }
+    }
+
+  for (int64_t R = gw; R < n; R += W) {
+    RowRaw<T> ng, nu;
+    if (PF && R + W < n) {
+      load_raw<T>(ng, wg + (R + W) * rowbytes, nsb, lane);
+      load_raw<T>(nu, wu + (R + W) * rowbytes, nsb, lane);
+    }
+    float ag[NR], au[NR];
+    {
+      RowRegs<T> rr;
+      unpack_row<T>(cg, slot, rr, nsb, lane);
+#pragma unroll
+      for (int r = 0; r < NR; r++) ag[r] = 0.0f;
+#pragma unroll
+      for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+          ag[r] = q4k_unit(rr.h[t], rr.qa[t], rr.qb[t], a[r].y[t], a[r].dy[t], a[r].p0[t], a[r].p1[t], j, ag[r]);
+    }
+    {
+      // the slot's second use: the gate row's reads above complete first
+      RowRegs<T> rr;
+      unpack_row<T>(cu, slot, rr, nsb, lane);
+#pragma unroll
+      for (int r = 0; r < NR; r++) au[r] = 0.0f;
+#pragma unroll
+      for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+          au[r] = q4k_unit(rr.h[t], rr.qa[t], rr.qb[t], a[r].y[t], a[r].dy[t], a[r].p0[t], a[r].p1[t], j, au[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const float g = wave_sum_dpp(ag[r]);
+      const float u = wave_sum_dpp(au[r]);
+      if (lane == 0) dst[r * ldd + R] = glu_act<ACT>(g, u);
+    }
+    if (PF) {
+      cg = ng;
+      cu = nu;
+    } else if (R + W < n) {
+      load_raw<T>(cg, wg + (R + W) * rowbytes, nsb, lane);
+      load_raw<T>(cu, wu + (R + W) * rowbytes, nsb, lane);
+    }
+  }
+}
+
+template <int NR, int T, bool PF, int ACT>
+hipError_t launch_glu_x(const void* wg, const void* wu, int64_t n, int nsb, const float* x, int64_t xstride,
+                        const ActPlanes* pre, float qmax, float* dst, int64_t ldd, int64_t waves, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  constexpr int WPG = 16;
+  const size_t lds = act_lds_bytes(NR, nsb) + (size_t)WPG * 144 * nsb;
+  const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
+  if (pre) {
+    auto* kf = mv_q4k_glu_kernel<NR, T, false, WPG, PF, ACT>;
+    if (lds > 65536 && set_max_dynamic_lds((const void*)kf) != hipSuccess) return hipErrorInvalidValue;
+    kf<<<grid, 64 * WPG, lds, st>>>((const uint8_t*)wg, (const uint8_t*)wu, n, nsb, nullptr, 0, pre->codes, pre->d,
+                                    (const int16_t*)pre->sums, qmax, dst, ldd);
+  } else {
+    auto* kf = mv_q4k_glu_kernel<NR, T, true, WPG, PF, ACT>;
+    if (lds > 65536 && set_max_dynamic_lds((const void*)kf) != hipSuccess) return hipErrorInvalidValue;
+    kf<<<grid, 64 * WPG, lds, st>>>((const uint8_t*)wg, (const uint8_t*)wu, n, nsb, x, xstride, nullptr, nullptr,
+                                    nullptr, qmax, dst, ldd);
+  }
+  return hipGetLastError();
+}
+
+template <int NR, int T, int ACT>
+hipError_t launch_glu_pf(const void* wg, const void* wu, int64_t n, int nsb, const float* x, int64_t xstride,
+                         const ActPlanes* pre, float qmax, float* dst, int64_t ldd, int cus, hipStream_t st) {
+  // one 16-wave workgroup a CU; a pair a wave where pairs are few, else the
+  // pairs spread over the CUs with the next pair in flight (C2's 14336 pairs:
+  // 14.6 us; two workgroups a CU 15.9 us, a pair a wave 20.2 us)
+  const int64_t cap = (int64_t)cus * 16;
+  if (n <= cap)
+    return launch_glu_x<NR, T, false, ACT>(wg, wu, n, nsb, x, xstride, pre, qmax, dst, ldd, (n + 15) / 16 * 16, st);
+  return launch_glu_x<NR, T, true, ACT>(wg, wu, n, nsb, x, xstride, pre, qmax, dst, ldd, cap, st);
+}
+
+template <int ACT>
+hipError_t launch_glu_act(const void* wg, const void* wu, int64_t n, int nsb, int64_t rows, const float* x,
+                          int64_t xstride, const ActPlanes* pre, float qmax, float* dst, int64_t ldd, int cus,
+                          hipStream_t st) {
+  const int T = (nsb + 15) / 16;
+  if (rows == 1)
+    return T <= 1 ? launch_glu_pf<1, 1, ACT>(wg, wu, n, nsb, x, xstride, pre, qmax, dst, ldd, cus, st)
+                  : launch_glu_pf<1, 2, ACT>(wg, wu, n, nsb, x, xstride, pre, qmax, dst, ldd, cus, st);
+  return T <= 1 ? launch_glu_pf<2, 1, ACT>(wg, wu, n, nsb, x, xstride, pre, qmax, dst, ldd, cus, st)
+                : launch_glu_pf<2, 2, ACT>(wg, wu, n, nsb, x, xstride, pre, qmax, dst, ldd, cus, st);
+}
+
 }  // namespace
 
 bool mv_q4k_rows_supported(int64_t k, int64_t rows) {
@@ -299,6 +450,23 @@ hipError_t launch_mv_q4k_rows(const MvTargets& t, int64_t k, int64_t rows, const
   }
   if (T <= 1) return launch_shape<2, 1>(t, nsb, x, xstride, pre, qmax, sh, st);
   return launch_shape<2, 2>(t, nsb, x, xstride, pre, qmax, sh, st);
+}
+
+// Rows of up to 8192 values (two units of 16 super-blocks a lane), 1-2
+// activation rows: the fused gate+up+GLU launch.
+bool mv_q4k_glu_supported(int64_t k, int64_t rows) {
+  return rows >= 1 && rows <= 2 && k % 256 == 0 && k >= 256 && k <= 8192;
+}
+
+hipError_t launch_mv_q4k_glu(int act, const void* wg, const void* wu, int64_t n, int64_t k, int64_t rows,
+                             const float* x, int64_t xstride, const ActPlanes* pre, float qmax, float* dst, int64_t ldd,
+                             int cus, hipStream_t st) {
+  const int nsb = (int)(k / 256);
+  if (act == GLU_SILU) return launch_glu_act<GLU_SILU>(wg, wu, n, nsb, rows, x, xstride, pre, qmax, dst, ldd, cus, st);
+  if (act == GLU_SWIGLU_OAI)
+    return launch_glu_act<GLU_SWIGLU_OAI>(wg, wu, n, nsb, rows, x, xstride, pre, qmax, dst, ldd, cus, st);
+  if (act == GLU_GELU) return launch_glu_act<GLU_GELU>(wg, wu, n, nsb, rows, x, xstride, pre, qmax, dst, ldd, cus, st);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace qmm

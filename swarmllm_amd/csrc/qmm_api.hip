@@ -394,6 +394,50 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
   return flush();
 }
 
+int qmm_forward_glu(int type, int act, const void* w_gate, const void* w_up, const float* x, int64_t x_stride,
+                    float* dst, int64_t ldd, void* workspace, size_t workspace_bytes, size_t* need, int64_t k,
+                    int64_t n, int64_t rows, int launch, int64_t stream) {
+  if (!shape_ok(type, k, n, rows) || act < QMM_GLU_SILU || act > QMM_GLU_GELU || need == nullptr || ldd < n ||
+      x_stride < k)
+    return QMM_UNSUPPORTED;
+  // workspace: the quantized activation, then the gate and up products of
+  // the two-launch form
+  const int layout = qmm_act_layout(type, rows);
+  const size_t abytes = qmm::act_bytes(layout, k, rows);
+  const size_t obytes = qmm::align_up((size_t)(rows * n) * 4, 256);
+  const size_t bytes = abytes + 2 * obytes;
+  *need = bytes;
+  if (!launch) return QMM_OK;
+  if (g_fail_next.exchange(false)) return QMM_NO_ROOM;
+  if (!w_gate || !w_up || !x || !dst) return QMM_UNSUPPORTED;
+  const hipStream_t st = (hipStream_t)stream;
+  clear_stale_error();
+  if (type == qmm::T_Q4_K && qmm::mv_q4k_glu_supported(k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
+    if (qmm::launch_mv_q4k_glu(act, w_gate, w_up, n, k, rows, x, x_stride, nullptr, q8k_scale(), dst, ldd,
+                               cu_count(), st) != hipSuccess)
+      return QMM_DEVICE_ERROR;
+    g_matvec_launches.fetch_add(1, std::memory_order_relaxed);
+    return QMM_OK;
+  }
+  if (workspace_bytes < bytes || workspace == nullptr) return QMM_WORKSPACE_TOO_SMALL;
+  float* gbuf = (float*)((char*)workspace + abytes);
+  float* ubuf = (float*)((char*)gbuf + obytes);
+  const void* w[2] = {w_gate, w_up};
+  const int64_t ns[2] = {n, n};
+  float* outs[2] = {gbuf, ubuf};
+  size_t need2 = 0;
+  const int r = qmm_forward_shared(type, 2, w, ns, outs, ns, x, x_stride, workspace, abytes, &need2, k, rows, 1,
+                                   stream);
+  if (r != QMM_OK) return r;
+  return status_of(qmm::launch_glu(act, gbuf, n, ubuf, n, dst, ldd, n, rows, st));
+}
+
+int qmm_glu(int act, const float* gate, const float* up, float* out, int64_t n, int64_t stream) {
+  if (act < QMM_GLU_SILU || act > QMM_GLU_GELU || n < 0 || (n > 0 && (!gate || !up || !out))) return QMM_UNSUPPORTED;
+  clear_stale_error();
+  return status_of(qmm::launch_glu(act, gate, n, up, n, out, n, n, 1, (hipStream_t)stream));
+}
+
 int qmm_dequantize(int type, const void* w, void* out, int out_f16, int64_t nelem, int64_t stream) {
   if (qmm_type_bytes(type, nelem) == 0 || !w || !out) return QMM_UNSUPPORTED;
   clear_stale_error();

@@ -129,6 +129,16 @@ bool gemm_q6k_skinny_fits(int64_t k, int64_t rows);
 hipError_t launch_gemm_q6k_skinny(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, int cus,
                                   hipStream_t st);
 
+// The gate+up+GLU decode launch (mv_q4k.hip): Q4_K, 1-2 rows, k <= 8192;
+// act is a GluAct (glu_act.h). And the elementwise GLU (glu.hip) over rows
+// of n values.
+bool mv_q4k_glu_supported(int64_t k, int64_t rows);
+hipError_t launch_mv_q4k_glu(int act, const void* wg, const void* wu, int64_t n, int64_t k, int64_t rows,
+                             const float* x, int64_t xstride, const ActPlanes* pre, float qmax, float* dst, int64_t ldd,
+                             int cus, hipStream_t st);
+hipError_t launch_glu(int act, const float* gate, int64_t ldg, const float* up, int64_t ldu, float* out, int64_t ldo,
+                      int64_t n, int64_t rows, hipStream_t st);
+
 // The Q8_0 hidden-state wire codec (wire.hip): bytes of n values (-1 when
 // they would not fit an int64), encode, decode.
 int64_t wire_bytes(int64_t n);

@@ -224,6 +224,62 @@ class QMatMul:
         return outs
 
 
+#: the gated activations of an MLP (src/inference/layers/mod.rs:583-632)
+ACTIVATIONS = {"silu": _lib.GLU_SILU, "swiglu_oai": _lib.GLU_SWIGLU_OAI, "gelu": _lib.GLU_GELU}
+
+
+def forward_glu(xs: torch.Tensor, gate: "QMatMul", up: "QMatMul", activation: str = "silu") -> torch.Tensor:
+    """act(xs · gateᵀ) * (xs · upᵀ): the gate and up products of an MLP sharing
+    one quantized activation and the gated activation between them, written
+    once (qmm_forward_glu: one launch for Q4_K at 1-2 rows; otherwise the
+    shared products and the elementwise GLU). The reference's forward_block
+    (src/inference/layers/mod.rs:583-632): forward_shared of ffn_up and
+    ffn_gate, then silu_mul / swiglu_oai_mul / gelu(gate) * up."""
+    if activation not in ACTIVATIONS:
+        raise ValueError(f"activation must be one of {sorted(ACTIVATIONS)}")
+    gq, uq = gate.qtensor, up.qtensor
+    if gq.shape != uq.shape or gq.dtype != uq.dtype:
+        raise ValueError("forward_glu: gate and up must have one shape and type")
+    n, k = gq.shape
+    if xs.dim() < 1 or xs.shape[-1] != k:
+        raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with k={k}")
+    if xs.dtype != torch.float32:
+        raise ValueError("Expected f32")
+    if not xs.is_contiguous():
+        raise ValueError(f"input tensor is not contiguous {tuple(xs.shape)}")
+    rows = xs.numel() // k
+    out = torch.empty((*xs.shape[:-1], n), dtype=torch.float32, device=xs.device)
+    if rows == 0:
+        return out
+    L = lib()
+    st = _stream()
+    t, act = int(gq.dtype), ACTIVATIONS[activation]
+    need = ctypes.c_size_t(0)
+    check("qmm_forward_glu", L.qmm_forward_glu(t, act, None, None, None, k, None, n, None, 0, ctypes.byref(need), k, n,
+                                               rows, 0, st))
+    buf = gate._ws.get(need.value, xs.device)
+    check("qmm_forward_glu", L.qmm_forward_glu(t, act, gq.data_.data_ptr(), uq.data_.data_ptr(), _ptr(xs), k,
+                                               _ptr(out), n, _ptr(buf), buf.numel(), ctypes.byref(need), k, n, rows,
+                                               1, st))
+    return out
+
+
+def glu(gate: torch.Tensor, up: torch.Tensor, activation: str = "silu") -> torch.Tensor:
+    """act(gate) * up elementwise (qmm_glu): the reference's silu_mul /
+    swiglu_oai_mul / gelu product (src/inference/fast_math.rs:48-130)."""
+    if activation not in ACTIVATIONS:
+        raise ValueError(f"activation must be one of {sorted(ACTIVATIONS)}")
+    if gate.shape != up.shape or gate.dtype != torch.float32 or up.dtype != torch.float32:
+        raise ValueError("glu: gate and up must be f32 tensors of one shape")
+    if not (gate.is_contiguous() and up.is_contiguous()) or not (gate.is_cuda and up.is_cuda):
+        raise ValueError("glu: contiguous GPU tensors")
+    out = torch.empty_like(gate)
+    n = gate.numel()
+    if n:
+        check("qmm_glu", lib().qmm_glu(ACTIVATIONS[activation], _ptr(gate), _ptr(up), _ptr(out), n, _stream()))
+    return out
+
+
 def moe_forward(xs: torch.Tensor, experts: QTensor, sorted_ids: torch.Tensor, expert_ids: torch.Tensor,
                 topk_weights: Optional[torch.Tensor], topk: int, workspace: Optional[Workspace] = None) -> torch.Tensor:
     """The grouped expert products of moe_gemm_gguf (candle-kernels/src/moe/
