@@ -201,6 +201,60 @@ int qmm_moe_forward(int type, const void *w, int num_experts, const float *x, in
                     float *dst, int64_t ldd, void *workspace, size_t workspace_bytes, size_t *need, int64_t k,
                     int64_t n, int64_t size_m, int launch, int64_t stream);
 
+/* ---- GGUF files into device memory --------------------------------------
+ * A parsed GGUF file: candle's gguf_file::Content::read
+ * (quantized/gguf_file.rs:415-487): header (magic "GGUF", versions 1-3),
+ * metadata key/value pairs, tensor infos (name, ggml type, dimensions
+ * outermost first, offset from the tensor data), and the tensor data's start,
+ * the end of the infos rounded up to general.alignment (U8/U16/U32 or a
+ * non-negative I8/I16/I32 value; 32 without it). qmm_gguf_open returns
+ * QMM_UNSUPPORTED with *out = NULL for a file that is not one (bad magic or
+ * version, an unknown value or ggml type, a truncated header). */
+typedef struct qmm_gguf qmm_gguf;
+int qmm_gguf_open(const char *path, qmm_gguf **out);
+void qmm_gguf_close(qmm_gguf *g);
+int qmm_gguf_version(const qmm_gguf *g);
+uint64_t qmm_gguf_alignment(const qmm_gguf *g);
+uint64_t qmm_gguf_data_offset(const qmm_gguf *g);
+
+/* Tensor infos (Content::tensor_infos): index by name (-1 when absent), name,
+ * and type / dimensions (dims[0..3], outermost first, 1 past n_dims) / offset
+ * from the data start / bytes (0 when the element count is not a whole
+ * number of blocks, which qmm_gguf_load then refuses). */
+int64_t qmm_gguf_tensor_count(const qmm_gguf *g);
+int64_t qmm_gguf_find_tensor(const qmm_gguf *g, const char *name);
+const char *qmm_gguf_tensor_name(const qmm_gguf *g, int64_t i);
+int qmm_gguf_tensor_info(const qmm_gguf *g, int64_t i, int *type, int *n_dims, int64_t *dims, uint64_t *offset,
+                         uint64_t *bytes);
+
+/* Metadata (Content::metadata) in file order (a repeated key keeps its last
+ * value): key, GGUF value type (0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32,
+ * 7 bool, 8 string, 9 array, 10 u64, 11 i64, 12 f64; -1 for no such pair)
+ * with the element type and length of an array (the type itself and 1 for a
+ * scalar), and element j of it (j = 0 for a scalar): integers and bools in
+ * *iv (a u64 as its bits), f32/f64 in *fv, strings in *sv (trailing NULs
+ * dropped, as the reference drops them). Arrays of arrays are parsed but not
+ * read element by element. */
+int64_t qmm_gguf_kv_count(const qmm_gguf *g);
+int64_t qmm_gguf_find_kv(const qmm_gguf *g, const char *key);
+const char *qmm_gguf_kv_key(const qmm_gguf *g, int64_t i);
+int qmm_gguf_kv_type(const qmm_gguf *g, int64_t i, int *elem_type, int64_t *len);
+int qmm_gguf_kv_get(const qmm_gguf *g, int64_t i, int64_t j, int64_t *iv, double *fv, const char **sv);
+
+/* Bytes of a device buffer for `nelem` values of ggml type `type`: its
+ * blocks plus MATRIX_ROW_PADDING = 512 values' worth of blocks
+ * (quantized/cuda.rs:43, 1846-1870); 0 for an unknown type or a count that
+ * is not a whole number of blocks. */
+size_t qmm_padded_bytes(int type, int64_t nelem);
+
+/* Tensor i's bytes from the file into device memory dst (dst_bytes >=
+ * qmm_padded_bytes of the tensor), the padding zeroed: ggml_file::
+ * qtensor_read + cuda::load_quantized_read (ggml_file.rs:220-256,
+ * cuda.rs:2025-2075), read through two pinned staging buffers of 16 MiB the
+ * library keeps (a chunk is read while the previous one copies). Returns when
+ * the bytes are on the device; loads on one process are serialized. */
+int qmm_gguf_load(const qmm_gguf *g, int64_t i, void *dst, size_t dst_bytes, int64_t stream);
+
 /* Dequantize `nelem` values of weight type `type` into f32 (out_f16 == 0)
  * or IEEE f16 (out_f16 != 0; each value is f16 of the f32 one).
  * Replaces QCudaStorage::dequantize / dequantize_f16

@@ -60,6 +60,24 @@ SIGNATURES = {
     "qmm_forward_glu": (_I, [_I, _I, _P, _P, _P, _I64, _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64, _I64, _I64,
                              _I, _I64]),
     "qmm_glu": (_I, [_I, _P, _P, _P, _I64, _I64]),
+    "qmm_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "qmm_gguf_close": (None, [_P]),
+    "qmm_gguf_version": (_I, [_P]),
+    "qmm_gguf_alignment": (ctypes.c_uint64, [_P]),
+    "qmm_gguf_data_offset": (ctypes.c_uint64, [_P]),
+    "qmm_gguf_tensor_count": (_I64, [_P]),
+    "qmm_gguf_find_tensor": (_I64, [_P, ctypes.c_char_p]),
+    "qmm_gguf_tensor_name": (ctypes.c_char_p, [_P, _I64]),
+    "qmm_gguf_tensor_info": (_I, [_P, _I64, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I64),
+                                  ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "qmm_gguf_kv_count": (_I64, [_P]),
+    "qmm_gguf_find_kv": (_I64, [_P, ctypes.c_char_p]),
+    "qmm_gguf_kv_key": (ctypes.c_char_p, [_P, _I64]),
+    "qmm_gguf_kv_type": (_I, [_P, _I64, ctypes.POINTER(_I), ctypes.POINTER(_I64)]),
+    "qmm_gguf_kv_get": (_I, [_P, _I64, _I64, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double),
+                             ctypes.POINTER(ctypes.c_char_p)]),
+    "qmm_padded_bytes": (_SZ, [_I, _I64]),
+    "qmm_gguf_load": (_I, [_P, _I64, _P, _SZ, _I64]),
 }
 
 _lib = None

@@ -14,7 +14,8 @@ namespace qmm {
 // the loop body. M0 is declared clobbered rather than saved and restored:
 // writing M0 back right after the copy holds the wave until the copy has
 // read it (a copy probe on gfx950 moved 28% more bytes a cycle without the
-// restore). A kernel waits for its copies itself (vmcnt(0) before the barrier
+// restore); no instruction of the kernels that copy this way reads M0
+// elsewhere. A kernel waits for its copies itself (vmcnt(0) before the barrier
 // after which they are read) and copies only into buffers no wave reads
 // until then.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {

@@ -24,19 +24,27 @@ from ._lib import check, lib
 
 
 class GgmlDType(enum.IntEnum):
-    """The GGUF type ids of the covered formats (mod.rs:319-371)."""
+    """GGUF type ids (mod.rs:319-371): the five formats the products take, and
+    F32 / F16 / BF16, which a GGUF file holds beside them (norms, biases) and
+    a QTensor stores but no product reads."""
 
+    F32 = 0
+    F16 = 1
     Q8_0 = 8
     Q4K = 12
     Q6K = 14
     Iq4Nl = 20
+    BF16 = 30
     Mxfp4 = 39
 
     def block_size(self) -> int:
-        return lib().qmm_block_size(int(self))
+        return {0: 1, 1: 1, 30: 1, 8: 32, 20: 32, 39: 32, 12: 256, 14: 256}[int(self)]
 
     def type_size(self) -> int:
-        return {8: 34, 12: 144, 14: 210, 20: 18, 39: 17}[int(self)]
+        return {0: 4, 1: 2, 30: 2, 8: 34, 12: 144, 14: 210, 20: 18, 39: 17}[int(self)]
+
+    def is_quantized(self) -> bool:
+        return int(self) not in (0, 1, 30)
 
 
 def _stream() -> int:
@@ -61,10 +69,12 @@ class QTensor:
     mod.rs:989-1025)."""
 
     def __init__(self, data: torch.Tensor, shape: Sequence[int], dtype: GgmlDType):
+        """The blocks of `shape` in `data` (uint8, on the device): exactly their
+        bytes, or a storage that holds padding past them (QTensor.alloc)."""
         dtype = GgmlDType(dtype)
         shape = tuple(int(d) for d in shape)
-        if len(shape) < 2:
-            raise ValueError(f"QTensor: shape {shape} has fewer than 2 dims")
+        if len(shape) < 1:
+            raise ValueError(f"QTensor: shape {shape} has no dims")
         k = shape[-1]
         qk = dtype.block_size()
         if k % qk:
@@ -72,12 +82,31 @@ class QTensor:
         nel = 1
         for d in shape:
             nel *= d
-        want = lib().qmm_type_bytes(int(dtype), nel)
-        if data.dtype != torch.uint8 or data.numel() != want or not data.is_cuda:
+        want = nel // qk * dtype.type_size()
+        if data.dtype != torch.uint8 or data.numel() < want or not data.is_cuda:
             raise ValueError(f"QTensor: {data.numel()} device bytes for {shape} {dtype.name} (want {want})")
-        self.data_ = data.contiguous()
+        self.storage_ = data.contiguous()
+        self.data_ = self.storage_[:want]
         self.shape = shape
         self.dtype = dtype
+
+    @staticmethod
+    def alloc(shape: Sequence[int], dtype: GgmlDType, device="cuda") -> "QTensor":
+        """Zeroed blocks of `shape` in a device buffer padded by 512 values'
+        worth of blocks past them, as the reference pads every device weight
+        (MATRIX_ROW_PADDING, quantized/cuda.rs:43, 1846-1870)."""
+        dtype = GgmlDType(dtype)
+        nel = 1
+        for d in shape:
+            nel *= int(d)
+        padded = lib().qmm_padded_bytes(int(dtype), nel)
+        if padded == 0 and nel:
+            raise ValueError(f"QTensor.alloc: {list(shape)} is not a whole number of {dtype.name} blocks")
+        return QTensor(torch.zeros(max(padded, 1), dtype=torch.uint8, device=device), shape, dtype)
+
+    def padded_bytes(self) -> int:
+        """Bytes of the device storage, padding included."""
+        return self.storage_.numel()
 
     def elem_count(self) -> int:
         nel = 1
@@ -87,9 +116,37 @@ class QTensor:
 
     @staticmethod
     def from_data(raw: bytes, shape: Sequence[int], dtype: GgmlDType, device="cuda") -> "QTensor":
-        """Blocks from the bytes a GGUF holds them as (QStorage::from_data, mod.rs:119-163)."""
-        t = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(device)
-        return QTensor(t, shape, dtype)
+        """Blocks from the bytes a GGUF holds them as (QStorage::from_data,
+        mod.rs:119-163), in a padded device buffer (cuda::load_quantized)."""
+        q = QTensor.alloc(shape, dtype, device)
+        if len(raw) != q.data_.numel():
+            raise ValueError(f"from_data: {len(raw)} bytes for {list(shape)} {GgmlDType(dtype).name}")
+        if len(raw):
+            q.data_.copy_(torch.frombuffer(bytearray(raw), dtype=torch.uint8))
+        return q
+
+    @staticmethod
+    def stack_some(slots: int, parts: Sequence[tuple], device="cuda") -> "QTensor":
+        """A [slots, rows, cols] stack holding each (slot, QTensor) part at its
+        slot, the other slots zero (QTensor::stack_some / cuda::
+        load_quantized_entries, mod.rs:989-1025, cuda.rs:2101-2127): every
+        part of one type and 2-D shape; the stack padded as a device weight."""
+        if not parts:
+            raise ValueError("stack_some: no parts")
+        first = parts[0][1]
+        if len(first.shape) != 2:
+            raise ValueError(f"stack_some: parts must be 2-D, got {first.shape}")
+        rows, cols = first.shape
+        out = QTensor.alloc((slots, rows, cols), first.dtype, device)
+        eb = first.data_.numel()
+        for slot, t in parts:
+            if t.dtype != first.dtype or t.shape != first.shape:
+                raise ValueError(f"stack_some: part {slot} is {t.dtype.name} {t.shape}, not {first.dtype.name} "
+                                 f"{first.shape}")
+            if not 0 <= slot < slots:
+                raise ValueError(f"stack_some: slot {slot} of {slots}")
+            out.data_[slot * eb:(slot + 1) * eb].copy_(t.data_)
+        return out
 
     @staticmethod
     def quantize(w: torch.Tensor, dtype: GgmlDType) -> "QTensor":
@@ -100,14 +157,16 @@ class QTensor:
         n, k = w.shape
         if k % dtype.block_size():
             raise ValueError(f"quantize: last dim {k} not divisible by block size {dtype.block_size()}")
+        if not dtype.is_quantized():
+            raise ValueError(f"quantize: {dtype.name} is not a block format")
         w = w.to(device="cuda", dtype=torch.float32).contiguous()
         nel = n * k
-        out = torch.empty(lib().qmm_type_bytes(int(dtype), nel), dtype=torch.uint8, device=w.device)
+        q = QTensor.alloc((n, k), dtype, w.device)
         sb = lib().qmm_quantize_scratch_bytes(int(dtype), nel)
         scratch = torch.empty(max(sb, 1), dtype=torch.uint8, device=w.device)
         check("qmm_quantize_weights",
-              lib().qmm_quantize_weights(int(dtype), _ptr(w), _ptr(out), nel, _ptr(scratch), sb, _stream()))
-        return QTensor(out, (n, k), dtype)
+              lib().qmm_quantize_weights(int(dtype), _ptr(w), _ptr(q.data_), nel, _ptr(scratch), sb, _stream()))
+        return q
 
     def dequantize(self) -> torch.Tensor:
         return self._dequant(False)
@@ -116,6 +175,11 @@ class QTensor:
         return self._dequant(True)
 
     def _dequant(self, f16: bool) -> torch.Tensor:
+        if not self.dtype.is_quantized():
+            # F32 / F16 / BF16 storage: the values themselves
+            src = {0: torch.float32, 1: torch.float16, 30: torch.bfloat16}[int(self.dtype)]
+            vals = self.data_.view(src).reshape(self.shape)
+            return vals.to(torch.float16 if f16 else torch.float32)
         out = torch.empty(self.shape, dtype=torch.float16 if f16 else torch.float32, device=self.data_.device)
         check("qmm_dequantize", lib().qmm_dequantize(int(self.dtype), _ptr(self.data_), _ptr(out), int(f16),
                                                      self.elem_count(), _stream()))
