@@ -185,8 +185,9 @@ int qmm_glu(int act, const float *gate, const float *up, float *out, int64_t n, 
  * p = sorted_ids[i], e = expert_ids[i], in_p = p when topk_w is given (one
  * input row per pair, size_m rows) else p / topk (one per token, size_m/topk
  * rows), scale_p = topk_w[p] or 1. `w` holds num_experts weights of n x k
- * back to back, each in GGUF blocks of `type` (Q8_0, IQ4_NL or MXFP4). The
- * activation is quantized per 32 values (Q8_0). Entries whose expert or pair
+ * back to back, each in GGUF blocks of `type`: Q8_0, IQ4_NL or MXFP4 (the
+ * activation quantized per 32 values, Q8_0), or Q4_K or Q6_K with k at most
+ * 16384 (per 256 values, Q8_K). Entries whose expert or pair
  * is out of range write nothing. Entries with one expert read its weights
  * once when they are consecutive (ids sorted by expert); any order gives
  * the same result. Each dst[p] equals qmm_forward of x[in_p] against W_e,

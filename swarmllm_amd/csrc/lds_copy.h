@@ -15,7 +15,10 @@ namespace qmm {
 // writing M0 back right after the copy holds the wave until the copy has
 // read it (a copy probe on gfx950 moved 28% more bytes a cycle without the
 // restore); no instruction of the kernels that copy this way reads M0
-// elsewhere. A kernel waits for its copies itself (vmcnt(0) before the barrier
+// elsewhere (their ISA shows none). The compiler warns that M0 in a clobber
+// list is a reserved register and does not track it: a kernel that adds an
+// instruction reading M0 (s_sendmsg, LDS-direct or indexed moves) must set
+// it again after the copies. A kernel waits for its copies itself (vmcnt(0) before the barrier
 // after which they are read) and copies only into buffers no wave reads
 // until then.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {

@@ -408,7 +408,11 @@ hipError_t launch_moe_fmt(const void* w, int num_experts, int64_t n, int64_t k, 
 
 }  // namespace
 
-bool moe_supported(int type) { return type == T_Q8_0 || type == T_IQ4_NL || type == T_MXFP4; }
+bool moe_supported(int type, int64_t k) {
+  return type == T_Q8_0 || type == T_IQ4_NL || type == T_MXFP4 || moe_kq_supported(type, k);
+}
+
+int moe_act_layout(int type) { return type == T_Q4_K || type == T_Q6_K ? ACT_Q8K : ACT_Q8_0; }
 
 size_t moe_runs_bytes(int64_t size_m) { return (size_t)(1 + 3 * size_m) * sizeof(int32_t); }
 

@@ -240,6 +240,69 @@ __device__ __forceinline__ void lds_words(const uint8_t* lds, int off, uint32_t*
 }
 __device__ __forceinline__ uint32_t lds_u16(const uint8_t* lds, int off) { return lds_u32(lds, off) & 0xFFFF; }
 
+// ---------------------------------------------------------------------------
+// Q6_K spans: a super-block is 210 bytes, so blocks are not 16-byte aligned;
+// a wave stages a span of up to 16 super-blocks of a row in its own LDS
+// buffer and each lane reads its unit from there.
+// ---------------------------------------------------------------------------
+constexpr int kQ6SpanSb = 16;                            // super-blocks per span
+constexpr int kQ6SpanBytes = kQ6SpanSb * 210;              // 3360
+constexpr int kQ6SpanPieces = (kQ6SpanBytes + 15) / 16 + 1; // 16-byte pieces, start not aligned: 211
+constexpr int kQ6PiecesPerLane = (kQ6SpanPieces + 63) / 64; // 4
+// LDS bytes per wave: the pieces, and the 8 bytes past the last that the
+// dword reads of lds_words may touch
+constexpr int kQ6SpanBuf = kQ6SpanPieces * 16 + 16;
+
+struct Q6Span {
+  uint4 p[kQ6PiecesPerLane];
+  int off;  // offset of the span's first byte in its first piece
+  int len;  // super-blocks in the span
+};
+
+// Loads the 16-byte aligned pieces (aligned as device addresses) from the one
+// holding byte p to the one holding byte p + len*210 - 1. Every piece read
+// holds at least one byte of the span, and an aligned piece never crosses a
+// page, so the bytes read beyond the span stay in mapped memory. Lane L holds
+// pieces L + 64c.
+__device__ __forceinline__ void load_q6_span(Q6Span& sp, const uint8_t* __restrict__ p, int len, int lane) {
+  // rounded down by pointer arithmetic: the compiler keeps these global
+  // loads (an integer round trip would make them flat loads, which every LDS
+  // wait also waits for)
+  sp.off = (int)((uintptr_t)p & 15);
+  const uint8_t* a0 = p - sp.off;
+  sp.len = len;
+  const int pieces = (int)((sp.off + len * 210 + 15) >> 4);
+  // every lane loads (no branches): lanes past the span's pieces load its
+  // last piece again, whose bytes are never read
+#pragma unroll
+  for (int c = 0; c < kQ6PiecesPerLane; c++) {
+    const int pc = lane + 64 * c;
+    sp.p[c] = ld_stream16(a0 + 16u * (uint32_t)(pc < pieces ? pc : pieces - 1));
+  }
+}
+
+// A lane's operands of one Q6_K unit (q6k_unit) from a span staged in LDS: the
+// super-block at LDS offset b, half h, l0 = 0 or 16.
+struct Q6Lane {
+  uint32_t qlA[4], qlB[4], qh[4];
+  int sc[4];
+  float dx;
+};
+
+__device__ __forceinline__ void load_q6_lane(const uint8_t* buf, int b, int h, int l0, Q6Lane& u) {
+  uint32_t s4[2];
+  lds_words<4>(buf, b + 64 * h + l0, u.qlA);
+  lds_words<4>(buf, b + 64 * h + 32 + l0, u.qlB);
+  lds_words<4>(buf, b + 128 + 32 * h + l0, u.qh);
+  lds_words<2>(buf, b + 192 + 8 * h, s4);  // scales 8h .. 8h+7
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int gg = (l0 >> 4) + 2 * t;
+    u.sc[t] = (int)(int8_t)((s4[gg >> 2] >> (8 * (gg & 3))) & 0xFF);
+  }
+  u.dx = h2f((uint16_t)lds_u16(buf, b + 208));
+}
+
 // Dynamic LDS past 64 KiB needs the kernel's limit raised (to the 160 KiB of
 // a CU), once per kernel function.
 inline hipError_t set_max_dynamic_lds(const void* fn) {

@@ -23,42 +23,6 @@ namespace qmm {
 
 namespace {
 
-constexpr int kSpanSb = 16;                            // super-blocks per span
-constexpr int kSpanBytes = kSpanSb * 210;              // 3360
-constexpr int kSpanPieces = (kSpanBytes + 15) / 16 + 1; // 16-byte pieces, start not aligned: 211
-constexpr int kPiecesPerLane = (kSpanPieces + 63) / 64; // 4
-// LDS bytes per wave: the pieces, and the 8 bytes past the last that the
-// dword reads of lds_words may touch
-constexpr int kSpanBuf = kSpanPieces * 16 + 16;
-
-struct Span {
-  uint4 p[kPiecesPerLane];
-  int off;  // offset of the span's first byte in its first piece
-  int len;  // super-blocks in the span
-};
-
-// Loads the 16-byte aligned pieces (aligned as device addresses) from the one
-// holding byte p to the one holding byte p + len*210 - 1. Every piece read
-// holds at least one byte of the span, and an aligned piece never crosses a
-// page, so the bytes read beyond the span stay in mapped memory. Lane L holds
-// pieces L + 64c.
-__device__ __forceinline__ void load_span(Span& sp, const uint8_t* __restrict__ p, int len, int lane) {
-  // rounded down by pointer arithmetic: the compiler keeps these global
-  // loads (an integer round trip would make them flat loads, which every LDS
-  // wait also waits for)
-  sp.off = (int)((uintptr_t)p & 15);
-  const uint8_t* a0 = p - sp.off;
-  sp.len = len;
-  const int pieces = (int)((sp.off + len * 210 + 15) >> 4);
-  // every lane loads (no branches): lanes past the span's pieces load its
-  // last piece again, whose bytes are never read
-#pragma unroll
-  for (int c = 0; c < kPiecesPerLane; c++) {
-    const int pc = lane + 64 * c;
-    sp.p[c] = ld_stream16(a0 + 16u * (uint32_t)(pc < pieces ? pc : pieces - 1));
-  }
-}
-
 // Work: each wave owns whole rows, gw, gw + W, ... (gw its index among the
 // W waves of the grid), and walks their spans in order with the loads of the
 // next kPfd spans in flight in a register ring (the loop is unrolled by kPfd,
@@ -95,12 +59,12 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const ActLds s = act_lds(smem, NR, nsb);
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* const buf = smem + (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + (size_t)wv * kSpanBuf;
+  uint8_t* const buf = smem + (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + (size_t)wv * kQ6SpanBuf;
   const int k = nsb * 256;
   const int64_t rowbytes = (int64_t)nsb * 210;
   // row numbers fit an int (the host checks)
   const int n_total = (int)tg.row_end[tg.count - 1];
-  const int nspan = (nsb + kSpanSb - 1) / kSpanSb;
+  const int nspan = (nsb + kQ6SpanSb - 1) / kQ6SpanSb;
   const int gw = blockIdx.x * kWaves + wv;
   // spans of this wave: its rows times the spans of a row
   const int nrows = gw < n_total ? (n_total - 1 - gw) / W + 1 : 0;
@@ -121,17 +85,17 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
   int lR = gw, lsp = 0;
   const uint8_t* lrow = nullptr;
   const uint8_t* const idle = FUSED ? (const uint8_t*)x : (const uint8_t*)yq;
-  auto load_next = [&](Span& sp) {
+  auto load_next = [&](Q6Span& sp) {
     if (lsp == 0 && lR < n_total) {
       int lr;
       const int t = target_of(lR, lr);
       lrow = (const uint8_t*)tg.w[t] + (int64_t)lr * rowbytes;
     }
-    const int s0 = lsp * kSpanSb;
+    const int s0 = lsp * kQ6SpanSb;
     if (lR < n_total)
-      load_span(sp, lrow + (int64_t)s0 * 210, nsb - s0 < kSpanSb ? nsb - s0 : kSpanSb, lane);
+      load_q6_span(sp, lrow + (int64_t)s0 * 210, nsb - s0 < kQ6SpanSb ? nsb - s0 : kQ6SpanSb, lane);
     else
-      load_span(sp, idle, 1, lane);
+      load_q6_span(sp, idle, 1, lane);
     if (++lsp == nspan) {
       lsp = 0;
       lR += W;
@@ -141,7 +105,7 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
   // 1. activation loads, then the first spans' loads
   ActBatch<NR, FUSED, kWaves> act;
   act.load(nsb, x, xstride, yq, yd, ybs);
-  Span ring[kPfd];
+  Q6Span ring[kPfd];
 #pragma unroll
   for (int j = 0; j < kPfd; j++) load_next(ring[j]);
 
@@ -157,13 +121,13 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
 #pragma unroll
   for (int r = 0; r < NR; r++) tot[r] = 0.0f;
 
-  auto step = [&](Span& cur, int sigma) {
+  auto step = [&](Q6Span& cur, int sigma) {
     // the span into this wave's LDS buffer (the previous span's reads are done)
     wave_lds_sync();
 #pragma unroll
-    for (int c = 0; c < kPiecesPerLane; c++) {
+    for (int c = 0; c < kQ6PiecesPerLane; c++) {
       const int pc = lane + 64 * c;
-      *(uint4*)(buf + 16 * (pc < kSpanPieces ? pc : kSpanPieces - 1)) = cur.p[c];
+      *(uint4*)(buf + 16 * (pc < kQ6SpanPieces ? pc : kQ6SpanPieces - 1)) = cur.p[c];
     }
     wave_lds_sync();
     const int off = cur.off, len = cur.len;
@@ -174,20 +138,9 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
 #pragma unroll
     for (int r = 0; r < NR; r++) acc[r] = 0.0f;
     if (sbl < len) {
-      const int b = off + 210 * sbl;
-      uint32_t qlA[4], qlB[4], qh[4], s4[2];
-      lds_words<4>(buf, b + 64 * h + l0, qlA);
-      lds_words<4>(buf, b + 64 * h + 32 + l0, qlB);
-      lds_words<4>(buf, b + 128 + 32 * h + l0, qh);
-      lds_words<2>(buf, b + 192 + 8 * h, s4);  // scales 8h .. 8h+7
-      int sc[4];
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const int gg = (l0 >> 4) + 2 * t;
-        sc[t] = (int)(int8_t)((s4[gg >> 2] >> (8 * (gg & 3))) & 0xFF);
-      }
-      const float dx = h2f((uint16_t)lds_u16(buf, b + 208));
-      const int sb = sp * kSpanSb + sbl;
+      Q6Lane u;
+      load_q6_lane(buf, off + 210 * sbl, h, l0, u);
+      const int sb = sp * kQ6SpanSb + sbl;
 #pragma unroll
       for (int r = 0; r < NR; r++) {
         const int8_t* yrow = s.codes + r * k + sb * 256 + 128 * h + l0;
@@ -198,7 +151,7 @@ __global__ __launch_bounds__(1024) void mv_q6k_stream_kernel(MvTargets tg, int n
           yv[t][0] = q.x; yv[t][1] = q.y; yv[t][2] = q.z; yv[t][3] = q.w;
           bs[t] = s.s16[(r * nsb + sb) * 16 + 8 * h + 2 * t + (l0 >> 4)];
         }
-        acc[r] = q6k_unit(qlA, qlB, qh, sc, dx, yv, s.dy[r * nsb + sb], bs, acc[r]);
+        acc[r] = q6k_unit(u.qlA, u.qlB, u.qh, u.sc, u.dx, yv, s.dy[r * nsb + sb], bs, acc[r]);
       }
     }
     // the span's sum, added to its row's in span order
@@ -236,7 +189,7 @@ hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xs
   if (n_total >= ((int64_t)1 << 30)) return hipErrorInvalidValue;  // row numbers are ints in the kernel
   int waves = cus * 16;
   if (waves > n_total) waves = (int)((n_total + 15) / 16 * 16);
-  const size_t lds = (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + 16 * (size_t)kSpanBuf;
+  const size_t lds = (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + 16 * (size_t)kQ6SpanBuf;
   const dim3 grid((unsigned)(waves / 16));
   if (pre) {
     auto* kfn = &mv_q6k_stream_kernel<NR, false>;

@@ -461,11 +461,12 @@ int qmm_moe_forward(int type, const void* w, int num_experts, const float* x, in
                     const int32_t* sorted_ids, const int32_t* expert_ids, const float* topk_w, int topk, float* dst,
                     int64_t ldd, void* workspace, size_t workspace_bytes, size_t* need, int64_t k, int64_t n,
                     int64_t size_m, int launch, int64_t stream) {
-  if (!qmm::moe_supported(type) || !shape_ok(type, k, n, size_m) || need == nullptr || ldd < n || x_stride < k ||
+  if (!qmm::moe_supported(type, k) || !shape_ok(type, k, n, size_m) || need == nullptr || ldd < n || x_stride < k ||
       num_experts < 1 || topk < 1 || (topk_w == nullptr && size_m % topk != 0) || size_m > ((int64_t)1 << 30))
     return QMM_UNSUPPORTED;
   const int64_t in_rows = topk_w ? size_m : size_m / topk;
-  const size_t act = (qmm::act_bytes(qmm::ACT_Q8_0, k, in_rows) + 255) / 256 * 256;
+  const int layout = qmm::moe_act_layout(type);
+  const size_t act = (qmm::act_bytes(layout, k, in_rows) + 255) / 256 * 256;
   const size_t bytes = act + qmm::moe_runs_bytes(size_m);
   *need = bytes;
   if (!launch) return QMM_OK;
@@ -474,14 +475,20 @@ int qmm_moe_forward(int type, const void* w, int num_experts, const float* x, in
   if (!w || !x || !dst || !sorted_ids || !expert_ids) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
-  // the activation's Q8_0 planes and the run table, one launch; then the grouped kernel
+  // the activation's planes (Q8_K for Q4_K / Q6_K, else Q8_0) and the run
+  // table, one launch; then the grouped kernel
   int32_t* runs = (int32_t*)((char*)workspace + act);
-  if (qmm::launch_act_quantize_moe(x, x_stride, k, in_rows, workspace, expert_ids, size_m, runs, st) != hipSuccess)
+  if (qmm::launch_act_quantize_moe(layout, x, x_stride, k, in_rows, workspace, expert_ids, size_m, runs, q8k_scale(),
+                                   st) != hipSuccess)
     return QMM_DEVICE_ERROR;
-  const qmm::ActPlanes p = qmm::act_planes(qmm::ACT_Q8_0, workspace, k, in_rows);
-  if (qmm::launch_moe(type, w, num_experts, n, k, p, runs, sorted_ids, topk_w, topk, size_m, dst, ldd,
-                      (int)cu_count(), st) != hipSuccess)
-    return QMM_DEVICE_ERROR;
+  const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, in_rows);
+  const hipError_t e =
+      layout == qmm::ACT_Q8K
+          ? qmm::launch_moe_kq(type, w, num_experts, n, k, p, runs, sorted_ids, topk_w, topk, size_m, dst, ldd,
+                               (int)cu_count(), st)
+          : qmm::launch_moe(type, w, num_experts, n, k, p, runs, sorted_ids, topk_w, topk, size_m, dst, ldd,
+                            (int)cu_count(), st);
+  if (e != hipSuccess) return QMM_DEVICE_ERROR;
   g_moe_launches.fetch_add(1, std::memory_order_relaxed);
   return QMM_OK;
 }

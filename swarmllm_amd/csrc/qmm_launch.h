@@ -42,10 +42,12 @@ ActPlanes act_planes(int layout, void* base, int64_t k, int64_t rows);
 // ---- launchers (return hipSuccess or the launch error) ---------------------
 hipError_t launch_act_quantize(int layout, const float* x, int64_t stride, int64_t k, int64_t rows,
                                void* out, float q8k_scale, hipStream_t s);
-// ACT_Q8_0 quantization for a grouped expert product, which also writes
-// its run table (1 + 3 size_m ints) from expert_ids in the same launch.
-hipError_t launch_act_quantize_moe(const float* x, int64_t stride, int64_t k, int64_t rows, void* out,
-                                   const int32_t* expert_ids, int64_t size_m, int32_t* runs, hipStream_t s);
+// The activation quantization of a grouped expert product (layout ACT_Q8_0
+// for the 32-value formats, ACT_Q8K for Q4_K and Q6_K), which also writes its
+// run table (1 + 3 size_m ints) from expert_ids in the same launch.
+hipError_t launch_act_quantize_moe(int layout, const float* x, int64_t stride, int64_t k, int64_t rows, void* out,
+                                   const int32_t* expert_ids, int64_t size_m, int32_t* runs, float q8k_scale,
+                                   hipStream_t s);
 hipError_t launch_weight_quantize(int type, const float* x, void* w, int64_t nelem, void* scratch,
                                   hipStream_t s);
 size_t weight_quantize_scratch_bytes(int type, int64_t nelem);
@@ -106,12 +108,18 @@ hipError_t launch_fill_normal(float* out, int64_t n, uint64_t seed, float mean, 
 // ---- prefill GEMM on the int8 matrix cores --------------------------------
 // dst = x · Wᵀ for a Q4_K weight from the Q8_K activation planes of `rows`
 // rows (qmm_quantize_act ACT_Q8K); used from gemm_q4k_min_rows() rows up.
-// Grouped expert products (moe.hip): types it covers, bytes of the run table
+// Grouped expert products (moe.hip, moe_kq.hip): the types and row lengths
+// covered, the activation layout each quantizes to, bytes of the run table
 // for size_m routing entries, and the grouped kernel's launch from an
-// activation already quantized in Q8_0 planes and its run table
+// activation already quantized in that layout and its run table
 // (launch_act_quantize_moe).
-bool moe_supported(int type);
+bool moe_supported(int type, int64_t k);
+int moe_act_layout(int type);
 size_t moe_runs_bytes(int64_t size_m);
+bool moe_kq_supported(int type, int64_t k);
+hipError_t launch_moe_kq(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
+                         const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
+                         float* dst, int64_t ldd, int cus, hipStream_t st);
 hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                       const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                       float* dst, int64_t ldd, int cus, hipStream_t st);

@@ -67,11 +67,16 @@ ActPlanes act_rows(int layout, const ActPlanes& p, int64_t k, int64_t r0) {
 // blocks per wave, through q8k_block_group16 (the routine the fused decode
 // kernels run in LDS).
 // ===========================================================================
-template <bool kVec>
+template <bool kVec, bool kRuns = false>
 __global__ __launch_bounds__(256) void act_q8k_kernel(const float* __restrict__ x, int64_t stride, int64_t k,
                                                       int64_t rows, int8_t* __restrict__ codes,
                                                       float* __restrict__ dout, int16_t* __restrict__ bsout,
-                                                      float qmax) {
+                                                      float qmax, const int32_t* __restrict__ expert_ids = nullptr,
+                                                      int size_m = 0, int32_t* __restrict__ runs = nullptr) {
+  if (kRuns && blockIdx.x == gridDim.x - 1) {
+    moe_runs_block<256>(expert_ids, size_m, runs);
+    return;
+  }
   const int lane = threadIdx.x & 63, gl = lane & 15;
   const int64_t nbk = k / 256;
   const int64_t blk = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
@@ -164,10 +169,22 @@ __global__ __launch_bounds__(256) void q8_0_kernel(const float* __restrict__ x, 
   }
 }
 
-hipError_t launch_act_quantize_moe(const float* x, int64_t stride, int64_t k, int64_t rows, void* out,
-                                   const int32_t* expert_ids, int64_t size_m, int32_t* runs, hipStream_t st) {
-  const ActPlanes p = act_planes(ACT_Q8_0, out, k, rows);
+hipError_t launch_act_quantize_moe(int layout, const float* x, int64_t stride, int64_t k, int64_t rows, void* out,
+                                   const int32_t* expert_ids, int64_t size_m, int32_t* runs, float q8k_scale,
+                                   hipStream_t st) {
+  const ActPlanes p = act_planes(layout, out, k, rows);
   const bool vec = ((uintptr_t)x % 16 == 0) && (stride % 4 == 0);
+  if (layout == ACT_Q8K) {
+    const int64_t blocks = rows * (k / 256);
+    const dim3 grid((unsigned)((blocks + 15) / 16 + 1));  // + the run table's workgroup
+    if (vec)
+      act_q8k_kernel<true, true><<<grid, 256, 0, st>>>(x, stride, k, rows, p.codes, p.d, (int16_t*)p.sums, q8k_scale,
+                                                       expert_ids, (int)size_m, runs);
+    else
+      act_q8k_kernel<false, true><<<grid, 256, 0, st>>>(x, stride, k, rows, p.codes, p.d, (int16_t*)p.sums, q8k_scale,
+                                                        expert_ids, (int)size_m, runs);
+    return hipGetLastError();
+  }
   const int64_t threads = rows * (k / 32) * 8;
   const dim3 grid((unsigned)((threads + 255) / 256 + 1));  // + the run table's workgroup
   if (vec)

@@ -87,11 +87,18 @@ def test_moe_plans_without_a_device_and_rejects_bad_routing_shapes():
     st = L.qmm_moe_forward(39, None, 32, None, 2880, None, None, fake_w, 4, None, 2880, None, 0, ctypes.byref(need),
                            2880, 2880, 32, 0, 0)
     assert st == _lib.QMM_OK and need.value == (L.qmm_act_bytes(_lib.ACT_Q8_0, 2880, 32) + 255) // 256 * 256 + 4 * 97
-    # size_m not a multiple of topk without weights, K-quant types, no experts
+    # Q4_K / Q6_K experts quantize the activation per 256 values (Q8_K planes)
+    for t in (12, 14):
+        st = L.qmm_moe_forward(t, None, 128, None, 2048, None, None, None, 8, None, 768, None, 0,
+                               ctypes.byref(need), 2048, 768, 32, 0, 0)
+        assert st == _lib.QMM_OK
+        assert need.value == (L.qmm_act_bytes(_lib.ACT_Q8K, 2048, 4) + 255) // 256 * 256 + 4 * 97
+    # size_m not a multiple of topk without weights, K-quant rows past 16384
+    # values, no experts
     assert L.qmm_moe_forward(39, None, 32, None, 2880, None, None, None, 4, None, 5760, None, 0, ctypes.byref(need),
                              2880, 5760, 30, 0, 0) == _lib.QMM_UNSUPPORTED
-    assert L.qmm_moe_forward(12, None, 32, None, 4096, None, None, None, 4, None, 64, None, 0, ctypes.byref(need),
-                             4096, 64, 32, 0, 0) == _lib.QMM_UNSUPPORTED
+    assert L.qmm_moe_forward(12, None, 32, None, 16640, None, None, None, 4, None, 64, None, 0, ctypes.byref(need),
+                             16640, 64, 32, 0, 0) == _lib.QMM_UNSUPPORTED
     assert L.qmm_moe_forward(39, None, 0, None, 2880, None, None, None, 4, None, 64, None, 0, ctypes.byref(need),
                              2880, 64, 32, 0, 0) == _lib.QMM_UNSUPPORTED
 

@@ -1,5 +1,6 @@
 """Grouped expert products (qmm_moe_forward, the reference's moe_gemm_gguf /
-QMatMul::matmul_many) against the CPU oracle, through the C ABI.
+QMatMul::matmul_many) against the CPU oracle, through the C ABI, for the
+32-value formats (MXFP4, Q8_0, IQ4_NL) and the K-quants (Q4_K, Q6_K).
 
 Routing as BASELINE C4 draws it: N(0,1) router logits [tokens, experts],
 top-k per token with ties to the lower index, routing entries sorted by
@@ -24,7 +25,8 @@ from swarmllm_amd._lib import QMM_NO_ROOM, QMM_UNSUPPORTED, QMM_WORKSPACE_TOO_SM
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-MOE_TYPES = {"MXFP4": 39, "Q8_0": 8, "IQ4_NL": 20}
+MOE_TYPES = {"MXFP4": 39, "Q8_0": 8, "IQ4_NL": 20, "Q4_K": 12, "Q6_K": 14}
+KQUANT = {12, 14}
 
 
 def routing(tokens: int, experts: int, topk: int, seed: int):
@@ -82,7 +84,8 @@ def check_against_forward(stack, xs_dev, out, sorted_ids, expert_ids, topk_w, to
 @pytest.mark.parametrize("weighted", [False, True])
 def test_moe_parity_small(name, weighted):
     qtype = MOE_TYPES[name]
-    E, n, k, tokens, topk = 8, 96, 320, 6, 3
+    E, n, tokens, topk = 8, 96, 6, 3
+    k = 512 if qtype in KQUANT else 320
     seed = zlib.crc32(f"{name}-{weighted}".encode())
     sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, seed)
     stack = expert_stack(qtype, E, n, k, seed & 0xFFFF)
@@ -165,7 +168,7 @@ def test_moe_more_runs_than_experts():
     check_against_forward(stack, xs, got, sorted_ids, expert_ids, None, topk)
 
 
-@pytest.mark.parametrize("name", ["MXFP4", "Q8_0"])
+@pytest.mark.parametrize("name", ["MXFP4", "Q8_0", "Q4_K", "Q6_K"])
 def test_moe_prepass_form_matches_one_launch_form(name):
     """Routings above a decode step's size, and inputs whose rows are not
     16-byte aligned, take the runs pre-pass and the standalone quantizer;
@@ -234,8 +237,53 @@ def test_moe_status_paths():
     L.qmm_fail_next_launch()
     assert L.qmm_moe_forward(*args, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 4, 1, 0) == QMM_NO_ROOM
     assert L.qmm_moe_forward(*args, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 4, 1, 0) == 0
-    # per-token inputs need size_m to be a multiple of topk; Q4_K is not a grouped type here
+    # per-token inputs need size_m to be a multiple of topk; K-quant rows of
+    # more than 16384 values are not a grouped shape here
     assert L.qmm_moe_forward(*args, ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, 3, 1, 0) == QMM_UNSUPPORTED
-    args_q4k = (12,) + args[1:]
-    assert L.qmm_moe_forward(*args_q4k, ws.data_ptr(), ws.numel(), ctypes.byref(need), 256, n, 4, 1, 0) == \
-        QMM_UNSUPPORTED
+    for t in (12, 14):
+        args_kq = (t,) + args[1:]
+        assert L.qmm_moe_forward(*args_kq, None, 0, ctypes.byref(need), 16640, n, 4, 0, 0) == QMM_UNSUPPORTED
+
+
+def test_moe_kquant_qwen3_moe_like_shapes():
+    """Q4_K gate [768, 2048] and Q6_K down [2048, 768] over 128 experts,
+    4 tokens with top-8 routing (the expert shapes of a Qwen3-MoE layer):
+    every pair against the oracle and bit-identical to its qmm_forward."""
+    E, tokens, topk = 128, 4, 8
+    sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, 31)
+    before = lib().qmm_moe_launches()
+    gate = expert_stack(12, E, 768, 2048, 31)
+    x = np.random.default_rng(31).standard_normal((tokens, 2048)).astype(np.float32)
+    xs = t32(x)
+    y1 = moe_forward(xs, gate, t32(sorted_ids), t32(expert_ids), None, topk).cpu().numpy()
+    check_against_oracle(12, gate, x, y1, sorted_ids, expert_ids, None, topk)
+    check_against_forward(gate, xs, y1, sorted_ids, expert_ids, None, topk)
+    del gate
+    down = expert_stack(14, E, 2048, 768, 32)
+    x2 = np.random.default_rng(32).standard_normal((tokens * topk, 768)).astype(np.float32)
+    xs2 = t32(x2)
+    y2 = moe_forward(xs2, down, t32(sorted_ids), t32(expert_ids), t32(topk_w), topk).cpu().numpy()
+    check_against_oracle(14, down, x2, y2, sorted_ids, expert_ids, topk_w, topk)
+    check_against_forward(down, xs2, y2, sorted_ids, expert_ids, topk_w, topk)
+    assert lib().qmm_moe_launches() >= before + 2
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("k", [4352, 8448, 16384])
+def test_moe_kquant_long_rows(name, k):
+    """Rows past 16 super-blocks (Q4_K: two and four units a lane; Q6_K:
+    two and more spans), and at 16384 values fewer entries a chunk than the
+    run holds (the chunk's rows fill the LDS budget): 7 entries on one
+    expert, 2 on another."""
+    qtype = MOE_TYPES[name]
+    E, n, topk = 3, 40, 1
+    stack = expert_stack(qtype, E, n, k, k + qtype)
+    x = np.random.default_rng(k).standard_normal((9, k)).astype(np.float32)
+    xs = t32(x)
+    sorted_ids = np.arange(9, dtype=np.int32)
+    expert_ids = np.array([1] * 7 + [2] * 2, np.int32)
+    tw = np.random.default_rng(k + 1).uniform(0.1, 1.0, 9).astype(np.float32)
+    got = moe_into(stack, xs, k, sorted_ids, expert_ids, tw, topk, 9)
+    check_against_forward(stack, xs, got, sorted_ids, expert_ids, tw, topk)
+    sel = [0, 6, 8]
+    check_against_oracle(qtype, stack, x, got, sorted_ids[sel], expert_ids[sel], tw, topk)
