@@ -105,10 +105,41 @@ int qmm_matvec(int type, const void *w, const void *xq, float *dst, int64_t ldd,
  * int8 matrix-core kernels from 4 rows on weights of 2 MiB or more and for
  * 9-32 rows, then the int8 matrix-core GEMMs from 33 rows; for Q8_0, IQ4_NL
  * and MXFP4 the int8 matrix-core GEMM from 9 rows. Nothing is allocated.
- * Replaces swarm_mmq_matmul's launch step (mmq_entry.cu:162-203), which
- * multiplies the activation swarm_mmq_quantize produced. */
+ * The SWARMLLM_QMATMUL_MMQ switches below move these lines. Replaces
+ * swarm_mmq_matmul's launch step (mmq_entry.cu:162-203), which multiplies
+ * the activation swarm_mmq_quantize produced. */
 int qmm_matmul(int type, const void *w, const void *xq, float *dst, int64_t ldd, int64_t k, int64_t n,
                int64_t rows, int64_t stream);
+
+/* The reference's A/B switches for the matrix-core line, read from the
+ * environment once per process (quantized/cuda.rs:737-872):
+ *   SWARMLLM_QMATMUL_MMQ=dp4a|0|off|false: no matrix-core kernel; products
+ *     run on the decode kernels, qmm_matvec_max_rows() rows a launch;
+ *   SWARMLLM_QMATMUL_MMQ_MAX_ROWS=N: the matrix-core kernels take at most N rows;
+ *   SWARMLLM_QMATMUL_MMQ_MIN_ROWS=N: one few-rows line for every type;
+ *   SWARMLLM_QMATMUL_MMQ_FEW_ROWS_BYTES=B: the least weight bytes of a
+ *     few-rows product (0: any);
+ *   SWARMLLM_QMATMUL_MMQ_CAPTURED=0|off|false: products of at most
+ *     qmm_matvec_max_rows() rows on a stream being captured stay on the
+ *     decode kernels.
+ * qmm_mmq_few_rows_line gives a type's line as this process reads it
+ * (mmq_few_rows_line, cuda.rs:850-872): products of fewest..8 rows against
+ * a weight of least_bytes or more go to the matrix cores.
+ * qmm_mmq_max_rows: the most rows a matrix-core kernel takes (0 when the
+ * switch is off). qmm_mmq_captured: 0 when captured few-rows products stay
+ * on the decode kernels. */
+int qmm_mmq_few_rows_line(int type, int64_t *fewest_rows, int64_t *least_bytes);
+int64_t qmm_mmq_max_rows(void);
+int qmm_mmq_captured(void);
+
+/* set_force_dmmv (quantized/cuda.rs:29-33): while on, qmm_forward,
+ * qmm_forward_shared and qmm_forward_glu dequantize each weight value (as
+ * qmm_dequantize does) against the f32 activation and sum in f32, without
+ * quantizing the activation: the reference's dequantize_mul_mat_vec and
+ * dequantize + f32 matmul path (cuda.rs:1653-1745). Grouped products and the
+ * entry points that take a quantized activation are not affected. */
+void qmm_set_force_dmmv(int on);
+int qmm_force_dmmv(void);
 
 /* dst = x · Wᵀ for any rows, from an f32 activation: quantizes it into the
  * workspace and picks the kernel by rows (the QCudaStorage::fwd policy,

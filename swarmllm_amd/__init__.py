@@ -3,6 +3,8 @@ over GGUF Q8_0, Q4_K, Q6_K, IQ4_NL, MXFP4) as hand-written HIP kernels for
 AMD Instinct MI355X (gfx950), behind the C ABI of include/qmm.h."""
 
 from ._lib import QmmError, lib  # noqa: F401
-from .qtensor import GgmlDType, QMatMul, QTensor, fill_normal, forward_glu, glu, moe_forward  # noqa: F401
+from .qtensor import (GgmlDType, QMatMul, QTensor, fill_normal, forward_glu, glu, mmq_few_rows_line,  # noqa: F401
+                      moe_forward, set_force_dmmv)
 
-__all__ = ["GgmlDType", "QMatMul", "QTensor", "QmmError", "fill_normal", "forward_glu", "glu", "lib", "moe_forward"]
+__all__ = ["GgmlDType", "QMatMul", "QTensor", "QmmError", "fill_normal", "forward_glu", "glu", "lib",
+           "mmq_few_rows_line", "moe_forward", "set_force_dmmv"]

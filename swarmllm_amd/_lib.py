@@ -34,6 +34,11 @@ SIGNATURES = {
     "qmm_act_planes": (_I, [_I, _I64, _I64, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "qmm_quantize_act": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64]),
     "qmm_matvec_max_rows": (_I, []),
+    "qmm_mmq_few_rows_line": (_I, [_I, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
+    "qmm_mmq_max_rows": (_I64, []),
+    "qmm_mmq_captured": (_I, []),
+    "qmm_set_force_dmmv": (None, [_I]),
+    "qmm_force_dmmv": (_I, []),
     "qmm_matvec": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64]),
     "qmm_matmul": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64]),
     "qmm_forward": (_I, [_I, _P, _P, _I64, _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64, _I64, _I64, _I, _I64]),

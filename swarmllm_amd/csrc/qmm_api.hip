@@ -17,6 +17,9 @@ std::atomic<uint64_t> g_matvec_launches{0};
 std::atomic<uint64_t> g_gemm_launches{0};
 std::atomic<bool> g_fail_next{false};
 std::atomic<uint64_t> g_moe_launches{0};
+// set_force_dmmv (quantized/cuda.rs:29-33): products of qmm_forward and its
+// shared / GLU forms dequantize the weight against the f32 activation.
+std::atomic<bool> g_force_dmmv{false};
 
 int block_size(int type) {
   switch (type) {
@@ -80,15 +83,100 @@ int cu_count() {
 // The reference's few-rows line (mmq_takes_few_rows, mmq_fewest_rows_default,
 // quantized/cuda.rs:775-839): K-quant products of 4 to 8 rows against a
 // weight of 2 MiB or more go to the matrix cores, as do all of more than 8.
+// The 32-value formats keep the decode kernels to 8 rows (their GEMM from 9:
+// on MI355X the decode kernels read such a weight faster than a 128-row tile
+// of 7-8 useful rows computes it).
 constexpr int64_t kFewRowsLeastBytes = (int64_t)2 << 20;
 constexpr int kFewRowsKQuant = 4;
+
+// The reference's A/B switches for that line, each read once
+// (quantized/cuda.rs:737-872):
+//   SWARMLLM_QMATMUL_MMQ=dp4a|0|off|false   no matrix-core kernel (products
+//       past the decode rows run on the decode kernels, 8 rows a launch);
+//   SWARMLLM_QMATMUL_MMQ_MAX_ROWS=N         the matrix-core kernels take at most N rows;
+//   SWARMLLM_QMATMUL_MMQ_MIN_ROWS=N         one few-rows line for every type
+//       (N > 8: never below 9 rows);
+//   SWARMLLM_QMATMUL_MMQ_FEW_ROWS_BYTES=B   the least weight bytes for a few-rows product (0: any);
+//   SWARMLLM_QMATMUL_MMQ_CAPTURED=0|off|false  products of at most 8 rows on a
+//       stream being captured stay on the decode kernels.
+// A value that does not parse as a count leaves the default, as there.
+struct MmqPolicy {
+  bool on = true;
+  int64_t max_rows = INT64_MAX;
+  int64_t min_rows = -1;  // -1: per type
+  int64_t few_bytes = kFewRowsLeastBytes;
+  bool captured = true;
+};
+
+bool env_is_off(const char* v) {
+  return v && (std::strcmp(v, "0") == 0 || std::strcmp(v, "off") == 0 || std::strcmp(v, "false") == 0);
+}
+
+// A decimal count (usize::parse: digits only, no sign or space), or -1.
+int64_t env_count(const char* name) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return -1;
+  int64_t r = 0;
+  for (const char* c = v; *c; c++) {
+    if (*c < '0' || *c > '9') return -1;
+    if (r > (INT64_MAX - 9) / 10) return INT64_MAX;
+    r = r * 10 + (*c - '0');
+  }
+  return r;
+}
+
+const MmqPolicy& mmq_policy() {
+  static const MmqPolicy pol = [] {
+    MmqPolicy p;
+    const char* v = std::getenv("SWARMLLM_QMATMUL_MMQ");
+    p.on = !(env_is_off(v) || (v && std::strcmp(v, "dp4a") == 0));
+    const int64_t mx = env_count("SWARMLLM_QMATMUL_MMQ_MAX_ROWS");
+    if (mx >= 0) p.max_rows = mx;
+    p.min_rows = env_count("SWARMLLM_QMATMUL_MMQ_MIN_ROWS");
+    const int64_t fb = env_count("SWARMLLM_QMATMUL_MMQ_FEW_ROWS_BYTES");
+    if (fb >= 0) p.few_bytes = fb;
+    p.captured = !env_is_off(std::getenv("SWARMLLM_QMATMUL_MMQ_CAPTURED"));
+    return p;
+  }();
+  return pol;
+}
+
+bool is_kquant(int type) { return type == qmm::T_Q4_K || type == qmm::T_Q6_K; }
+
+// The few-rows line of a type: (fewest rows, least weight bytes).
+void few_rows_line(int type, int64_t& rows, int64_t& bytes) {
+  const MmqPolicy& pol = mmq_policy();
+  rows = pol.min_rows >= 0 ? pol.min_rows : (is_kquant(type) ? kFewRowsKQuant : qmm::gemm_b32_min_rows());
+  bytes = pol.few_bytes;
+}
+
+bool stream_is_capturing(hipStream_t st) {
+  hipStreamCaptureStatus s = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(st, &s);
+  if (e != hipSuccess) (void)hipGetLastError();
+  return e == hipSuccess && s != hipStreamCaptureStatusNone;
+}
+
+// Whether a product of rows <= matvec_max_rows() against wbytes of weight
+// goes to a matrix-core kernel (mmq_takes_few_rows, cuda.rs:823-839).
+bool few_rows_take(int type, int64_t rows, int64_t wbytes, hipStream_t st) {
+  int64_t fewest, least;
+  few_rows_line(type, fewest, least);
+  if (rows < (fewest > 2 ? fewest : 2) || wbytes < least) return false;
+  return mmq_policy().captured || !stream_is_capturing(st);
+}
+
+bool mmq_allows(int64_t rows) {
+  const MmqPolicy& pol = mmq_policy();
+  return pol.on && rows <= pol.max_rows;
+}
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // The few-row matrix-core kernels (Q4_K, Q6_K): up to
 // gemm_q4k_skinny_max_rows() rows past the few-rows line.
-bool skinny_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows) {
-  if (rows > qmm::gemm_q4k_skinny_max_rows() || !aligned16(w) || !aligned16(xq)) return false;
+bool skinny_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows, hipStream_t st) {
+  if (!mmq_allows(rows) || rows > qmm::gemm_q4k_skinny_max_rows() || !aligned16(w) || !aligned16(xq)) return false;
   int64_t wbytes;
   if (type == qmm::T_Q4_K && qmm::gemm_q4k_skinny_fits(k, rows))
     wbytes = n * (k / 256) * 144;
@@ -97,7 +185,7 @@ bool skinny_takes(int type, const void* w, const void* xq, int64_t n, int64_t k,
   else
     return false;
   if (rows > qmm::matvec_max_rows()) return true;
-  return rows >= kFewRowsKQuant && wbytes >= kFewRowsLeastBytes;
+  return few_rows_take(type, rows, wbytes, st);
 }
 
 hipError_t launch_skinny(int type, const qmm::MvTargets& t, int64_t k, const qmm::ActPlanes& p, int64_t rows,
@@ -107,14 +195,22 @@ hipError_t launch_skinny(int type, const qmm::MvTargets& t, int64_t k, const qmm
 }
 
 // The tiled int8 matrix-core GEMMs: Q4_K and Q6_K past the skinny kernels'
-// rows, Q8_0 / IQ4_NL / MXFP4 past the decode kernels' rows; weight and
-// quantized activation 16-byte aligned (their 16-byte copies), sizes inside
-// their 32-bit offsets.
-bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows) {
-  if (!aligned16(w) || !aligned16(xq)) return false;
+// rows, Q8_0 / IQ4_NL / MXFP4 past the decode kernels' rows (or from the
+// few-rows line, where SWARMLLM_QMATMUL_MMQ_MIN_ROWS moves it below); weight
+// and quantized activation 16-byte aligned (their 16-byte copies), sizes
+// inside their 32-bit offsets.
+bool gemm_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows, hipStream_t st) {
+  if (!mmq_allows(rows) || !aligned16(w) || !aligned16(xq)) return false;
   if (type == qmm::T_Q4_K) return rows >= qmm::gemm_q4k_min_rows() && qmm::gemm_q4k_fits(n, k, rows);
   if (type == qmm::T_Q6_K) return rows >= qmm::gemm_q6k_min_rows() && qmm::gemm_q6k_fits(n, k, rows);
-  return rows >= qmm::gemm_b32_min_rows() && qmm::gemm_b32_fits(type, n, k, rows);
+  if (!qmm::gemm_b32_fits(type, n, k, rows)) return false;
+  if (rows > qmm::matvec_max_rows()) return true;
+  return few_rows_take(type, rows, n * (k / 32) * type_size(type), st);
+}
+
+// Whether a product goes to a matrix-core kernel rather than the decode kernels.
+bool matrix_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows, hipStream_t st) {
+  return gemm_takes(type, w, xq, n, k, rows, st) || skinny_takes(type, w, xq, n, k, rows, st);
 }
 
 // Q4_K: from 129 rows the single-pass GEMM (256-row tiles); 33-128 rows keep
@@ -250,6 +346,22 @@ int qmm_quantize_act(const float* x, void* xq, int layout, int64_t k, int64_t ro
 
 int qmm_matvec_max_rows(void) { return qmm::matvec_max_rows(); }
 
+void qmm_set_force_dmmv(int on) { g_force_dmmv.store(on != 0, std::memory_order_relaxed); }
+int qmm_force_dmmv(void) { return g_force_dmmv.load(std::memory_order_relaxed) ? 1 : 0; }
+
+int qmm_mmq_few_rows_line(int type, int64_t* rows, int64_t* bytes) {
+  if (block_size(type) == 0 || !rows || !bytes) return QMM_UNSUPPORTED;
+  few_rows_line(type, *rows, *bytes);
+  return QMM_OK;
+}
+
+int64_t qmm_mmq_max_rows(void) {
+  const MmqPolicy& pol = mmq_policy();
+  return pol.on ? pol.max_rows : 0;
+}
+
+int qmm_mmq_captured(void) { return mmq_policy().captured ? 1 : 0; }
+
 int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd, int64_t k, int64_t n, int64_t rows,
                int64_t stream) {
   if (!shape_ok(type, k, n, rows) || rows > qmm::matvec_max_rows() || ldd < n || !w || !xq || !dst)
@@ -271,12 +383,12 @@ int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd,
 // kernels a chunk of at most matvec_max_rows() rows at a time.
 int launch_product(int type, const void* w, int64_t n, int64_t k, const void* xq, const qmm::ActPlanes& p,
                    int layout, int64_t rows, float* dst, int64_t ldd, hipStream_t st) {
-  if (gemm_takes(type, w, xq, n, k, rows)) {
+  if (gemm_takes(type, w, xq, n, k, rows, st)) {
     if (launch_gemm(type, w, n, k, p, rows, dst, ldd, st) != hipSuccess) return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
   }
-  if (skinny_takes(type, w, xq, n, k, rows)) {
+  if (skinny_takes(type, w, xq, n, k, rows, st)) {
     qmm::MvTargets t{};
     t.w[0] = w;
     t.dst[0] = dst;
@@ -322,7 +434,10 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   if (!w || !x || !dst) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
-  if (stream_supported(type, k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
+  if (g_force_dmmv.load(std::memory_order_relaxed))
+    return status_of(qmm::launch_dmmv(type, w, n, k, x, x_stride, rows, dst, ldd, st));
+  if (stream_supported(type, k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride) &&
+      !matrix_takes(type, w, workspace, n, k, rows, st)) {
     // the activation is quantized inside the product's own launch
     const hipError_t e = launch_stream_targets(type, 1, &w, &n, &dst, &ldd, k, rows, x, x_stride, nullptr, st);
     if (e != hipSuccess) return QMM_DEVICE_ERROR;
@@ -351,7 +466,15 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
     if (!w[i] || !dst[i]) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
-  if (stream_supported(type, k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
+  if (g_force_dmmv.load(std::memory_order_relaxed)) {
+    for (int i = 0; i < count; i++)
+      if (qmm::launch_dmmv(type, w[i], n[i], k, x, x_stride, rows, dst[i], ldd[i], st) != hipSuccess)
+        return QMM_DEVICE_ERROR;
+    return QMM_OK;
+  }
+  bool fused = stream_supported(type, k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride);
+  for (int i = 0; fused && i < count; i++) fused = !matrix_takes(type, w[i], workspace, n[i], k, rows, st);
+  if (fused) {
     // one launch per kMaxTargets weights, each quantizing the activation in LDS
     for (int i0 = 0; i0 < count; i0 += qmm::kMaxTargets) {
       const int c = count - i0 < qmm::kMaxTargets ? count - i0 : qmm::kMaxTargets;
@@ -379,7 +502,8 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
     return QMM_OK;
   };
   for (int i = 0; i < count; i++) {
-    if (!gemm_takes(type, w[i], workspace, n[i], k, rows) && skinny_takes(type, w[i], workspace, n[i], k, rows)) {
+    if (!gemm_takes(type, w[i], workspace, n[i], k, rows, st) &&
+        skinny_takes(type, w[i], workspace, n[i], k, rows, st)) {
       grp.w[grp.count] = w[i];
       grp.dst[grp.count] = dst[i];
       grp.ldd[grp.count] = ldd[i];
@@ -412,7 +536,9 @@ int qmm_forward_glu(int type, int act, const void* w_gate, const void* w_up, con
   if (!w_gate || !w_up || !x || !dst) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
-  if (type == qmm::T_Q4_K && qmm::mv_q4k_glu_supported(k, rows) && qmm::mv_q4k_rows_fusable(x, x_stride)) {
+  if (type == qmm::T_Q4_K && !g_force_dmmv.load(std::memory_order_relaxed) && qmm::mv_q4k_glu_supported(k, rows) &&
+      qmm::mv_q4k_rows_fusable(x, x_stride) &&
+      !matrix_takes(type, w_gate, workspace, n, k, rows, st) && !matrix_takes(type, w_up, workspace, n, k, rows, st)) {
     if (qmm::launch_mv_q4k_glu(act, w_gate, w_up, n, k, rows, x, x_stride, nullptr, q8k_scale(), dst, ldd,
                                cu_count(), st) != hipSuccess)
       return QMM_DEVICE_ERROR;

@@ -52,6 +52,10 @@ hipError_t launch_weight_quantize(int type, const float* x, void* w, int64_t nel
                                   hipStream_t s);
 size_t weight_quantize_scratch_bytes(int type, int64_t nelem);
 hipError_t launch_dequantize(int type, const void* w, void* out, int out_f16, int64_t nelem, hipStream_t s);
+// dst = x · Wᵀ with each weight value dequantized (to_float) and the f32
+// activation unquantized, summed in f32: the set_force_dmmv path.
+hipError_t launch_dmmv(int type, const void* w, int64_t n, int64_t k, const float* x, int64_t xstride, int64_t rows,
+                       float* dst, int64_t ldd, hipStream_t s);
 // `p` points at the first of `rows` activation rows (planes already offset).
 hipError_t launch_matvec(int type, const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows,
                          float* dst, int64_t ldd, hipStream_t s);

@@ -638,34 +638,34 @@ __device__ __forceinline__ void put<float>(float* o, int64_t i, float v) { o[i] 
 template <>
 __device__ __forceinline__ void put<uint16_t>(uint16_t* o, int64_t i, float v) { o[i] = f2h(v); }
 
-template <typename OutT>
-__global__ __launch_bounds__(256) void dequant_kernel(int type, const uint8_t* __restrict__ w, OutT* __restrict__ y,
-                                                      int64_t ngroups) {
-  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;  // group of 32 outputs
-  if (g >= ngroups) return;
-  const int64_t base = g * 32;
+// The 32 values of group g (of 32 consecutive values) of a weight in GGUF
+// blocks of `type`, to_float's arithmetic.
+__device__ __forceinline__ void deq_group(int type, const uint8_t* __restrict__ w, int64_t g, float (&v)[32]) {
   switch (type) {
     case T_Q8_0: {
       const uint8_t* b = w + g * 34;
       const float d = h2f((uint16_t)(b[0] | (b[1] << 8)));
-      for (int j = 0; j < 32; j++) put(y, base + j, (float)(int8_t)b[2 + j] * d);
+#pragma unroll
+      for (int j = 0; j < 32; j++) v[j] = (float)(int8_t)b[2 + j] * d;
       break;
     }
     case T_MXFP4: {
       const uint8_t* b = w + g * 17;
       const float d = e8m0_half(b[0]);
+#pragma unroll
       for (int j = 0; j < 16; j++) {
-        put(y, base + j, (float)kMxfp4Values[b[1 + j] & 0xF] * d);
-        put(y, base + j + 16, (float)kMxfp4Values[b[1 + j] >> 4] * d);
+        v[j] = (float)kMxfp4Values[b[1 + j] & 0xF] * d;
+        v[j + 16] = (float)kMxfp4Values[b[1 + j] >> 4] * d;
       }
       break;
     }
     case T_IQ4_NL: {
       const uint8_t* b = w + g * 18;
       const float d = h2f((uint16_t)(b[0] | (b[1] << 8)));
+#pragma unroll
       for (int j = 0; j < 16; j++) {
-        put(y, base + j, d * (float)kIq4nlValues[b[2 + j] & 0xF]);
-        put(y, base + j + 16, d * (float)kIq4nlValues[b[2 + j] >> 4]);
+        v[j] = d * (float)kIq4nlValues[b[2 + j] & 0xF];
+        v[j + 16] = d * (float)kIq4nlValues[b[2 + j] >> 4];
       }
       break;
     }
@@ -679,11 +679,12 @@ __global__ __launch_bounds__(256) void dequant_kernel(int type, const uint8_t* _
       const float d1 = d * (float)sc, m1 = mn * (float)m;
       const uint8_t* q = b + 16 + 32 * (sub >> 1);
       const int shift = (sub & 1) ? 4 : 0;
-      for (int l = 0; l < 32; l++) put(y, base + l, d1 * (float)((q[l] >> shift) & 0xF) - m1);
+#pragma unroll
+      for (int l = 0; l < 32; l++) v[l] = d1 * (float)((q[l] >> shift) & 0xF) - m1;
       break;
     }
     case T_Q6_K: {
-      // group g: super-block sb, half h (0/1), quarter t (0..3) -> outputs 128h + 32t + l
+      // group g: super-block sb, half h (0/1), quarter t (0..3) -> values 128h + 32t + l
       const int64_t sb = g >> 3;
       const int h = (int)((g >> 2) & 1), t = (int)(g & 3);
       const uint8_t* b = w + sb * 210;
@@ -691,17 +692,92 @@ __global__ __launch_bounds__(256) void dequant_kernel(int type, const uint8_t* _
       const int8_t* sc = (const int8_t*)(b + 192) + 8 * h;
       const uint8_t* ql = b + 64 * h;
       const uint8_t* qh = b + 128 + 32 * h;
+#pragma unroll
       for (int l = 0; l < 32; l++) {
         const int lo = (t & 1) ? ql[l + 32] : ql[l];
         const int nib = (t & 2) ? (lo >> 4) : (lo & 0xF);
         const int q = (int)(int8_t)((nib | (((qh[l] >> (2 * t)) & 3) << 4)) - 32);
-        put(y, base + l, d * (float)sc[l / 16 + 2 * t] * (float)q);
+        v[l] = d * (float)sc[l / 16 + 2 * t] * (float)q;
       }
       break;
     }
     default:
+#pragma unroll
+      for (int l = 0; l < 32; l++) v[l] = 0.0f;
       break;
   }
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(256) void dequant_kernel(int type, const uint8_t* __restrict__ w, OutT* __restrict__ y,
+                                                      int64_t ngroups) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;  // group of 32 outputs
+  if (g >= ngroups) return;
+  float v[32];
+  deq_group(type, w, g, v);
+#pragma unroll
+  for (int j = 0; j < 32; j++) put(y, g * 32 + j, v[j]);
+}
+
+// The dequantize-then-multiply path the reference takes under set_force_dmmv
+// (dequantize_mul_mat_vec and the dequantize + f32 matmul of
+// quantized/cuda.rs:1653-1745): each weight value is dequantized as to_float
+// does, multiplied by the f32 activation and summed in f32, with no
+// activation quantization. A wave per weight row, lane L taking groups
+// L, L + 64, ... of 32 values; up to kDmmvRows activation rows a launch.
+constexpr int kDmmvRows = 8;
+
+__global__ __launch_bounds__(256) void dmmv_kernel(int type, const uint8_t* __restrict__ w, int64_t n, int64_t k,
+                                                   int64_t rowbytes, const float* __restrict__ x, int64_t xstride,
+                                                   int nr, float* __restrict__ dst, int64_t ldd) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;  // whole waves
+  const uint8_t* wr = w + row * rowbytes;
+  const int64_t groups = k / 32;
+  float acc[kDmmvRows];
+#pragma unroll
+  for (int r = 0; r < kDmmvRows; r++) acc[r] = 0.0f;
+  for (int64_t g = lane; g < groups; g += 64) {
+    float v[32];
+    deq_group(type, wr, g, v);
+#pragma unroll
+    for (int r = 0; r < kDmmvRows; r++) {
+      if (r >= nr) break;
+      const float* xp = x + r * xstride + g * 32;
+#pragma unroll
+      for (int l = 0; l < 32; l++) acc[r] = __fmaf_rn(v[l], xp[l], acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kDmmvRows; r++) {
+    if (r >= nr) break;
+    const float sum = wave_sum(acc[r]);
+    if (lane == 0) dst[r * ldd + row] = sum;
+  }
+}
+
+hipError_t launch_dmmv(int type, const void* w, int64_t n, int64_t k, const float* x, int64_t xstride, int64_t rows,
+                       float* dst, int64_t ldd, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  int64_t rowbytes;
+  switch (type) {
+    case T_Q8_0: rowbytes = k / 32 * 34; break;
+    case T_IQ4_NL: rowbytes = k / 32 * 18; break;
+    case T_MXFP4: rowbytes = k / 32 * 17; break;
+    case T_Q4_K: rowbytes = k / 256 * 144; break;
+    case T_Q6_K: rowbytes = k / 256 * 210; break;
+    default: return hipErrorInvalidValue;
+  }
+  const dim3 grid((unsigned)((n + 3) / 4));
+  for (int64_t r0 = 0; r0 < rows; r0 += kDmmvRows) {
+    const int nr = (int)(rows - r0 < kDmmvRows ? rows - r0 : kDmmvRows);
+    dmmv_kernel<<<grid, 256, 0, st>>>(type, (const uint8_t*)w, n, k, rowbytes, x + r0 * xstride, xstride, nr,
+                                      dst + r0 * ldd, ldd);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_dequantize(int type, const void* w, void* out, int out_f16, int64_t nelem, hipStream_t st) {

@@ -15,7 +15,7 @@ from __future__ import annotations
 import ctypes
 import enum
 from dataclasses import dataclass
-from typing import List, Optional, Sequence
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
@@ -380,6 +380,22 @@ def moe_forward(xs: torch.Tensor, experts: QTensor, sorted_ids: torch.Tensor, ex
     buf = (workspace or Workspace()).get(need.value, xs.device)
     check("qmm_moe_forward", L.qmm_moe_forward(*args, _ptr(buf), buf.numel(), ctypes.byref(need), k, n, size_m, 1, st))
     return out
+
+
+def set_force_dmmv(flag: bool) -> None:
+    """candle's quantized::cuda::set_force_dmmv (quantized/cuda.rs:29-33):
+    while set, QMatMul.forward / forward_shared / forward_glu dequantize the
+    weight against the f32 activation (no activation quantization)."""
+    lib().qmm_set_force_dmmv(1 if flag else 0)
+
+
+def mmq_few_rows_line(dtype: GgmlDType) -> Tuple[int, int]:
+    """(fewest rows, least weight bytes) of a product of up to 8 rows that
+    the matrix-core kernels take in this process, the environment read once
+    (quantized/cuda.rs:850-872, mmq_few_rows_line)."""
+    rows, nbytes = ctypes.c_int64(0), ctypes.c_int64(0)
+    check("qmm_mmq_few_rows_line", lib().qmm_mmq_few_rows_line(int(dtype), ctypes.byref(rows), ctypes.byref(nbytes)))
+    return rows.value, nbytes.value
 
 
 def quantize_act(x: torch.Tensor, layout: int) -> torch.Tensor:

@@ -120,3 +120,57 @@ def test_available_is_false_without_a_gfx950():
     if torch.cuda.is_available():
         pytest.skip("a device is present")
     assert lib().qmm_available() == 0
+
+
+def test_mmq_lines_default_and_force_dmmv_flag():
+    """The few-rows line as the reference draws it (K-quants from 4 rows,
+    2 MiB; the 32-value formats keep the decode kernels to 8 rows), no row
+    cap, captured products allowed; set_force_dmmv is a process flag."""
+    L = lib()
+    rows, nbytes = ctypes.c_int64(0), ctypes.c_int64(0)
+    for t, fewest in ((12, 4), (14, 4), (8, 9), (20, 9), (39, 9)):
+        assert L.qmm_mmq_few_rows_line(t, ctypes.byref(rows), ctypes.byref(nbytes)) == _lib.QMM_OK
+        assert (rows.value, nbytes.value) == (fewest, 2 << 20)
+    assert L.qmm_mmq_few_rows_line(3, ctypes.byref(rows), ctypes.byref(nbytes)) == _lib.QMM_UNSUPPORTED
+    assert L.qmm_mmq_max_rows() == 2**63 - 1 and L.qmm_mmq_captured() == 1
+    assert L.qmm_force_dmmv() == 0
+    L.qmm_set_force_dmmv(1)
+    assert L.qmm_force_dmmv() == 1
+    L.qmm_set_force_dmmv(0)
+    assert L.qmm_force_dmmv() == 0
+
+
+def _knobs_in_child(env: dict) -> list:
+    """The lines a fresh process reads with `env` added (the environment is read once)."""
+    import json
+    import os
+    import subprocess
+    import sys
+    code = ("import ctypes, json; from swarmllm_amd._lib import lib; L = lib(); r, b = ctypes.c_int64(), "
+            "ctypes.c_int64(); out = []\n"
+            "for t in (12, 8):\n"
+            "    L.qmm_mmq_few_rows_line(t, ctypes.byref(r), ctypes.byref(b)); out.append([r.value, b.value])\n"
+            "out.append([L.qmm_mmq_max_rows(), L.qmm_mmq_captured()]); print(json.dumps(out))")
+    full = dict(os.environ)
+    for k in list(full):
+        if k.startswith("SWARMLLM_QMATMUL_MMQ"):
+            del full[k]
+    full.update(env)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, "-c", code], env=full, cwd=root, capture_output=True, text=True,
+                         timeout=120, check=True)
+    return json.loads(res.stdout.strip().splitlines()[-1])
+
+
+def test_mmq_switches_read_from_the_environment():
+    assert _knobs_in_child({}) == [[4, 2 << 20], [9, 2 << 20], [2**63 - 1, 1]]
+    got = _knobs_in_child({"SWARMLLM_QMATMUL_MMQ_MIN_ROWS": "3", "SWARMLLM_QMATMUL_MMQ_FEW_ROWS_BYTES": "0",
+                           "SWARMLLM_QMATMUL_MMQ_MAX_ROWS": "100", "SWARMLLM_QMATMUL_MMQ_CAPTURED": "off"})
+    assert got == [[3, 0], [3, 0], [100, 0]]
+    # off in any of its spellings; counts that do not parse leave the default
+    for off in ("dp4a", "0", "off", "false"):
+        assert _knobs_in_child({"SWARMLLM_QMATMUL_MMQ": off})[2] == [0, 1]
+    got = _knobs_in_child({"SWARMLLM_QMATMUL_MMQ": "on", "SWARMLLM_QMATMUL_MMQ_MIN_ROWS": "-1",
+                           "SWARMLLM_QMATMUL_MMQ_FEW_ROWS_BYTES": "2 MiB", "SWARMLLM_QMATMUL_MMQ_MAX_ROWS": "x",
+                           "SWARMLLM_QMATMUL_MMQ_CAPTURED": "1"})
+    assert got == [[4, 2 << 20], [9, 2 << 20], [2**63 - 1, 1]]
