@@ -130,8 +130,14 @@ void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
   const int k = nsb * 256;
   const int64_t rowbytes = (int64_t)nsb * 144;
   const int64_t n_total = tg.row_end[tg.count - 1];
-  const int64_t W = (int64_t)gridDim.x * kWaves;
-  const int64_t gw = (int64_t)blockIdx.x * kWaves + wv;
+  // workgroup b owns rows [b N / G, (b + 1) N / G), its waves interleaved
+  // within: every CU streams the same number of rows (a stride over the whole
+  // grid leaves the CUs that host two workgroups of full waves a row in 7
+  // more: 14336 rows over 8192 waves, 64 against 48 rows a CU)
+  const int64_t G = gridDim.x;
+  const int64_t gw = (int64_t)blockIdx.x * n_total / G + wv;
+  const int64_t R_end = (int64_t)(blockIdx.x + 1) * n_total / G;
+  constexpr int64_t W = kWaves;
 
   auto row_ptr = [&](int64_t R, float*& out, int64_t& ldd) -> const uint8_t* {
     int t = 0;
@@ -154,7 +160,7 @@ void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
   RowRaw<T> craw;
   float* out = nullptr;
   int64_t ldd = 0;
-  if (gw < n_total) {
+  if (gw < R_end) {
     if (XCHG)
       load_raw<T>(craw, row_ptr(gw, out, ldd), nsb, lane);
     else
@@ -189,14 +195,22 @@ void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
       }
     }
 
-  // 3. stream the rows
-  for (int64_t R = gw; R < n_total; R += W) {
+  // 3. stream the rows. The results of a wave's first two rows are stored
+  // when its rows are done: a store in the loop would hold the wait for the
+  // next row's loads until the store is acknowledged (a wave's loads and
+  // stores share one counter; 0.3-0.5 us on C2's gate).
+  float keep0[NR], keep1[NR];
+  float* kout0 = nullptr;
+  float* kout1 = nullptr;
+  int64_t kldd0 = 0, kldd1 = 0;
+  int done = 0;
+  for (int64_t R = gw; R < R_end; R += W) {
     // PF: the next row's loads go out before this row's compute
     RowRegs<T> nxt;
     RowRaw<T> nraw;
     float* nout = nullptr;
     int64_t nldd = 0;
-    if (PF && R + W < n_total) {
+    if (PF && R + W < R_end) {
       if (XCHG)
         load_raw<T>(nraw, row_ptr(R + W, nout, nldd), nsb, lane);
       else
@@ -215,8 +229,22 @@ void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
 #pragma unroll
     for (int r = 0; r < NR; r++) {
       const float v = wave_sum_dpp(acc[r]);
-      if (lane == 0) out[r * ldd] = v;
+      if (done == 0) {
+        keep0[r] = v;
+      } else if (done == 1) {
+        keep1[r] = v;
+      } else if (lane == 0) {
+        out[r * ldd] = v;
+      }
     }
+    if (done == 0) {
+      kout0 = out;
+      kldd0 = ldd;
+    } else if (done == 1) {
+      kout1 = out;
+      kldd1 = ldd;
+    }
+    done++;
     if (PF) {
       if (XCHG)
         craw = nraw;
@@ -224,11 +252,18 @@ void mv_q4k_stream_kernel(MvTargets tg, int nsb, const float* __restrict__ x,
         cur = nxt;
       out = nout;
       ldd = nldd;
-    } else if (R + W < n_total) {
+    } else if (R + W < R_end) {
       if (XCHG)
         load_raw<T>(craw, row_ptr(R + W, out, ldd), nsb, lane);
       else
         load_row<T>(cur, row_ptr(R + W, out, ldd), nsb, lane);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      if (done > 0) kout0[r * kldd0] = keep0[r];
+      if (done > 1) kout1[r * kldd1] = keep1[r];
     }
   }
 }
