@@ -587,6 +587,91 @@ def c4_moe(stream, reps: int = 20, copies: int = 2) -> dict:
             "percent_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
 
 
+def moe_kquant(stream, reps: int = 10, copies: int = 2) -> dict:
+    """Grouped K-quant experts: 128 experts of a 2048-wide MoE layer (expert
+    width 768), gate_up [1536, 2048] in Q4_K and down [2048, 768] in Q6_K,
+    routed top-8 from seeded N(0,1) logits (entries sorted by expert, pair);
+    one step = the gate_up product (per-token inputs) and the down product
+    (per-pair inputs, routing weights), at a decode step (1 token) and at a
+    512-token prompt, over `copies` weight stacks. Decode reports the
+    touched experts' bytes per step; the prompt its int8 ops per step."""
+    import numpy as np
+    import torch
+
+    from swarmllm_amd import GgmlDType, QTensor, fill_normal
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    E, topk, hidden, inter = 128, 8, 2048, 768
+
+    def stack(t, n, k, seed):
+        parts = [QTensor.quantize(fill_normal(n * k, seed=(seed << 8) | i, std=0.02).reshape(n, k), GgmlDType(t))
+                 for i in range(E)]
+        return torch.cat([p.data_ for p in parts])
+
+    gu = [stack(Q4K, 2 * inter, hidden, 60 + 2 * c) for c in range(copies)]
+    dn = [stack(Q6K, hidden, inter, 61 + 2 * c) for c in range(copies)]
+    out = {}
+    for tokens in (1, 512):
+        rng = np.random.default_rng(6 + tokens)
+        logits = rng.standard_normal((tokens, E)).astype(np.float32)
+        choice = np.argsort(-logits, axis=1, kind="stable")[:, :topk]
+        pairs = sorted((int(choice[t, j]), t * topk + j) for t in range(tokens) for j in range(topk))
+        eids = torch.tensor([e for e, _ in pairs], dtype=torch.int32, device="cuda")
+        sids = torch.tensor([p for _, p in pairs], dtype=torch.int32, device="cuda")
+        sel = np.take_along_axis(logits, choice, axis=1).astype(np.float64)
+        wts = np.exp(sel - sel.max(axis=1, keepdims=True))
+        wts /= wts.sum(axis=1, keepdims=True)
+        topk_w = torch.tensor(wts.reshape(-1), dtype=torch.float32, device="cuda")
+        touched = len(set(e for e, _ in pairs))
+        size_m = tokens * topk
+        x1 = fill_normal(tokens * hidden, seed=(6 << 40) | tokens).reshape(tokens, hidden)
+        x2 = fill_normal(size_m * inter, seed=(7 << 40) | tokens).reshape(size_m, inter)
+        y1 = torch.empty((size_m, 2 * inter), dtype=torch.float32, device="cuda")
+        y2 = torch.empty((size_m, hidden), dtype=torch.float32, device="cuda")
+        need = ctypes.c_size_t(0)
+        check("qmm_moe_forward", L.qmm_moe_forward(Q4K, None, E, None, hidden, None, None, None, topk, None,
+                                                   2 * inter, None, 0, ctypes.byref(need), hidden, 2 * inter, size_m,
+                                                   0, 0))
+        ws1 = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+        check("qmm_moe_forward", L.qmm_moe_forward(Q6K, None, E, None, inter, None, None, ctypes.c_void_p(16), topk,
+                                                   None, hidden, None, 0, ctypes.byref(need), inter, hidden, size_m,
+                                                   0, 0))
+        ws2 = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+        before = L.qmm_moe_launches()
+
+        def fn(s):
+            for c in range(copies):
+                check("qmm_moe_forward", L.qmm_moe_forward(
+                    Q4K, gu[c].data_ptr(), E, x1.data_ptr(), hidden, sids.data_ptr(), eids.data_ptr(), None, topk,
+                    y1.data_ptr(), 2 * inter, ws1.data_ptr(), ws1.numel(), ctypes.byref(need), hidden, 2 * inter,
+                    size_m, 1, s))
+                check("qmm_moe_forward", L.qmm_moe_forward(
+                    Q6K, dn[c].data_ptr(), E, x2.data_ptr(), inter, sids.data_ptr(), eids.data_ptr(),
+                    topk_w.data_ptr(), topk, y2.data_ptr(), hidden, ws2.data_ptr(), ws2.numel(), ctypes.byref(need),
+                    inter, hidden, size_m, 1, s))
+
+        g = capture(fn, stream)
+        if L.qmm_moe_launches() < before + 2 * copies:
+            raise RuntimeError("the K-quant MoE step did not run the grouped kernels")
+        for _ in range(2):
+            g.replay()
+        ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+        us = ms * 1e3 / (reps * copies)
+        per_expert = 2 * inter * (hidden // 256) * 144 + hidden * (inter // 256) * 210
+        alg = touched * per_expert + 4 * (tokens * hidden + size_m * inter + size_m * 2 * inter + size_m * hidden)
+        ops = 2.0 * size_m * (2 * inter * hidden + hidden * inter)
+        key = "decode" if tokens == 1 else "prompt"
+        out[key] = {"tokens": tokens, "entries": size_m, "experts_touched": touched, "us_per_step": round(us, 3),
+                    "alg_bytes": alg, "gbs": round(alg / (us * 1e-6) / 1e9, 1),
+                    "tops": round(ops / (us * 1e-6) / 1e12, 2)}
+        log(f"K-quant MoE, {tokens} token(s): {us:.2f} us per step ({touched} experts touched), "
+            f"{out[key]['gbs']:.0f} GB/s, {out[key]['tops']:.1f} TOP/s")
+    out["workload"] = ("grouped K-quant experts: 128 experts, hidden 2048, expert width 768, gate_up Q4_K "
+                       "[1536, 2048] + down Q6_K [2048, 768], top-8, at 1 token and 512 tokens")
+    return out
+
+
 def c1_q8_0(stream, reps: int = 50, copies: int = 16) -> dict:
     """BASELINE C1 (the reference's CPU-runnable case) on the device: Q8_0
     4096 x 4096 (N(0,0.02), seed 0) against one N(0,1) row, rotated over
@@ -850,6 +935,7 @@ def main() -> int:
     if not args.no_extra:
         extra["c1"] = c1_q8_0(stream)
         extra["c4"] = c4_moe(stream)
+        extra["moe_kquant"] = moe_kquant(stream)
         extra["c5"] = c5_shard(stream)
         extra["prefill_b32"] = prefill_b32(stream)
 

@@ -45,9 +45,7 @@ __host__ __device__ inline size_t kq_act_bytes(int nsb, int pairs) {
 }
 
 template <int TYPE>
-__host__ __device__ inline size_t kq_stage_bytes() {
-  return TYPE == T_Q6_K ? (size_t)kKqWaves * kQ6SpanBuf : 0;
-}
+__host__ __device__ inline size_t kq_stage_bytes();
 
 // Q4_K: the header and the lane's 32 code bytes of each of its super-blocks
 // sbl + 16t of a row (mv_q4k.hip's per-lane layout).
@@ -68,27 +66,74 @@ __device__ __forceinline__ void load_q4_row(Q4Row<T>& rr, const uint8_t* __restr
   }
 }
 
-template <int TYPE, int T>
+// Q6_K rows of up to 16 / P super-blocks, P rows a wave: lane group q (G =
+// 64 / P lanes) stages row q's block span in its own slot of the wave's
+// buffer, 4 aligned 16-byte pieces a lane.
+template <int P>
+struct Q6Pack {
+  static constexpr int G = 64 / P;
+  static constexpr int kSlot = G * 4 * 16;  // bytes a row: the pieces (the span and its over-read fit)
+  uint4 p[4];
+  int off;
+};
+
+template <int P>
+__device__ __forceinline__ void load_q6_pack(Q6Pack<P>& sp, const uint8_t* __restrict__ row, int nsb, int pl) {
+  sp.off = (int)((uintptr_t)row & 15);
+  const uint8_t* a0 = row - sp.off;
+  const int pieces = (sp.off + nsb * 210 + 15) >> 4;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int pc = pl + Q6Pack<P>::G * c;
+    sp.p[c] = ld_stream16(a0 + 16u * (uint32_t)(pc < pieces ? pc : pieces - 1));
+  }
+}
+
+// LDS bytes a wave stages Q6_K spans in
+constexpr int kKqStageBuf = kQ6SpanBuf > 4 * 1024 + 16 ? kQ6SpanBuf : 4 * 1024 + 16;
+
+template <int TYPE>
+__host__ __device__ inline size_t kq_stage_bytes() {
+  return TYPE == T_Q6_K ? (size_t)kKqWaves * kKqStageBuf : 0;
+}
+
+// P weight rows a wave at a time (P = 2, 4 where a row's units take at most
+// 64 / P lanes: Q4_K and Q6_K rows of at most 8 or 4 super-blocks). Row q of
+// the P takes lanes [q G, (q + 1) G) with the 1-row decode kernel's lane
+// mapping inside them, and its sum is the 16-lane row sums of its lanes:
+// the 1-row kernel's wave sum (a + b) + (c + d) over the same units, whose
+// other rows of lanes hold no unit and add +0 (a sum of units is never -0:
+// every lane's sum starts at +0), so each row's result is bit-identical.
+template <int TYPE, int T, int P>
 __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
     const uint8_t* __restrict__ W, int64_t n, int nsb, int64_t estride, int num_experts,
     const int8_t* __restrict__ yq, const float* __restrict__ yd, const int16_t* __restrict__ ybs,
     const int32_t* __restrict__ runs, const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int topk,
     int size_m, float* __restrict__ dst, int64_t ldd, int rpw, int npairs) {
+  static_assert(P == 1 || T == 1, "packed rows take one unit a lane");
+  constexpr int G = 64 / P;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int k = nsb * 256;
   int8_t* const acodes = (int8_t*)smem;                                     // [P][k]
   int16_t* const asums = (int16_t*)(smem + (size_t)npairs * k);             // [P][nsb*16]
   float* const ad = (float*)(smem + (size_t)npairs * (k + 32 * nsb));       // [P][nsb]
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint8_t* const buf = smem + kq_act_bytes(nsb, npairs) + (size_t)wv * kQ6SpanBuf;  // Q6_K only
+  uint8_t* const buf = smem + kq_act_bytes(nsb, npairs) + (size_t)wv * kKqStageBuf;  // Q6_K only
 
   const int64_t rowbytes = (int64_t)nsb * (TYPE == T_Q4_K ? 144 : 210);
   const int64_t r0 = ((int64_t)blockIdx.x * kKqWaves + wv) * rpw;
   const int nrows = r0 < n ? (int)(n - r0 < rpw ? n - r0 : rpw) : 0;
-  // Q4_K lanes: chunk j of super-blocks sbl + 16t; Q6_K lanes: unit u of
-  // super-block sbl of a span (half h, l0)
-  const int j = lane & 3, sbl = lane >> 2, h = j >> 1, l0 = 16 * (j & 1);
+  const int iters = (nrows + P - 1) / P;
+  // the lane's row of a pack and its place in it: Q4_K chunk j of
+  // super-blocks sbl + 16t; Q6_K unit (half h, l0) of super-block sbl of a span
+  const int q = lane / G, pl = lane % G;
+  const int j = pl & 3, sbl = pl >> 2, h = j >> 1, l0 = 16 * (j & 1);
   const int nspan = (nsb + kQ6SpanSb - 1) / kQ6SpanSb;
+  // row of iteration it for this lane (the last row again past the wave's rows)
+  auto prow = [&](int it) -> int64_t {
+    const int r = it * P + q;
+    return r0 + (r < nrows ? r : nrows - 1);
+  };
 
   // Runs blockIdx.y, blockIdx.y + gridDim.y, ...; the loop and its barriers
   // are uniform over the workgroup.
@@ -102,6 +147,32 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
 
     for (int c0 = 0; c0 < len; c0 += npairs) {
       const int cnt = len - c0 < npairs ? len - c0 : npairs;
+      // the first rows' weight loads go out before the entries are looked up
+      Q4Row<T> q4cur;
+      Q6Pack<P> q6cur;
+      Q6Span q6s;
+      int lr = 0, lsp = 0;  // Q6_K, one row a wave: the span loaded next (span lsp of row r0 + lr)
+      auto load_next = [&](Q6Span& spn) {
+        if (lr < nrows) {
+          const int s0 = lsp * kQ6SpanSb;
+          load_q6_span(spn, We + (r0 + lr) * rowbytes + (int64_t)s0 * 210, nsb - s0 < kQ6SpanSb ? nsb - s0 : kQ6SpanSb,
+                       lane);
+        } else {
+          load_q6_span(spn, (const uint8_t*)yq, 1, lane);
+        }
+        if (++lsp == nspan) {
+          lsp = 0;
+          lr++;
+        }
+      };
+      if constexpr (TYPE == T_Q4_K) {
+        if (nrows > 0) load_q4_row<T>(q4cur, We + prow(0) * rowbytes, nsb, j, sbl);
+      } else if constexpr (P > 1) {
+        if (nrows > 0) load_q6_pack<P>(q6cur, We + prow(0) * rowbytes, nsb, pl);
+      } else {
+        load_next(q6s);
+      }
+
       int pr[kKqPairs];
 #pragma unroll
       for (int p = 0; p < kKqPairs; p++)
@@ -136,12 +207,40 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
       }
       __syncthreads();
 
+      // a pack's sums per entry, stored by lane 0 (the results are wave-uniform)
+      auto store = [&](int it, const float (&acc)[kKqPairs]) {
+#pragma unroll
+        for (int p = 0; p < kKqPairs; p++) {
+          if (!use[p]) continue;
+          float v[4];
+          if constexpr (P == 1) {
+            v[0] = wave_sum_dpp(acc[p]);
+          } else {
+            float a, b, c, d;
+            wave_row16_sums(acc[p], a, b, c, d);
+            if constexpr (P == 2) {
+              v[0] = __fadd_rn(a, b);
+              v[1] = __fadd_rn(c, d);
+            } else {
+              v[0] = a;
+              v[1] = b;
+              v[2] = c;
+              v[3] = d;
+            }
+          }
+          if (lane == 0) {
+#pragma unroll
+            for (int qq = 0; qq < P; qq++)
+              if (it * P + qq < nrows) dst[out_row[p] * ldd + r0 + it * P + qq] = __fmul_rn(v[qq], scale[p]);
+          }
+        }
+      };
+
       if constexpr (TYPE == T_Q4_K) {
-        // rows in order, the next row's loads in flight under this row's units
-        Q4Row<T> cur, nxt;
-        if (nrows > 0) load_q4_row<T>(cur, We + r0 * rowbytes, nsb, j, sbl);
-        for (int i = 0; i < nrows; i++) {
-          if (i + 1 < nrows) load_q4_row<T>(nxt, We + (r0 + i + 1) * rowbytes, nsb, j, sbl);
+        // rows in order, the next pack's loads in flight under this one's units
+        Q4Row<T> nxt;
+        for (int it = 0; it < iters; it++) {
+          if (it + 1 < iters) load_q4_row<T>(nxt, We + prow(it + 1) * rowbytes, nsb, j, sbl);
           float acc[kKqPairs];
 #pragma unroll
           for (int p = 0; p < kKqPairs; p++) acc[p] = 0.0f;
@@ -155,61 +254,75 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
                 const int4* yp = (const int4*)(acodes + p * k + sb * 256 + 64 * j);
                 int y[16];
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                  const int4 v = yp[q];
-                  y[4 * q] = v.x; y[4 * q + 1] = v.y; y[4 * q + 2] = v.z; y[4 * q + 3] = v.w;
+                for (int qq = 0; qq < 4; qq++) {
+                  const int4 v = yp[qq];
+                  y[4 * qq] = v.x; y[4 * qq + 1] = v.y; y[4 * qq + 2] = v.z; y[4 * qq + 3] = v.w;
                 }
                 // sub-blocks 2j, 2j+1 = groups 4j .. 4j+3
                 const uint2 g = *(const uint2*)(asums + (p * nsb + sb) * 16 + 4 * j);
                 const int32_t p0 = (int32_t)(int16_t)(g.x & 0xFFFF) + (int32_t)(int16_t)(g.x >> 16);
                 const int32_t p1 = (int32_t)(int16_t)(g.y & 0xFFFF) + (int32_t)(int16_t)(g.y >> 16);
-                acc[p] = q4k_unit(cur.h[t], cur.qa[t], cur.qb[t], y, ad[p * nsb + sb], p0, p1, j, acc[p]);
+                acc[p] = q4k_unit(q4cur.h[t], q4cur.qa[t], q4cur.qb[t], y, ad[p * nsb + sb], p0, p1, j, acc[p]);
               }
             }
           }
+          store(it, acc);
+          q4cur = nxt;
+        }
+      } else if constexpr (P > 1) {
+        // packs of P rows, one span each, the next pack's loads in flight
+        uint8_t* const slot = buf + q * Q6Pack<P>::kSlot;
+        Q6Pack<P> nxt;
+        for (int it = 0; it < iters; it++) {
+          wave_lds_sync();
 #pragma unroll
-          for (int p = 0; p < kKqPairs; p++) {
-            if (!use[p]) continue;
-            const float v = wave_sum_dpp(acc[p]);
-            if (lane == 0) dst[out_row[p] * ldd + r0 + i] = __fmul_rn(v, scale[p]);
+          for (int c = 0; c < 4; c++) *(uint4*)(slot + 16 * (pl + G * c)) = q6cur.p[c];
+          wave_lds_sync();
+          const int off = q6cur.off;
+          if (it + 1 < iters) load_q6_pack<P>(nxt, We + prow(it + 1) * rowbytes, nsb, pl);
+          float acc[kKqPairs];
+#pragma unroll
+          for (int p = 0; p < kKqPairs; p++) acc[p] = 0.0f;
+          if (sbl < nsb) {
+            Q6Lane u;
+            load_q6_lane(slot, off + 210 * sbl, h, l0, u);
+            const int sb = sbl;
+#pragma unroll
+            for (int p = 0; p < kKqPairs; p++) {
+              if (!use[p]) continue;
+              const int8_t* yrow = acodes + p * k + sb * 256 + 128 * h + l0;
+              int yv[4][4], bs[4];
+#pragma unroll
+              for (int t = 0; t < 4; t++) {
+                const int4 qv = *(const int4*)(yrow + 32 * t);
+                yv[t][0] = qv.x; yv[t][1] = qv.y; yv[t][2] = qv.z; yv[t][3] = qv.w;
+                bs[t] = asums[(p * nsb + sb) * 16 + 8 * h + 2 * t + (l0 >> 4)];
+              }
+              acc[p] = q6k_unit(u.qlA, u.qlB, u.qh, u.sc, u.dx, yv, ad[p * nsb + sb], bs, acc[p]);
+            }
           }
-          cur = nxt;
+          store(it, acc);
+          q6cur = nxt;
         }
       } else {
         // spans of 16 super-blocks in order, the next span's loads in flight;
         // past the wave's last span the loads read the (cached) first bytes
         // of the quantized activation, never used
         const int S = nrows * nspan;
-        int lr = 0, lsp = 0;  // the span loaded next: span lsp of row r0 + lr
-        auto load_next = [&](Q6Span& spn) {
-          if (lr < nrows) {
-            const int s0 = lsp * kQ6SpanSb;
-            load_q6_span(spn, We + (r0 + lr) * rowbytes + (int64_t)s0 * 210, nsb - s0 < kQ6SpanSb ? nsb - s0 : kQ6SpanSb,
-                         lane);
-          } else {
-            load_q6_span(spn, (const uint8_t*)yq, 1, lane);
-          }
-          if (++lsp == nspan) {
-            lsp = 0;
-            lr++;
-          }
-        };
-        Q6Span cur;
-        load_next(cur);
         float tot[kKqPairs];
 #pragma unroll
         for (int p = 0; p < kKqPairs; p++) tot[p] = 0.0f;
         int row = 0, sp = 0;
-        for (int s = 0; s < S; s++) {
+        for (int sidx = 0; sidx < S; sidx++) {
           wave_lds_sync();
 #pragma unroll
           for (int c = 0; c < kQ6PiecesPerLane; c++) {
             const int pc = lane + 64 * c;
-            *(uint4*)(buf + 16 * (pc < kQ6SpanPieces ? pc : kQ6SpanPieces - 1)) = cur.p[c];
+            *(uint4*)(buf + 16 * (pc < kQ6SpanPieces ? pc : kQ6SpanPieces - 1)) = q6s.p[c];
           }
           wave_lds_sync();
-          const int off = cur.off, slen = cur.len;
-          load_next(cur);
+          const int off = q6s.off, slen = q6s.len;
+          load_next(q6s);
           float acc[kKqPairs];
 #pragma unroll
           for (int p = 0; p < kKqPairs; p++) acc[p] = 0.0f;
@@ -224,8 +337,8 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
               int yv[4][4], bs[4];
 #pragma unroll
               for (int t = 0; t < 4; t++) {
-                const int4 q = *(const int4*)(yrow + 32 * t);
-                yv[t][0] = q.x; yv[t][1] = q.y; yv[t][2] = q.z; yv[t][3] = q.w;
+                const int4 qv = *(const int4*)(yrow + 32 * t);
+                yv[t][0] = qv.x; yv[t][1] = qv.y; yv[t][2] = qv.z; yv[t][3] = qv.w;
                 bs[t] = asums[(p * nsb + sb) * 16 + 8 * h + 2 * t + (l0 >> 4)];
               }
               acc[p] = q6k_unit(u.qlA, u.qlB, u.qh, u.sc, u.dx, yv, ad[p * nsb + sb], bs, acc[p]);
@@ -251,7 +364,7 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
   }
 }
 
-template <int TYPE, int T>
+template <int TYPE, int T, int P>
 hipError_t launch_kq(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p, const int32_t* runs,
                      const int32_t* ids, const float* topk_w, int topk, int64_t size_m, float* dst, int64_t ldd,
                      int cus, hipStream_t st) {
@@ -263,14 +376,14 @@ hipError_t launch_kq(const void* w, int num_experts, int64_t n, int64_t k, const
   int64_t pairs = (int64_t)((kKqLdsBudget - kq_stage_bytes<TYPE>()) / kq_pair_bytes(nsb));
   if (pairs > kKqPairs) pairs = kKqPairs;
   if (pairs < 1) pairs = 1;
-  // rows a wave: one while the runs' rows fill 32 waves a CU, more beyond
-  int64_t rpw = (n * gy + (int64_t)cus * 32 - 1) / ((int64_t)cus * 32);
-  if (rpw < 1) rpw = 1;
+  // rows a wave: P while the runs' row packs fill 32 waves a CU, more beyond
+  int64_t rpw = (n * gy + (int64_t)cus * 32 * P - 1) / ((int64_t)cus * 32 * P) * P;
+  if (rpw < P) rpw = P;
   if (rpw > 64) rpw = 64;
   const int64_t rows_per_wg = (int64_t)kKqWaves * rpw;
   const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
   const size_t lds = kq_act_bytes(nsb, (int)pairs) + kq_stage_bytes<TYPE>();
-  auto* kfn = &moe_kq_kernel<TYPE, T>;
+  auto* kfn = &moe_kq_kernel<TYPE, T, P>;
   if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
   kfn<<<grid, 64 * kKqWaves, lds, st>>>((const uint8_t*)w, n, nsb, estride, num_experts, p.codes, p.d,
                                         (const int16_t*)p.sums, runs, ids, topk_w, topk, (int)size_m, dst, ldd,
@@ -291,12 +404,18 @@ hipError_t launch_moe_kq(int type, const void* w, int num_experts, int64_t n, in
                          const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                          float* dst, int64_t ldd, int cus, hipStream_t st) {
   if (!moe_kq_supported(type, k)) return hipErrorInvalidValue;
-  if (type == T_Q6_K)
-    return launch_kq<T_Q6_K, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-  const int T = (int)((k / 256 + 15) / 16);
-  if (T <= 1) return launch_kq<T_Q4_K, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-  if (T <= 2) return launch_kq<T_Q4_K, 2>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-  return launch_kq<T_Q4_K, 4>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+  const int64_t nsb = k / 256;
+  if (type == T_Q6_K) {
+    if (nsb <= 4) return launch_kq<T_Q6_K, 1, 4>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+    if (nsb <= 8) return launch_kq<T_Q6_K, 1, 2>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+    return launch_kq<T_Q6_K, 1, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+  }
+  if (nsb <= 4) return launch_kq<T_Q4_K, 1, 4>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+  if (nsb <= 8) return launch_kq<T_Q4_K, 1, 2>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+  const int64_t T = (nsb + 15) / 16;
+  if (T <= 1) return launch_kq<T_Q4_K, 1, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+  if (T <= 2) return launch_kq<T_Q4_K, 2, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+  return launch_kq<T_Q4_K, 4, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
 }
 
 }  // namespace qmm

@@ -127,15 +127,21 @@ __device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) { r
 // Sum over the 64 lanes: DPP within rows of 16, then the four row sums, in a
 // fixed order (every decode kernel of a format reduces with this one, so a
 // row's result does not depend on which kernel or batch width computed it).
-__device__ __forceinline__ float wave_sum_dpp(float v) {
+// The sums of the four 16-lane rows of the wave (DPP within each row).
+__device__ __forceinline__ void wave_row16_sums(float v, float& a, float& b, float& c, float& d) {
   v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));   // quad 1,0,3,2
   v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));   // quad 2,3,0,1
   v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));  // half mirror
   v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // mirror
-  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  float a, b, c, d;
+  wave_row16_sums(v, a, b, c, d);
   return __fadd_rn(__fadd_rn(a, b), __fadd_rn(c, d));
 }
 

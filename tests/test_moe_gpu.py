@@ -287,3 +287,21 @@ def test_moe_kquant_long_rows(name, k):
     check_against_forward(stack, xs, got, sorted_ids, expert_ids, tw, topk)
     sel = [0, 6, 8]
     check_against_oracle(qtype, stack, x, got, sorted_ids[sel], expert_ids[sel], tw, topk)
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("k", [256, 768, 1280, 2048])
+def test_moe_kquant_short_rows_packed(name, k):
+    """Rows of at most 8 super-blocks run 2 or 4 rows a wave; an expert of
+    37 rows leaves a partial pack. Each pair still equals its own
+    qmm_forward bit for bit, and the oracle."""
+    qtype = MOE_TYPES[name]
+    E, n, tokens, topk = 5, 37, 7, 3
+    sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, k + 5)
+    stack = expert_stack(qtype, E, n, k, k + 7)
+    x = np.random.default_rng(k).standard_normal((tokens * topk, k)).astype(np.float32)
+    xs = t32(x)
+    got = moe_into(stack, xs, k, sorted_ids, expert_ids, topk_w, topk, tokens * topk)
+    assert not np.isnan(got).any()
+    check_against_forward(stack, xs, got, sorted_ids, expert_ids, topk_w, topk)
+    check_against_oracle(qtype, stack, x, got, sorted_ids, expert_ids, topk_w, topk)
