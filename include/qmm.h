@@ -233,6 +233,37 @@ int qmm_moe_forward(int type, const void *w, int num_experts, const float *x, in
                     float *dst, int64_t ldd, void *workspace, size_t workspace_bytes, size_t *need, int64_t k,
                     int64_t n, int64_t size_m, int launch, int64_t stream);
 
+/* Input types of qmm_moe_forward_prefill: the reference's input_dtype (0 f16,
+ * 1 bf16), and f32, which the product rounds to f16 as the reference's caller
+ * does before its launch (src/inference/layers/moe_card.rs:113-121). */
+enum qmm_x_dtype { QMM_X_F16 = 0, QMM_X_BF16 = 1, QMM_X_F32 = 2 };
+
+/* Grouped expert products of a prompt on the f16 / bf16 matrix cores. The
+ * routing, `w`, scale_p, in_p and the output rows are qmm_moe_forward's; x
+ * holds the input rows (x_stride values apart) as f16, bf16 or f32
+ * (x_dtype). It writes
+ *   dst[p][j] = scale_p * sum_i r(x[in_p][i]) * r(W_e[j][i])
+ * with r the rounding to f16 (f16 or f32 input) or bf16 (bf16 input), to
+ * nearest even, of each input value and of each weight value dequantized in
+ * f32 as qmm_dequantize does; the products are summed in f32 in an order of
+ * the kernel's (the reference's tensor-core sum: not the bits of
+ * qmm_moe_forward, whose activation is quantized). Types: Q8_0, IQ4_NL, MXFP4
+ * (k a multiple of 32) and Q4_K, Q6_K (k a multiple of 256). Entries whose
+ * expert or pair is out of range write nothing; entries in any order give the
+ * same result, consecutive entries of one expert (up to 32 a workgroup) read
+ * its weights together. Plan (launch == 0) and launch as qmm_forward: the
+ * workspace holds the routing's run and chunk tables and a 16-bit copy of the
+ * input rows (used for f32 input, or 16-bit input whose rows are not 16-byte
+ * aligned). Two launches. Replaces moe_gemm_gguf_prefill
+ * (candle-kernels/src/moe/moe_wmma_gguf.cu:450-535, kernel :191-371, which
+ * allocates its own tables and reads expert_ids to size them), as
+ * src/inference/layers/moe_card.rs:48-170 calls it for a prompt of more than
+ * 8 tokens (src/inference/layers/mod.rs:2753). */
+int qmm_moe_forward_prefill(int type, const void *w, int num_experts, const void *x, int x_dtype, int64_t x_stride,
+                            const int32_t *sorted_ids, const int32_t *expert_ids, const float *topk_w, int topk,
+                            float *dst, int64_t ldd, void *workspace, size_t workspace_bytes, size_t *need,
+                            int64_t k, int64_t n, int64_t size_m, int launch, int64_t stream);
+
 /* ---- GGUF files into device memory --------------------------------------
  * A parsed GGUF file: candle's gguf_file::Content::read
  * (quantized/gguf_file.rs:415-487): header (magic "GGUF", versions 1-3),
@@ -332,10 +363,13 @@ int qmm_fill_normal(float *out, int64_t n, uint64_t seed, float mean, float std,
 
 /* Kernel launches enqueued by this library since the process started
  * (the evidence of which kernel ran, like mmq_mma_products,
- * quantized/cuda.rs:937-945): matvec launches, GEMM launches. */
+ * quantized/cuda.rs:937-945): matvec launches, GEMM launches, grouped
+ * expert products (qmm_moe_forward) and prompt grouped products
+ * (qmm_moe_forward_prefill). */
 uint64_t qmm_matvec_launches(void);
 uint64_t qmm_gemm_launches(void);
 uint64_t qmm_moe_launches(void);
+uint64_t qmm_moe_prefill_launches(void);
 
 /* The launcher of the last kernel this library enqueued, with its template
  * arguments (a static string, "" before any launch): which instantiation

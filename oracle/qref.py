@@ -184,3 +184,55 @@ def glu(activation: str, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     if g.size:
         getattr(lib(), fn)(_p(g), _p(u), _p(out), g.size)
     return out
+
+
+def round_f16(x: np.ndarray) -> np.ndarray:
+    """f32 values rounded to f16 (to nearest even, subnormals kept), back in
+    f32: T(v) with T = half in the reference's tensor-core MoE kernel
+    (moe_wmma_gguf.cu:60-165) and its caller's to_dtype(F16)."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """f32 values rounded to bf16 (to nearest even on the f32 bits), back in
+    f32: T(v) with T = nv_bfloat16 in the same kernel. NaN stays NaN."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    b = a.view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    out = r.view(np.float32).copy()
+    nan = np.isnan(a)
+    out[nan] = a[nan]
+    return out
+
+
+def moe_prefill(qtype: int, stack: np.ndarray, num_experts: int, n: int, k: int, x: np.ndarray, bf16: bool,
+                sorted_ids: np.ndarray, expert_ids: np.ndarray, topk_w, topk: int, size_m: int = -1) -> np.ndarray:
+    """moe_gemm_gguf_prefill (candle-kernels/src/moe/moe_wmma_gguf.cu:191-371):
+    entry i (pair p = sorted_ids[i], expert e = expert_ids[i], both in range)
+    gives row p = scale_p * sum_j T(x[in_p][j]) T(w_e[.][j]) with T the
+    rounding to f16 (bf16 when `bf16`) of the input value and of the weight's
+    to_float value (:60-165, dequantize_block_warp), scale_p = topk_w[p] or 1
+    (:356-367), in_p = p with topk_w else p // topk (:267). Summed here in
+    f64 (the kernel's f32 tensor-core sum differs from it by rounding only).
+    Rows no entry writes are NaN. size_m: the routing's entry count (pairs
+    at or past it are out of range); -1 for len(sorted_ids), less to check a
+    sample of a routing's entries."""
+    rnd = round_bf16 if bf16 else round_f16
+    size_m = len(sorted_ids) if size_m < 0 else size_m
+    per = nbytes(qtype, n * k)
+    out = np.full((size_m, n), np.nan, dtype=np.float32)
+    wcache = {}
+    for i in range(len(sorted_ids)):
+        p, e = int(sorted_ids[i]), int(expert_ids[i])
+        if not (0 <= p < size_m and 0 <= e < num_experts):
+            continue
+        if e not in wcache:
+            w = to_float(qtype, stack[e * per:(e + 1) * per], n * k).reshape(n, k)
+            wcache[e] = rnd(w).astype(np.float64)
+        row = p if topk_w is not None else p // topk
+        xr = rnd(np.asarray(x[row], dtype=np.float32)).astype(np.float64)
+        y = wcache[e] @ xr
+        scale = np.float64(np.float32(topk_w[p])) if topk_w is not None else 1.0
+        out[p] = (y * scale).astype(np.float32)
+    return out

@@ -3,8 +3,10 @@ over GGUF Q8_0, Q4_K, Q6_K, IQ4_NL, MXFP4) as hand-written HIP kernels for
 AMD Instinct MI355X (gfx950), behind the C ABI of include/qmm.h."""
 
 from ._lib import QmmError, lib  # noqa: F401
-from .qtensor import (GgmlDType, QMatMul, QTensor, fill_normal, forward_glu, glu, mmq_few_rows_line,  # noqa: F401
-                      moe_forward, set_force_dmmv)
+from .qtensor import (MOE_CARD_ONE_ROW_MAX_TOKENS, GgmlDType, QMatMul, QTensor, fill_normal,  # noqa: F401
+                      forward_glu, glu, mmq_few_rows_line, moe_forward, moe_prompt_on_tensor_cores,
+                      moe_uses_prompt_kernel, set_force_dmmv)
 
-__all__ = ["GgmlDType", "QMatMul", "QTensor", "QmmError", "fill_normal", "forward_glu", "glu", "lib",
-           "mmq_few_rows_line", "moe_forward", "set_force_dmmv"]
+__all__ = ["MOE_CARD_ONE_ROW_MAX_TOKENS", "GgmlDType", "QMatMul", "QTensor", "QmmError", "fill_normal", "forward_glu",
+           "glu", "lib", "mmq_few_rows_line", "moe_forward", "moe_prompt_on_tensor_cores", "moe_uses_prompt_kernel",
+           "set_force_dmmv"]

@@ -16,6 +16,7 @@ QMM_OK, QMM_UNSUPPORTED, QMM_WORKSPACE_TOO_SMALL, QMM_DEVICE_ERROR, QMM_NO_TILE,
 STATUS_NAMES = {0: "OK", 1: "UNSUPPORTED", 2: "WORKSPACE_TOO_SMALL", 3: "DEVICE_ERROR", 4: "NO_TILE", 5: "NO_ROOM"}
 ACT_Q8K, ACT_Q8_0 = 0, 1
 GLU_SILU, GLU_SWIGLU_OAI, GLU_GELU = 0, 1, 2
+X_F16, X_BF16, X_F32 = 0, 1, 2
 
 
 class QmmError(RuntimeError):
@@ -46,6 +47,8 @@ SIGNATURES = {
                                 ctypes.POINTER(_I64), _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64, _I64, _I, _I64]),
     "qmm_moe_forward": (_I, [_I, _P, _I, _P, _I64, _P, _P, _P, _I, _P, _I64, _P, _SZ, ctypes.POINTER(_SZ), _I64,
                              _I64, _I64, _I, _I64]),
+    "qmm_moe_forward_prefill": (_I, [_I, _P, _I, _P, _I, _I64, _P, _P, _P, _I, _P, _I64, _P, _SZ,
+                                     ctypes.POINTER(_SZ), _I64, _I64, _I64, _I, _I64]),
     "qmm_dequantize": (_I, [_I, _P, _P, _I, _I64, _I64]),
     "qmm_quantize_scratch_bytes": (_SZ, [_I, _I64]),
     "qmm_quantize_weights": (_I, [_I, _P, _P, _I64, _P, _SZ, _I64]),
@@ -56,6 +59,7 @@ SIGNATURES = {
     "qmm_matvec_launches": (_U64, []),
     "qmm_gemm_launches": (_U64, []),
     "qmm_moe_launches": (_U64, []),
+    "qmm_moe_prefill_launches": (_U64, []),
     "qmm_last_kernel": (ctypes.c_char_p, []),
     "qmm_forward_noalloc": (_I, [_I, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64]),
     "qmm_forward_noalloc_max_bytes": (_SZ, []),

@@ -56,4 +56,51 @@ __device__ __forceinline__ void moe_runs_block(const int32_t* __restrict__ exper
   if (t == 0) runs[0] = base;
 }
 
+// The chunk table of a run table written by this workgroup: run r cut into
+// ceil(len / ch) chunks of up to ch consecutive entries, in run order.
+//   chunks[0] = number of chunks; chunk c at chunks[1 + 3c]: first entry,
+//   length, expert.
+// At most size_m / ch + (number of runs) chunks.
+template <int NT>
+__device__ __forceinline__ void moe_chunks_block(const int32_t* __restrict__ runs, int ch,
+                                                 int32_t* __restrict__ chunks) {
+  constexpr int kW = NT / 64;
+  __shared__ int s_sum[kW];
+  const int t = (int)threadIdx.x, lane = t & 63, w = t >> 6;
+  __syncthreads();  // the run table is written
+  const int nruns = runs[0];
+  int base = 0;  // chunks of the runs before this block of runs
+  for (int r0 = 0; r0 < nruns; r0 += NT) {
+    const int r = r0 + t;
+    const int len = r < nruns ? runs[2 + 3 * r] : 0;
+    const int nc = (len + ch - 1) / ch;
+    int v = nc;  // inclusive sum over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int u = __shfl_up(v, d);
+      if (lane >= d) v += u;
+    }
+    if (lane == 63) s_sum[w] = v;
+    __syncthreads();
+    int before = base, total = base;
+#pragma unroll
+    for (int j = 0; j < kW; j++) {
+      const int c = s_sum[j];
+      before += j < w ? c : 0;
+      total += c;
+    }
+    if (r < nruns) {
+      const int first = before + v - nc, s = runs[1 + 3 * r], e = runs[3 + 3 * r];
+      for (int c = 0; c < nc; c++) {
+        chunks[1 + 3 * (first + c)] = s + c * ch;
+        chunks[2 + 3 * (first + c)] = len - c * ch < ch ? len - c * ch : ch;
+        chunks[3 + 3 * (first + c)] = e;
+      }
+    }
+    base = total;
+    __syncthreads();  // s_sum is rewritten by the next block of runs
+  }
+  if (t == 0) chunks[0] = base;
+}
+
 }  // namespace qmm

@@ -17,6 +17,7 @@ std::atomic<uint64_t> g_matvec_launches{0};
 std::atomic<uint64_t> g_gemm_launches{0};
 std::atomic<bool> g_fail_next{false};
 std::atomic<uint64_t> g_moe_launches{0};
+std::atomic<uint64_t> g_moe_prefill_launches{0};
 // set_force_dmmv (quantized/cuda.rs:29-33): products of qmm_forward and its
 // shared / GLU forms dequantize the weight against the f32 activation.
 std::atomic<bool> g_force_dmmv{false};
@@ -620,6 +621,51 @@ int qmm_moe_forward(int type, const void* w, int num_experts, const float* x, in
 }
 
 uint64_t qmm_moe_launches(void) { return g_moe_launches.load(std::memory_order_relaxed); }
+
+int qmm_moe_forward_prefill(int type, const void* w, int num_experts, const void* x, int x_dtype, int64_t x_stride,
+                            const int32_t* sorted_ids, const int32_t* expert_ids, const float* topk_w, int topk,
+                            float* dst, int64_t ldd, void* workspace, size_t workspace_bytes, size_t* need, int64_t k,
+                            int64_t n, int64_t size_m, int launch, int64_t stream) {
+  if (!qmm::moe_pf_supported(type, k) || !shape_ok(type, k, n, size_m) || need == nullptr || ldd < n ||
+      x_stride < k || num_experts < 1 || topk < 1 || (topk_w == nullptr && size_m % topk != 0) ||
+      size_m > ((int64_t)1 << 30) || x_dtype < QMM_X_F16 || x_dtype > QMM_X_F32)
+    return QMM_UNSUPPORTED;
+  const int64_t in_rows = topk_w ? size_m : size_m / topk;
+  // 32-bit byte offsets inside the kernel: an expert's weights, the 16-bit rows
+  if (n * qmm::moe_pf_row_bytes(type, k) >= ((int64_t)1 << 31) || in_rows * k * 2 >= ((int64_t)1 << 31))
+    return QMM_UNSUPPORTED;
+  const size_t runs_b = qmm::align_up(qmm::moe_runs_bytes(size_m), 256);
+  const size_t chunks_b = qmm::align_up(qmm::moe_pf_chunks_bytes(size_m), 256);
+  const size_t xo_b = qmm::align_up((size_t)(in_rows * k * 2), 256);
+  *need = runs_b + chunks_b + xo_b;
+  if (!launch) return QMM_OK;
+  if (g_fail_next.exchange(false)) return QMM_NO_ROOM;
+  if (workspace_bytes < *need || workspace == nullptr) return QMM_WORKSPACE_TOO_SMALL;
+  if (!w || !x || !dst || !sorted_ids || !expert_ids) return QMM_UNSUPPORTED;
+  const hipStream_t st = (hipStream_t)stream;
+  clear_stale_error();
+  int32_t* runs = (int32_t*)workspace;
+  int32_t* chunks = (int32_t*)((char*)workspace + runs_b);
+  uint16_t* xo = (uint16_t*)((char*)workspace + runs_b + chunks_b);
+  // A 16-bit input with 16-byte aligned rows is read in place; an f32 input
+  // is rounded to f16 (the reference's caller converts a prompt's input to
+  // f16, moe_card.rs:113-121) and any other is copied aligned, in the
+  // prologue that writes the routing tables.
+  const bool direct = x_dtype != QMM_X_F32 && ((uintptr_t)x & 15) == 0 && x_stride % 8 == 0 &&
+                      in_rows * x_stride * 2 < ((int64_t)1 << 31);
+  const int kind = direct ? -1 : x_dtype == QMM_X_F32 ? 2 : x_dtype;
+  if (qmm::launch_moe_pf_prep(expert_ids, size_m, runs, chunks, x, kind, x_stride, k, in_rows, xo, (int)cu_count(),
+                              st) != hipSuccess)
+    return QMM_DEVICE_ERROR;
+  const hipError_t e = qmm::launch_moe_pf(type, x_dtype == QMM_X_BF16, w, num_experts, n, k,
+                                          direct ? (const uint16_t*)x : xo, direct ? x_stride : k, chunks, sorted_ids,
+                                          topk_w, topk, size_m, dst, ldd, st);
+  if (e != hipSuccess) return QMM_DEVICE_ERROR;
+  g_moe_prefill_launches.fetch_add(1, std::memory_order_relaxed);
+  return QMM_OK;
+}
+
+uint64_t qmm_moe_prefill_launches(void) { return g_moe_prefill_launches.load(std::memory_order_relaxed); }
 
 size_t qmm_wire_bytes(int64_t n) {
   const int64_t b = qmm::wire_bytes(n);

@@ -128,6 +128,22 @@ hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64
                       const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                       float* dst, int64_t ldd, int cus, hipStream_t st);
 
+// Grouped expert products of prompt-size routings on the f16 / bf16 matrix
+// cores (moe_pf.hip): the types and row lengths covered, a weight row's
+// bytes, bytes of the chunk table, the prologue (run and chunk tables from
+// expert_ids; the input rows into 16-bit values at xo when x_kind >= 0: 0 f16
+// or 1 bf16 copied, 2 f32 to f16, 3 f32 to bf16) and the grouped kernel over
+// 16-bit input rows (16-byte aligned, x_stride a multiple of 8).
+bool moe_pf_supported(int type, int64_t k);
+int64_t moe_pf_row_bytes(int type, int64_t k);
+size_t moe_pf_chunks_bytes(int64_t size_m);
+hipError_t launch_moe_pf_prep(const int32_t* expert_ids, int64_t size_m, int32_t* runs, int32_t* chunks,
+                              const void* x, int x_kind, int64_t x_stride, int64_t k, int64_t rows, uint16_t* xo,
+                              int cus, hipStream_t st);
+hipError_t launch_moe_pf(int type, bool bf16, const void* w, int num_experts, int64_t n, int64_t k, const uint16_t* x,
+                         int64_t x_stride, const int32_t* chunks, const int32_t* ids, const float* topk_w, int topk,
+                         int64_t size_m, float* dst, int64_t ldd, hipStream_t st);
+
 // Q4_K products of a few rows (gemm_q4k_skinny.hip): up to
 // gemm_q4k_skinny_max_rows() activation rows, targets as the stream kernels.
 int gemm_q4k_skinny_max_rows();

@@ -14,13 +14,14 @@ from __future__ import annotations
 
 import ctypes
 import enum
+import os
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
 import torch
 
 from . import _lib
-from ._lib import check, lib
+from ._lib import X_BF16, X_F16, X_F32, check, lib
 
 
 class GgmlDType(enum.IntEnum):
@@ -344,20 +345,54 @@ def glu(gate: torch.Tensor, up: torch.Tensor, activation: str = "silu") -> torch
     return out
 
 
+# Tokens up to which a card's grouped expert products run one row per pair
+# (qmm_moe_forward); above it a prompt's run on the matrix cores
+# (qmm_moe_forward_prefill): MOE_CARD_ONE_ROW_MAX_TOKENS and the caller's
+# choice in MoeFfn::stacked_products (src/inference/layers/mod.rs:475, 2753).
+MOE_CARD_ONE_ROW_MAX_TOKENS = 8
+
+_X_DTYPES = {torch.float16: X_F16, torch.bfloat16: X_BF16, torch.float32: X_F32}
+
+
+def moe_prompt_on_tensor_cores() -> bool:
+    """prompt_on_tensor_cores (src/inference/layers/mod.rs:1232-1235): the
+    prompt kernel unless SWARMLLM_MOE_CARD_PROMPT=rows, read once."""
+    global _PROMPT_ON
+    if _PROMPT_ON is None:
+        _PROMPT_ON = os.environ.get("SWARMLLM_MOE_CARD_PROMPT") != "rows"
+    return _PROMPT_ON
+
+
+_PROMPT_ON: Optional[bool] = None
+
+
+def moe_uses_prompt_kernel(tokens: int) -> bool:
+    """The caller's choice of kernel for a chunk of `tokens` tokens
+    (src/inference/layers/mod.rs:2753)."""
+    return tokens > MOE_CARD_ONE_ROW_MAX_TOKENS and moe_prompt_on_tensor_cores()
+
+
 def moe_forward(xs: torch.Tensor, experts: QTensor, sorted_ids: torch.Tensor, expert_ids: torch.Tensor,
-                topk_weights: Optional[torch.Tensor], topk: int, workspace: Optional[Workspace] = None) -> torch.Tensor:
-    """The grouped expert products of moe_gemm_gguf (candle-kernels/src/moe/
-    moe_gguf.cu:149-252, as layers::moe_card calls it, moe_card.rs:48-170):
-    experts [E, n, k] in GGUF blocks; routing entry i pairs sorted_ids[i]
-    (token * topk + k-th choice) with expert_ids[i]; xs holds one row per
-    pair when topk_weights is given (each output row then scaled by its
-    pair's weight), else one row per token. Returns [len(sorted_ids), n]
-    f32, row p the product of pair p (qmm_moe_forward)."""
+                topk_weights: Optional[torch.Tensor], topk: int, prompt: bool = False,
+                workspace: Optional[Workspace] = None) -> torch.Tensor:
+    """The grouped expert products of moe_gemm_gguf / moe_gemm_gguf_prefill as
+    layers::moe_card calls them (moe_card.rs:48-170; candle-kernels/src/moe/
+    moe_gguf.cu:149-252, moe_wmma_gguf.cu:450-535): experts [E, n, k] in
+    GGUF blocks; routing entry i pairs sorted_ids[i] (token * topk + k-th
+    choice) with expert_ids[i]; xs holds one row per pair when topk_weights is
+    given (each output row then scaled by its pair's weight), else one row per
+    token. Returns [len(sorted_ids), n] f32, row p the product of pair p.
+    prompt=False: one row per pair with the activation quantized
+    (qmm_moe_forward; xs f32). prompt=True: the matrix-core product of the
+    f16-rounded (bf16 for a bf16 xs) input and weights (qmm_moe_forward_prefill;
+    xs f32, f16 or bf16)."""
     if len(experts.shape) != 3:
         raise ValueError(f"moe_forward: expert weights [E, n, k], not {experts.shape}")
     e, n, k = experts.shape
-    if xs.dtype != torch.float32 or xs.dim() != 2 or xs.shape[1] != k or not xs.is_contiguous():
-        raise ValueError(f"moe_forward: input [rows, {k}] contiguous f32, not {tuple(xs.shape)} {xs.dtype}")
+    ok_dtype = xs.dtype in _X_DTYPES if prompt else xs.dtype == torch.float32
+    if not ok_dtype or xs.dim() != 2 or xs.shape[1] != k or not xs.is_contiguous():
+        raise ValueError(f"moe_forward: input [rows, {k}] contiguous {'f32/f16/bf16' if prompt else 'f32'}, "
+                         f"not {tuple(xs.shape)} {xs.dtype}")
     size_m = int(sorted_ids.numel())
     for name, t in (("sorted_ids", sorted_ids), ("expert_ids", expert_ids)):
         if t.dtype != torch.int32 or t.numel() != size_m or not t.is_contiguous():
@@ -374,11 +409,17 @@ def moe_forward(xs: torch.Tensor, experts: QTensor, sorted_ids: torch.Tensor, ex
     st = _stream()
     tw = _ptr(topk_weights) if topk_weights is not None else None
     need = ctypes.c_size_t(0)
-    args = (int(experts.dtype), _ptr(experts.data_), e, _ptr(xs), k, _ptr(sorted_ids), _ptr(expert_ids), tw, topk,
-            _ptr(out), n)
-    check("qmm_moe_forward", L.qmm_moe_forward(*args, None, 0, ctypes.byref(need), k, n, size_m, 0, st))
+    if prompt:
+        fn, call = "qmm_moe_forward_prefill", L.qmm_moe_forward_prefill
+        args = (int(experts.dtype), _ptr(experts.data_), e, _ptr(xs), _X_DTYPES[xs.dtype], k, _ptr(sorted_ids),
+                _ptr(expert_ids), tw, topk, _ptr(out), n)
+    else:
+        fn, call = "qmm_moe_forward", L.qmm_moe_forward
+        args = (int(experts.dtype), _ptr(experts.data_), e, _ptr(xs), k, _ptr(sorted_ids), _ptr(expert_ids), tw,
+                topk, _ptr(out), n)
+    check(fn, call(*args, None, 0, ctypes.byref(need), k, n, size_m, 0, st))
     buf = (workspace or Workspace()).get(need.value, xs.device)
-    check("qmm_moe_forward", L.qmm_moe_forward(*args, _ptr(buf), buf.numel(), ctypes.byref(need), k, n, size_m, 1, st))
+    check(fn, call(*args, _ptr(buf), buf.numel(), ctypes.byref(need), k, n, size_m, 1, st))
     return out
 
 
