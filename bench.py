@@ -667,9 +667,107 @@ def moe_kquant(stream, reps: int = 10, copies: int = 2) -> dict:
                     "tops": round(ops / (us * 1e-6) / 1e12, 2)}
         log(f"K-quant MoE, {tokens} token(s): {us:.2f} us per step ({touched} experts touched), "
             f"{out[key]['gbs']:.0f} GB/s, {out[key]['tops']:.1f} TOP/s")
+        if tokens > 8:
+            out["prompt_mfma"] = moe_prompt_step(stream, Q4K, Q6K, gu, dn, E, hidden, inter, topk, tokens, sids, eids,
+                                                 topk_w, x1, x2, touched, reps)
     out["workload"] = ("grouped K-quant experts: 128 experts, hidden 2048, expert width 768, gate_up Q4_K "
-                       "[1536, 2048] + down Q6_K [2048, 768], top-8, at 1 token and 512 tokens")
+                       "[1536, 2048] + down Q6_K [2048, 768], top-8, at 1 token and 512 tokens (prompt: the "
+                       "one-row-per-pair kernels, and prompt_mfma: the f16 matrix-core kernels of "
+                       "qmm_moe_forward_prefill)")
     return out
+
+
+def moe_prompt_step(stream, qg, qd, gu, dn, E, hidden, inter, topk, tokens, sids, eids, topk_w, x1, x2, touched,
+                    reps) -> dict:
+    """One MoE step of a prompt through qmm_moe_forward_prefill (the
+    reference's moe_gemm_gguf_prefill): the gate_up product (per-token f32
+    inputs, rounded to f16 in the launch's prologue) and the down product
+    (per-pair inputs, routing weights), over the weight stacks gu / dn in
+    turn. Reports us per step, the touched experts' weight bytes per second
+    and f16 matrix-core TFLOP/s (2 * entries * n * k per product)."""
+    import torch
+
+    from swarmllm_amd._lib import X_F32, check, lib
+
+    L = lib()
+    size_m = tokens * topk
+    y1 = torch.empty((size_m, 2 * inter), dtype=torch.float32, device="cuda")
+    y2 = torch.empty((size_m, hidden), dtype=torch.float32, device="cuda")
+    need = ctypes.c_size_t(0)
+    check("qmm_moe_forward_prefill", L.qmm_moe_forward_prefill(
+        qg, None, E, None, X_F32, hidden, None, None, None, topk, None, 2 * inter, None, 0, ctypes.byref(need), hidden,
+        2 * inter, size_m, 0, 0))
+    ws1 = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+    check("qmm_moe_forward_prefill", L.qmm_moe_forward_prefill(
+        qd, None, E, None, X_F32, inter, None, None, ctypes.c_void_p(16), topk, None, hidden, None, 0,
+        ctypes.byref(need), inter, hidden, size_m, 0, 0))
+    ws2 = torch.empty(need.value, dtype=torch.uint8, device="cuda")
+    before = L.qmm_moe_prefill_launches()
+
+    def fn(s):
+        for c in range(len(gu)):
+            check("qmm_moe_forward_prefill", L.qmm_moe_forward_prefill(
+                qg, gu[c].data_ptr(), E, x1.data_ptr(), X_F32, hidden, sids.data_ptr(), eids.data_ptr(), None, topk,
+                y1.data_ptr(), 2 * inter, ws1.data_ptr(), ws1.numel(), ctypes.byref(need), hidden, 2 * inter, size_m,
+                1, s))
+            check("qmm_moe_forward_prefill", L.qmm_moe_forward_prefill(
+                qd, dn[c].data_ptr(), E, x2.data_ptr(), X_F32, inter, sids.data_ptr(), eids.data_ptr(),
+                topk_w.data_ptr(), topk, y2.data_ptr(), hidden, ws2.data_ptr(), ws2.numel(), ctypes.byref(need), inter,
+                hidden, size_m, 1, s))
+
+    g = capture(fn, stream)
+    if L.qmm_moe_prefill_launches() < before + 2 * len(gu):
+        raise RuntimeError("the prompt MoE step did not run the matrix-core grouped kernels")
+    for _ in range(2):
+        g.replay()
+    ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+    us = ms * 1e3 / (reps * len(gu))
+    wbytes = touched * (gu[0].numel() + dn[0].numel()) // E
+    flops = 2.0 * size_m * (2 * inter * hidden + hidden * inter)
+    r = {"tokens": tokens, "entries": size_m, "experts_touched": touched, "us_per_step": round(us, 3),
+         "weight_bytes": wbytes, "weight_gbs": round(wbytes / (us * 1e-6) / 1e9, 1),
+         "tflops_f16": round(flops / (us * 1e-6) / 1e12, 2)}
+    log(f"prompt MoE (matrix cores), {tokens} tokens: {us:.2f} us per step, {r['weight_gbs']:.0f} GB/s of weights, "
+        f"{r['tflops_f16']:.1f} TFLOP/s")
+    return r
+
+
+def moe_prompt_gpt_oss(stream, reps: int = 10, copies: int = 2, tokens: int = 512) -> dict:
+    """BASELINE C4's experts (gpt-oss-20b: 32 MXFP4 experts, gate_up [5760,
+    2880], down [2880, 2880], top-4) at a 512-token prompt through
+    qmm_moe_forward_prefill."""
+    import numpy as np
+    import torch
+
+    from swarmllm_amd import GgmlDType, QTensor, fill_normal
+
+    E, topk, hidden, inter = 32, 4, 2880, 2880
+    rng = np.random.default_rng(8)
+    logits = rng.standard_normal((tokens, E)).astype(np.float32)
+    choice = np.argsort(-logits, axis=1, kind="stable")[:, :topk]
+    pairs = sorted((int(choice[t, j]), t * topk + j) for t in range(tokens) for j in range(topk))
+    eids = torch.tensor([e for e, _ in pairs], dtype=torch.int32, device="cuda")
+    sids = torch.tensor([p for _, p in pairs], dtype=torch.int32, device="cuda")
+    sel = np.take_along_axis(logits, choice, axis=1).astype(np.float64)
+    wts = np.exp(sel - sel.max(axis=1, keepdims=True))
+    wts /= wts.sum(axis=1, keepdims=True)
+    topk_w = torch.tensor(wts.reshape(-1), dtype=torch.float32, device="cuda")
+    touched = len(set(e for e, _ in pairs))
+
+    def stack(n, k, seed):
+        parts = [QTensor.quantize(fill_normal(n * k, seed=(seed << 8) | i, std=0.02).reshape(n, k), GgmlDType(MXFP4))
+                 for i in range(E)]
+        return torch.cat([p.data_ for p in parts])
+
+    gu = [stack(2 * inter, hidden, 80 + 2 * c) for c in range(copies)]
+    dn = [stack(hidden, inter, 81 + 2 * c) for c in range(copies)]
+    x1 = fill_normal(tokens * hidden, seed=(8 << 40) | 1).reshape(tokens, hidden)
+    x2 = fill_normal(tokens * topk * inter, seed=(8 << 40) | 2).reshape(tokens * topk, inter)
+    r = moe_prompt_step(stream, MXFP4, MXFP4, gu, dn, E, hidden, inter, topk, tokens, sids, eids, topk_w, x1, x2,
+                        touched, reps)
+    r["workload"] = ("gpt-oss-20b experts (BASELINE C4's weights: 32 MXFP4 experts, gate_up [5760, 2880], down "
+                     "[2880, 2880], top-4) at a 512-token prompt, qmm_moe_forward_prefill")
+    return r
 
 
 def c1_q8_0(stream, reps: int = 50, copies: int = 16) -> dict:
@@ -936,6 +1034,7 @@ def main() -> int:
         extra["c1"] = c1_q8_0(stream)
         extra["c4"] = c4_moe(stream)
         extra["moe_kquant"] = moe_kquant(stream)
+        extra["moe_prompt_gpt_oss"] = moe_prompt_gpt_oss(stream)
         extra["c5"] = c5_shard(stream)
         extra["prefill_b32"] = prefill_b32(stream)
 

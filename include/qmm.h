@@ -248,10 +248,10 @@ enum qmm_x_dtype { QMM_X_F16 = 0, QMM_X_BF16 = 1, QMM_X_F32 = 2 };
  * f32 as qmm_dequantize does; the products are summed in f32 in an order of
  * the kernel's (the reference's tensor-core sum: not the bits of
  * qmm_moe_forward, whose activation is quantized). Types: Q8_0, IQ4_NL, MXFP4
- * (k a multiple of 32) and Q4_K, Q6_K (k a multiple of 256). Entries whose
- * expert or pair is out of range write nothing; entries in any order give the
- * same result, consecutive entries of one expert (up to 32 a workgroup) read
- * its weights together. Plan (launch == 0) and launch as qmm_forward: the
+ * (k a multiple of 32) and Q4_K (k a multiple of 256, w 16-byte aligned),
+ * Q6_K (k a multiple of 256). Entries whose expert or pair is out of range
+ * write nothing; entries in any order give the same result, consecutive
+ * entries of one expert (up to 64 a workgroup) read its weights together. Plan (launch == 0) and launch as qmm_forward: the
  * workspace holds the routing's run and chunk tables and a 16-bit copy of the
  * input rows (used for f32 input, or 16-bit input whose rows are not 16-byte
  * aligned). Two launches. Replaces moe_gemm_gguf_prefill

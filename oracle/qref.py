@@ -232,7 +232,8 @@ def moe_prefill(qtype: int, stack: np.ndarray, num_experts: int, n: int, k: int,
             wcache[e] = rnd(w).astype(np.float64)
         row = p if topk_w is not None else p // topk
         xr = rnd(np.asarray(x[row], dtype=np.float32)).astype(np.float64)
-        y = wcache[e] @ xr
+        with np.errstate(invalid="ignore"):  # 0 * inf weights give NaN, as in the kernel
+            y = wcache[e] @ xr
         scale = np.float64(np.float32(topk_w[p])) if topk_w is not None else 1.0
         out[p] = (y * scale).astype(np.float32)
     return out

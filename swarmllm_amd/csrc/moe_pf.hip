@@ -14,19 +14,21 @@
 // writing nothing) is that of the grouped decode product (moe.hip).
 //
 // Shape of the work: the routing's runs (moe_runs.h) are cut into chunks of
-// up to 32 entries of one expert, in a table written by the one-workgroup
-// prologue launch (moe_pf_prep_kernel). A workgroup takes a chunk and a tile
-// of 32 x waves weight rows of the chunk's expert and walks k in stages of
-// 256 values. For each stage, direct global-to-LDS copies bring each weight
-// row's bytes of the stage (its 16-byte aligned window) and the chunk's 32
-// input rows (256 values each, 16-byte pieces XOR-swizzled by row) into one
-// half of double buffers while the waves work on the other half. Each wave
-// owns 32 weight rows: lane L dequantizes row L%32 into the B operand of
-// v_mfma_f32_32x32x16_{f16,bf16} (the chunk's entries are the A side), 16
-// steps a stage. The order in which a stage's 256 values enter the steps is
-// chosen per format so that a lane's 8 values of a step come from 8
-// consecutive bytes of its row; the A side reads the input values of the same
-// positions, and any order gives the same sum of products.
+// up to 64 entries of one expert, in a table written by the one-workgroup
+// prologue launch (moe_pf_prep_kernel). A workgroup of 4 waves takes a chunk
+// and a tile of 128 weight rows of the chunk's expert and walks k in stages of
+// 128 values. For each stage, direct global-to-LDS copies bring each weight
+// row's bytes of the stage (the 16-byte aligned windows of the byte ranges the
+// stage reads) and the chunk's input rows (128 values each, 16-byte pieces
+// XOR-swizzled by row) into one half of double buffers while the waves work on
+// the other half; two workgroups share a CU, one computing while the other
+// waits for its copies. Each wave owns 32 weight rows: lane L dequantizes row
+// L%32 into the B operand of v_mfma_f32_32x32x16_{f16,bf16}, which it applies
+// to the chunk's first and (past 32 entries) second 32 entries, 8 steps a
+// stage. The order in which a stage's 128 values enter the steps is chosen per
+// format so that a lane's 8 values of a step come from 8 consecutive bytes of
+// its row; the A side reads the input values of the same positions, and any
+// order gives the same sum of products.
 #include "b32_common.h"
 #include "lds_copy.h"
 #include "moe_runs.h"
@@ -44,28 +46,51 @@ typedef float pf_f2 __attribute__((ext_vector_type(2)));
 typedef float pf_f16 __attribute__((ext_vector_type(16)));
 typedef unsigned pf_u4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPfM = 32;                   // routing entries a chunk: the MFMA's M
-constexpr int kPfK = 256;                  // values a stage
-constexpr int kPfABytes = kPfM * kPfK * 2;  // the input tile of a stage (16-bit values)
+constexpr int kPfM = 64;                   // routing entries a chunk: two MFMA row tiles
+constexpr int kPfK = 128;                  // values a stage
+constexpr int kPfRowBytes = kPfK * 2;      // an input row's stage (16-bit values)
+constexpr int kPfABytes = kPfM * kPfRowBytes;
 constexpr int kPfACopies = kPfABytes / 1024;
+constexpr int kPfW = 4;                    // waves a workgroup
+constexpr int kPfNT = 32 * kPfW;           // weight rows a workgroup
 constexpr int kPfPrepThreads = 256;
 
-// Bytes of a weight row's stage (256 values), the 16-byte pieces of its window
-// (aligned: the stage starts on a 16-byte boundary), the LDS row stride in
-// pieces (odd, so that the 32 rows a wave reads in one instruction fall on
-// distinct banks), waves, and the weight buffer of a stage.
-template <int FMT, bool AL>
+// A weight row's stage: the byte ranges it reads (up to 3 regions, each an
+// offset from the stage's base and a length, with their change from the first
+// half of a super-block to the second: K-quant stages are half super-blocks),
+// the 16-byte pieces of each region's aligned window, and the LDS row stride
+// in pieces (odd, so the 32 rows a wave reads in one instruction fall on
+// distinct banks).
+//   Q4_K (16-byte aligned rows): d, dmin, scales (16 bytes); qs[64h .. +63].
+//   Q6_K: ql[64h .. +63]; qh[32h .. +31]; sc[8h ..] and d (bytes 192 + 8h to
+//         209).
+//   32-value formats: 4 blocks.
+template <int FMT>
 struct PfShape {
-  static constexpr int SB = FMT == T_Q4_K ? 144 : FMT == T_Q6_K ? 210 : FMT == T_Q8_0 ? 272 : FMT == T_IQ4_NL ? 144 : 136;
-  static constexpr int P = AL ? SB / 16 : (SB + 30) / 16;
+  static constexpr bool KQ = FMT == T_Q4_K || FMT == T_Q6_K;
+  static constexpr int BB = FMT == T_Q4_K ? 144 : FMT == T_Q6_K ? 210 : FMT == T_Q8_0 ? 34 : FMT == T_IQ4_NL ? 18 : 17;
+  static constexpr int NR = FMT == T_Q4_K ? 2 : FMT == T_Q6_K ? 3 : 1;
+  __host__ __device__ static constexpr int off0(int r) {
+    return FMT == T_Q4_K ? (r == 0 ? 0 : 16) : FMT == T_Q6_K ? (r == 0 ? 0 : r == 1 ? 128 : 192) : 0;
+  }
+  __host__ __device__ static constexpr int dlt(int r) {
+    return FMT == T_Q4_K ? (r == 0 ? 0 : 64) : FMT == T_Q6_K ? (r == 0 ? 64 : r == 1 ? 32 : 8) : 0;
+  }
+  __host__ __device__ static constexpr int len0(int r) {
+    return FMT == T_Q4_K ? (r == 0 ? 16 : 64) : FMT == T_Q6_K ? (r == 0 ? 64 : r == 1 ? 32 : 18) : 4 * BB;
+  }
+  __host__ __device__ static constexpr int dlen(int r) { return FMT == T_Q6_K && r == 2 ? -8 : 0; }
+  __host__ __device__ static constexpr int pieces(int r) {
+    return FMT == T_Q4_K ? len0(r) / 16 : (len0(r) + 30) / 16;
+  }
+  static constexpr int P = pieces(0) + (NR > 1 ? pieces(1) : 0) + (NR > 2 ? pieces(2) : 0);
   static constexpr int Ps = P | 1;
-  static constexpr int W = FMT == T_Q8_0 ? 4 : 8;
-  static constexpr int NT = 32 * W;
-  static constexpr int WCopies = (NT * Ps + 63) / 64;
+  static constexpr int WCopies = (kPfNT * Ps + 63) / 64;
   static constexpr int WBytes = WCopies * 1024;
+  static constexpr int Copies = WCopies + kPfACopies;
+  static constexpr int CopiesPerWave = (Copies + kPfW - 1) / kPfW;
   static constexpr int Lds = 2 * kPfABytes + 2 * WBytes + 3 * kPfM * 4;
-  static_assert(!AL || SB % 16 == 0, "aligned stages are whole pieces");
-  static_assert(Lds <= 160 * 1024, "one workgroup's buffers fit a CU's LDS");
+  static_assert(Lds <= 80 * 1024, "two workgroups' buffers fit a CU's LDS");
 };
 
 // Two f32 values rounded to the 16-bit type (to nearest even), packed.
@@ -94,6 +119,9 @@ __device__ __forceinline__ pf_f16 mfma16(pf_u4 a, pf_u4 b, pf_f16 c) {
 // multiply-then-add gives.
 template <bool BF>
 __device__ __forceinline__ pf_u4 deq8(uint32_t w0, uint32_t w1, float d, float c) {
+  // opaque to the compiler, so that byte i converts in one v_cvt_f32_ubyte<i>
+  // rather than a bit-field extract of the caller's mask and a conversion
+  asm("" : "+v"(w0), "+v"(w1));
   float v[8];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
@@ -108,47 +136,31 @@ __device__ __forceinline__ pf_u4 deq8(uint32_t w0, uint32_t w1, float d, float c
   return r;
 }
 
-template <bool AL, int N>
-__device__ __forceinline__ void lds_get(const uint8_t* win, int off, uint32_t* out) {
-  if constexpr (AL && N == 4) {
-    const uint4 v = *(const uint4*)(win + off);
-    out[0] = v.x;
-    out[1] = v.y;
-    out[2] = v.z;
-    out[3] = v.w;
-  } else if constexpr (AL && N == 2) {
-    const uint2 v = *(const uint2*)(win + off);
-    out[0] = v.x;
-    out[1] = v.y;
-  } else {
-    lds_words<N>(win, off, out);
-  }
-}
-
-// One stage of a weight row for lane half h, from the row's window at byte o:
-// step(piece, b) for each of its 16 steps, `piece` the 8-value group (of the
-// stage's 32) whose values b holds. nb_left = the row's 32-value blocks from
-// this stage on (32-value formats: blocks past the row are skipped).
-template <int FMT, bool AL, bool BF, class Step>
-__device__ __forceinline__ void pf_stage(const uint8_t* win, int o, int h, int nb_left, uint32_t t0, uint32_t t1,
-                                         uint32_t t2, uint32_t t3, Step&& step) {
+// One stage of a weight row for lane half h from its LDS window `win`; `o`
+// is the stage base's offset in its 16-byte piece, `hf` the super-block half
+// (K-quants), nb_left the row's 32-value blocks from this stage on (blocks
+// past the row are skipped). step(piece, b) for each of the 8 steps, `piece`
+// the 8-value group (of the stage's 16) whose values b holds.
+template <int FMT, bool BF, class Step>
+__device__ __forceinline__ void pf_stage(const uint8_t* win, int o, int hf, int h, int nb_left, uint32_t t0,
+                                         uint32_t t1, uint32_t t2, uint32_t t3, Step&& step) {
   if constexpr (FMT == T_Q4_K) {
     // d, dmin, 12 scale bytes, then qs[128]: value 64p + l is the low nibble
     // of qs[32p + l], value 64p + 32 + l its high nibble (l < 32); sub-block
     // j = 2p (low) and 2p + 1 (high) scale d * sc_j, offset dmin * m_j
-    // (k_quants.rs to_float of BlockQ4K). Lane half h takes bytes
-    // 32p + 16h .. +15: steps t = 0, 1 the low nibbles of its bytes 0-7, 8-15,
-    // t = 2, 3 the high nibbles.
-    uint32_t hd[4];
-    lds_get<AL, 4>(win, o, hd);
+    // (k_quants.rs to_float of BlockQ4K). This half holds p = 2 hf, 2 hf + 1.
+    // Lane half h takes bytes 32p + 16h .. +15: steps t = 0, 1 the low
+    // nibbles of its bytes 0-7, 8-15, t = 2, 3 the high nibbles.
+    const uint4 hv = *(const uint4*)win;
+    const uint32_t hd[4] = {hv.x, hv.y, hv.z, hv.w};
     const float d = h2f((uint16_t)(hd[0] & 0xFFFF)), dm = h2f((uint16_t)(hd[0] >> 16));
     auto sb = [&](int i) { return (int)((hd[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFF); };
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
+    for (int pp = 0; pp < 2; pp++) {
       int sc[2], mn[2];
 #pragma unroll
       for (int u = 0; u < 2; u++) {
-        const int j = 2 * p + u;
+        const int j = 4 * hf + 2 * pp + u;  // uniform
         if (j < 4) {
           sc[u] = sb(j) & 63;
           mn[u] = sb(j + 4) & 63;
@@ -160,56 +172,55 @@ __device__ __forceinline__ void pf_stage(const uint8_t* win, int o, int h, int n
       const float d1a = d * (float)sc[0], m1a = dm * (float)mn[0];
       // the high nibbles are read in place (16 q): the scale / 16 is exact
       const float d1b = d * (float)sc[1] * 0.0625f, m1b = dm * (float)mn[1];
-      uint32_t q[4];
-      lds_get<AL, 4>(win, o + 16 + 32 * p + 16 * h, q);
-      step(8 * p + 2 * h, deq8<BF>(q[0] & 0x0F0F0F0Fu, q[1] & 0x0F0F0F0Fu, d1a, -m1a));
-      step(8 * p + 2 * h + 1, deq8<BF>(q[2] & 0x0F0F0F0Fu, q[3] & 0x0F0F0F0Fu, d1a, -m1a));
-      step(8 * p + 4 + 2 * h, deq8<BF>(q[0] & 0xF0F0F0F0u, q[1] & 0xF0F0F0F0u, d1b, -m1b));
-      step(8 * p + 4 + 2 * h + 1, deq8<BF>(q[2] & 0xF0F0F0F0u, q[3] & 0xF0F0F0F0u, d1b, -m1b));
+      const uint4 qv = *(const uint4*)(win + 16 + 32 * pp + 16 * h);
+      step(8 * pp + 2 * h, deq8<BF>(qv.x & 0x0F0F0F0Fu, qv.y & 0x0F0F0F0Fu, d1a, -m1a));
+      step(8 * pp + 2 * h + 1, deq8<BF>(qv.z & 0x0F0F0F0Fu, qv.w & 0x0F0F0F0Fu, d1a, -m1a));
+      step(8 * pp + 4 + 2 * h, deq8<BF>(qv.x & 0xF0F0F0F0u, qv.y & 0xF0F0F0F0u, d1b, -m1b));
+      step(8 * pp + 4 + 2 * h + 1, deq8<BF>(qv.z & 0xF0F0F0F0u, qv.w & 0xF0F0F0F0u, d1b, -m1b));
     }
   } else if constexpr (FMT == T_Q6_K) {
     // ql[128], qh[64], sc[16] (int8), d: in half g (values 128g ..), value
     // 128g + 32j + l (l < 32) is the 6-bit code of ql[64g + 32(j&1) + l]'s
     // low (j < 2) or high nibble and bits 2j, 2j+1 of qh[32g + l], minus 32,
-    // times d * sc[8g + l/16 + 2j] (to_float of BlockQ6K). Lane half h takes
-    // l = 16u + 8h .. +7.
-    uint32_t scw[4];
-    lds_words<4>(win, o + 192, scw);
-    const float d = h2f((uint16_t)lds_u16(win, o + 208));
+    // times d * sc[8g + l/16 + 2j] (to_float of BlockQ6K). This half g = hf;
+    // its regions: ql[64g ..] at window byte o, qh[32g ..] at 80 + o, sc[8g ..]
+    // then d at 128 + ((o + 8g) & 15). Lane half h takes l = 16u + 8h .. +7.
+    const int o2 = 128 + ((o + 8 * hf) & 15);
+    uint32_t scw[2];
+    lds_words<2>(win, o2, scw);
+    const float d = h2f((uint16_t)lds_u16(win, o2 + 16 - 8 * hf));
 #pragma unroll
-    for (int g = 0; g < 2; g++)
+    for (int u = 0; u < 2; u++) {
+      uint32_t A[2], B[2], H[2];
+      lds_words<2>(win, o + 16 * u + 8 * h, A);
+      lds_words<2>(win, o + 32 + 16 * u + 8 * h, B);
+      lds_words<2>(win, 80 + o + 16 * u + 8 * h, H);
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
-        uint32_t A[2], B[2], H[2];
-        lds_words<2>(win, o + 64 * g + 16 * u + 8 * h, A);
-        lds_words<2>(win, o + 64 * g + 32 + 16 * u + 8 * h, B);
-        lds_words<2>(win, o + 128 + 32 * g + 16 * u + 8 * h, H);
+      for (int j = 0; j < 4; j++) {
+        const uint32_t* src = (j & 1) ? B : A;
+        uint32_t c[2];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const uint32_t* src = (j & 1) ? B : A;
-          uint32_t c[2];
-#pragma unroll
-          for (int w = 0; w < 2; w++) {
-            const uint32_t nib = (j & 2) ? ((src[w] >> 4) & 0x0F0F0F0Fu) : (src[w] & 0x0F0F0F0Fu);
-            c[w] = nib | (((H[w] >> (2 * j)) & 0x03030303u) << 4);
-          }
-          const int si = 8 * g + u + 2 * j;
-          const float ds = d * (float)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xFF);
-          // ds (code - 32) as one rounding of ds * code - 32 ds
-          step(16 * g + 4 * j + 2 * u + h, deq8<BF>(c[0], c[1], ds, -32.0f * ds));
+        for (int w = 0; w < 2; w++) {
+          const uint32_t nib = (j & 2) ? ((src[w] >> 4) & 0x0F0F0F0Fu) : (src[w] & 0x0F0F0F0Fu);
+          c[w] = nib | (((H[w] >> (2 * j)) & 0x03030303u) << 4);
         }
+        const int si = u + 2 * j;
+        const float ds = d * (float)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xFF);
+        // ds (code - 32) as one rounding of ds * code - 32 ds
+        step(4 * j + 2 * u + h, deq8<BF>(c[0], c[1], ds, -32.0f * ds));
       }
+    }
   } else {
-    // 8 blocks of 32 values. Q8_0: f16 d, 32 int8 codes; lane half h takes
+    // 4 blocks of 32 values. Q8_0: f16 d, 32 int8 codes; lane half h takes
     // codes 16t + 8h .. +7 for steps t = 0, 1. IQ4_NL (f16 d) and MXFP4 (e8m0
     // scale, halved against the doubled table): value l < 16 the low nibble of
     // qs[l], 16 + l the high; lane half h takes qs[8h .. 8h+7], the low
     // nibbles at t = 0, the high at t = 1. Signed codes are read as
     // unsigned (code + 128) and fma(d, code + 128, -128 d): exact.
-    constexpr int B = FMT == T_Q8_0 ? 34 : FMT == T_IQ4_NL ? 18 : 17;
+    constexpr int B = PfShape<FMT>::BB;
     constexpr int Head = FMT == T_MXFP4 ? 1 : 2;
 #pragma unroll
-    for (int b = 0; b < 8; b++) {
+    for (int b = 0; b < 4; b++) {
       if (b >= nb_left) break;  // uniform
       const int ob = o + B * b;
       float d;
@@ -227,26 +238,66 @@ __device__ __forceinline__ void pf_stage(const uint8_t* win, int o, int h, int n
       } else {
         uint32_t q[2];
         lds_words<2>(win, ob + Head + 8 * h, q);
+        pf_u4 bv[2];
+        bool table = true;
+        if constexpr (FMT == T_MXFP4) {
+          // E2M1 codes times the scale 2^(e-127), rounded to the 16-bit type,
+          // by the converter of gfx950 (two codes of a byte a conversion, its
+          // low nibble first): the table path's value bit for bit (checked on
+          // every code at every scale byte but 255, whose 2^128 is not an f32;
+          // and the sign of a zero code, invisible in any sum of products).
+          // Pairs of the lane's bytes' low (t = 0) or high nibbles are packed
+          // into one byte each, bytes 0 and 2 of a word.
+          const uint32_t e = lds_u32(win, ob) & 0xFF;
+          table = e == 255;
+          if (!table) {
+            const float sc = __builtin_bit_cast(float, e == 0 ? 0x00400000u : e << 23);
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-          const uint32_t c0 = (uint32_t)lut16(t ? (q[0] >> 4) & 0x0F0F0F0Fu : q[0] & 0x0F0F0F0Fu, t0, t1, t2, t3);
-          const uint32_t c1 = (uint32_t)lut16(t ? (q[1] >> 4) & 0x0F0F0F0Fu : q[1] & 0x0F0F0F0Fu, t0, t1, t2, t3);
-          step(4 * b + 2 * t + h, deq8<BF>(c0 ^ 0x80808080u, c1 ^ 0x80808080u, d, -128.0f * d));
+            for (int t = 0; t < 2; t++) {
+              uint32_t r[4];
+#pragma unroll
+              for (int w = 0; w < 2; w++) {
+                uint32_t v = t ? (q[w] >> 4) & 0x0F0F0F0Fu : q[w] & 0x0F0F0F0Fu;
+                v |= v >> 4;
+                if constexpr (BF) {
+                  r[2 * w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 0));
+                  r[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 2));
+                } else {
+                  r[2 * w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 0));
+                  r[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 2));
+                }
+              }
+              bv[t].x = r[0];
+              bv[t].y = r[1];
+              bv[t].z = r[2];
+              bv[t].w = r[3];
+            }
+          }
         }
+        if (table) {
+#pragma unroll
+          for (int t = 0; t < 2; t++) {
+            const uint32_t c0 = (uint32_t)lut16(t ? (q[0] >> 4) & 0x0F0F0F0Fu : q[0] & 0x0F0F0F0Fu, t0, t1, t2, t3);
+            const uint32_t c1 = (uint32_t)lut16(t ? (q[1] >> 4) & 0x0F0F0F0Fu : q[1] & 0x0F0F0F0Fu, t0, t1, t2, t3);
+            bv[t] = deq8<BF>(c0 ^ 0x80808080u, c1 ^ 0x80808080u, d, -128.0f * d);
+          }
+        }
+        step(4 * b + h, bv[0]);
+        step(4 * b + 2 + h, bv[1]);
       }
     }
   }
 }
 
-template <int FMT, bool AL, bool BF>
-__global__ __launch_bounds__((64 * PfShape<FMT, AL>::W)) void moe_pf_kernel(
+template <int FMT, bool BF>
+__global__ __launch_bounds__(64 * kPfW, 2) void moe_pf_kernel(
     const uint8_t* __restrict__ W, int64_t n, int64_t k, int64_t rb, int64_t estride, int num_experts,
     const uint16_t* __restrict__ x, int64_t x_stride, const int32_t* __restrict__ chunks,
     const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int topk, int size_m, float* __restrict__ dst,
     int64_t ldd) {
-  using S = PfShape<FMT, AL>;
+  using S = PfShape<FMT>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* const sA = smem;                          // [2][32 rows][512 B]
+  uint8_t* const sA = smem;                          // [2][64 rows][256 B]
   uint8_t* const sW = smem + 2 * kPfABytes;          // [2][WBytes]
   int* const s_in = (int*)(sW + 2 * S::WBytes);      // the chunk's input rows
   int* const s_out = s_in + kPfM;                    // output rows (-1: none)
@@ -255,7 +306,7 @@ __global__ __launch_bounds__((64 * PfShape<FMT, AL>::W)) void moe_pf_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31, h = lane >> 5;
-  const int64_t n0 = (int64_t)blockIdx.x * S::NT;
+  const int64_t n0 = (int64_t)blockIdx.x * kPfNT;
   const int nb32 = (int)(k / 32);
   const int nst = (int)((k + kPfK - 1) / kPfK);
   const int nch = __builtin_amdgcn_readfirstlane(chunks[0]);
@@ -270,6 +321,10 @@ __global__ __launch_bounds__((64 * PfShape<FMT, AL>::W)) void moe_pf_kernel(
   // this lane's weight row (rows past n read the last; never stored)
   const int64_t wrow = n0 + 32 * wv + r32 < n ? n0 + 32 * wv + r32 : n - 1;
   const uint32_t wrow_off = (uint32_t)(wrow * rb);
+  // a stage's base in a weight row: its super-block (K-quants) or 4 blocks
+  auto stage_base = [&](int st) -> uint32_t {
+    return S::KQ ? (uint32_t)(S::BB * (st >> 1)) : (uint32_t)(4 * S::BB * st);
+  };
 
   for (int c = blockIdx.y; c < nch; c += gridDim.y) {
     const int start = __builtin_amdgcn_readfirstlane(chunks[1 + 3 * c]);
@@ -285,35 +340,68 @@ __global__ __launch_bounds__((64 * PfShape<FMT, AL>::W)) void moe_pf_kernel(
     }
     __syncthreads();
     const uint8_t* const We = W + (int64_t)e * estride;
+    const bool two = cnt > 32;  // the second row tile has entries
 
-    // The copies of stage st into buffer half `buf`: weight copy i moves
-    // window pieces f = 64 i + L (row f / Ps, piece f % Ps of the aligned
-    // window at or before the row's stage, clamped to the piece holding the
-    // stage's last byte in the row); input copy i moves rows 2i, 2i + 1, lane
-    // L writing position L % 32 of row m = 2i + L/32, which holds piece
-    // (L % 32) ^ m of the row's stage (clamped to the row's last piece). The
-    // waves take copies wv, wv + W, ...
+    // The copies of a stage into buffer half `buf`. Weight copy i moves window
+    // pieces f = 64 i + L: row f / Ps, piece f % Ps, which is piece q of region
+    // r's aligned window (clamped to the piece holding the region's last byte
+    // in the row). Input copy i moves rows 4i .. 4i + 3: lane L writes position
+    // L % 16 of row m = 4i + L/16, which holds piece (L % 16) ^ (m % 16) of the
+    // row's stage (clamped to the row's last piece); copies of rows past the
+    // chunk's entries are skipped. The waves take copies wv, wv + W, ...; a
+    // lane keeps, per copy, its row's byte offset and its piece's offset in the
+    // window (with the region number in the high half).
+    uint32_t c_row[S::CopiesPerWave], c_pr[S::CopiesPerWave];
+#pragma unroll
+    for (int u = 0; u < S::CopiesPerWave; u++) {
+      const int j = wv + kPfW * u;
+      if (j < S::WCopies) {
+        const uint32_t f = 64u * (uint32_t)j + (uint32_t)lane;
+        const uint32_t r = f / (uint32_t)S::Ps < (uint32_t)kPfNT ? f / (uint32_t)S::Ps : kPfNT - 1;
+        const int64_t gr = n0 + r < n ? n0 + r : n - 1;
+        int pc = (int)(f % (uint32_t)S::Ps), reg = 0;
+        pc = pc < S::P ? pc : S::P - 1;  // the odd stride's spare piece repeats the last
+#pragma unroll
+        for (int q = 0; q < S::NR - 1; q++)
+          if (pc >= S::pieces(reg)) {
+            pc -= S::pieces(reg);
+            reg++;
+          }
+        c_row[u] = (uint32_t)(gr * rb);
+        c_pr[u] = 16u * (uint32_t)pc | ((uint32_t)reg << 16);
+      } else {
+        const int m = 4 * (j - S::WCopies) + (lane >> 4);
+        c_row[u] = 2u * (uint32_t)s_in[m < kPfM ? m : 0] * (uint32_t)x_stride;
+        c_pr[u] = 16u * (uint32_t)((lane & 15) ^ (m & 15));
+      }
+    }
     auto issue = [&](int st, int buf) {
-      for (int j = wv; j < S::WCopies + kPfACopies; j += S::W) {
+      const uint32_t sbase = stage_base(st);
+      const int hf = st & 1;
+      // the regions' offsets from the row and lengths at this stage (uniform)
+      uint32_t ra[3], rl[3];
+#pragma unroll
+      for (int r = 0; r < 3; r++) {
+        ra[r] = sbase + (uint32_t)(S::off0(r) + hf * S::dlt(r));
+        rl[r] = (uint32_t)(S::len0(r) + hf * S::dlen(r));
+      }
+#pragma unroll
+      for (int u = 0; u < S::CopiesPerWave; u++) {
+        const int j = wv + kPfW * u;
         if (j < S::WCopies) {
-          const uint32_t f = 64u * (uint32_t)j + (uint32_t)lane;
-          const uint32_t r = f / (uint32_t)S::Ps < (uint32_t)S::NT ? f / (uint32_t)S::Ps : S::NT - 1;
-          const int64_t gr = n0 + r < n ? n0 + r : n - 1;
-          const uint32_t rs = (uint32_t)(gr * rb);
-          const uint32_t a = rs + (uint32_t)(S::SB * st);
-          const uint32_t send = a + S::SB < rs + (uint32_t)rb ? a + S::SB : rs + (uint32_t)rb;
-          const uint32_t first = a & ~15u, last = (send - 1u) & ~15u;
-          const uint32_t off = first + 16u * (f % (uint32_t)S::Ps);
-          dma16(We, off < last ? off : last,
-                __builtin_amdgcn_readfirstlane(lds_addr(sW + buf * S::WBytes + 1024 * j)));
-        } else {
-          const int i = j - S::WCopies;
-          const int m = 2 * i + (lane >> 5);
-          const uint32_t q = (uint32_t)((lane & 31) ^ m);
-          const uint32_t el = (uint32_t)(kPfK * st) + 8u * q;
-          const uint32_t cl = el < (uint32_t)k - 8u ? el : (uint32_t)k - 8u;
-          dma16(x, 2u * ((uint32_t)s_in[m] * (uint32_t)x_stride + cl),
-                __builtin_amdgcn_readfirstlane(lds_addr(sA + buf * kPfABytes + 1024 * i)));
+          const uint32_t reg = c_pr[u] >> 16;
+          const uint32_t ro = S::NR == 1 ? ra[0] : reg == 0 ? ra[0] : (S::NR == 2 || reg == 1) ? ra[1] : ra[2];
+          const uint32_t rlen = S::NR == 1 ? rl[0] : reg == 0 ? rl[0] : (S::NR == 2 || reg == 1) ? rl[1] : rl[2];
+          const uint32_t a = c_row[u] + ro;
+          const uint32_t rend = a + rlen, row_end = c_row[u] + (uint32_t)rb;
+          const uint32_t send = rend < row_end ? rend : row_end;
+          const uint32_t last = (send - 1u) & ~15u, o = (a & ~15u) + (c_pr[u] & 0xFFFFu);
+          dma16(We, o < last ? o : last, __builtin_amdgcn_readfirstlane(lds_addr(sW + buf * S::WBytes + 1024 * j)));
+        } else if (j < S::Copies && 4 * (j - S::WCopies) < cnt) {
+          const uint32_t el = (uint32_t)(kPfRowBytes * st) + c_pr[u];
+          const uint32_t lim = 2u * ((uint32_t)k - 8u);
+          dma16(x, c_row[u] + (el < lim ? el : lim),
+                __builtin_amdgcn_readfirstlane(lds_addr(sA + buf * kPfABytes + 1024 * (j - S::WCopies))));
         }
       }
     };
@@ -321,38 +409,47 @@ __global__ __launch_bounds__((64 * PfShape<FMT, AL>::W)) void moe_pf_kernel(
     issue(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    pf_f16 acc;
+    pf_f16 acc0, acc1;
 #pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+    for (int i = 0; i < 16; i++) {
+      acc0[i] = 0.0f;
+      acc1[i] = 0.0f;
+    }
+    const int sw = r32 & 15;  // this lane's A rows' swizzle (rows r32 and 32 + r32)
     for (int st = 0; st < nst; st++) {
       const int cur = st & 1;
       if (st + 1 < nst) issue(st + 1, cur ^ 1);
       const uint8_t* win = sW + cur * S::WBytes + (32 * wv + r32) * (S::Ps * 16);
-      const int o = AL ? 0 : (int)((wrow_off + (uint32_t)(S::SB * st)) & 15u);
-      const uint8_t* arow = sA + cur * kPfABytes + r32 * 512;
-      pf_stage<FMT, AL, BF>(win, o, h, nb32 - 8 * st, t0, t1, t2, t3, [&](int piece, pf_u4 b) {
-        const pf_u4 a = *(const pf_u4*)(arow + 16 * (piece ^ r32));
-        acc = mfma16<BF>(a, b, acc);
+      const int o = (int)((wrow_off + stage_base(st)) & 15u);
+      const uint8_t* arow = sA + cur * kPfABytes + r32 * kPfRowBytes;
+      pf_stage<FMT, BF>(win, o, st & 1, h, nb32 - 4 * st, t0, t1, t2, t3, [&](int piece, pf_u4 b) {
+        const int ap = 16 * (piece ^ sw);
+        acc0 = mfma16<BF>(*(const pf_u4*)(arow + ap), b, acc0);
+        if (two) acc1 = mfma16<BF>(*(const pf_u4*)(arow + 32 * kPfRowBytes + ap), b, acc1);
       });
       // the next stage has landed, and every wave is done with this one
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
-    // lane L holds entries m = 8 (i/4) + 4 h + i%4 of weight row r32
+    // lane L holds entries m = 8 (i/4) + 4 h + i%4 (and 32 + m) of weight row r32
     const int64_t col = n0 + 32 * wv + r32;
     if (col < n) {
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const int m = 8 * (i >> 2) + 4 * h + (i & 3);
         const int p = s_out[m];
-        if (p >= 0) dst[(int64_t)p * ldd + col] = __fmul_rn(acc[i], s_sc[m]);
+        if (p >= 0) dst[(int64_t)p * ldd + col] = __fmul_rn(acc0[i], s_sc[m]);
+        if (two) {
+          const int p1 = s_out[32 + m];
+          if (p1 >= 0) dst[(int64_t)p1 * ldd + col] = __fmul_rn(acc1[i], s_sc[32 + m]);
+        }
       }
     }
     __syncthreads();  // the entry tables are rewritten by the next chunk
   }
 }
 
-// Block 0: the run table and the chunk table of 32 entries. Blocks 1..: the
+// Block 0: the run table and the chunk table of 64 entries. Blocks 1..: the
 // input rows into 16-bit values (f32 rounded to nearest even, or a 16-bit
 // input copied) at xo [rows][k], 16-byte aligned, 8 values a thread.
 template <int XK>
@@ -389,39 +486,38 @@ __global__ __launch_bounds__(kPfPrepThreads) void moe_pf_prep_kernel(const int32
   }
 }
 
-template <int FMT, bool AL, bool BF>
+template <int FMT, bool BF>
 hipError_t launch_pf(const void* w, int num_experts, int64_t n, int64_t k, const uint16_t* x, int64_t x_stride,
                      const int32_t* chunks, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                      float* dst, int64_t ldd, hipStream_t st) {
   QMM_NOTE_LAUNCH();
-  using S = PfShape<FMT, AL>;
-  const int64_t rb = FMT == T_Q4_K ? k / 256 * 144 : FMT == T_Q6_K ? k / 256 * 210 : k / 32 * (S::SB / 8);
+  using S = PfShape<FMT>;
+  const int64_t rb = S::KQ ? k / 256 * S::BB : k / 32 * S::BB;
   const int64_t estride = n * rb;
-  // chunk slots: with entries grouped by expert at most size_m/32 + experts
+  // chunk slots: with entries grouped by expert at most size_m/64 + experts
   // chunks; more (entries in any order) are taken by the workgroups in turn
   const int64_t runs_max = size_m < num_experts ? size_m : num_experts;
   int64_t gy = (size_m + kPfM - 1) / kPfM + runs_max;
   gy = gy < 1 ? 1 : gy > 65535 ? 65535 : gy;
-  const dim3 grid((unsigned)((n + S::NT - 1) / S::NT), (unsigned)gy);
-  auto* kfn = &moe_pf_kernel<FMT, AL, BF>;
-  if (set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
-  kfn<<<grid, 64 * S::W, S::Lds, st>>>((const uint8_t*)w, n, k, rb, estride, num_experts, x, x_stride, chunks, ids,
+  const dim3 grid((unsigned)((n + kPfNT - 1) / kPfNT), (unsigned)gy);
+  auto* kfn = &moe_pf_kernel<FMT, BF>;
+  if (S::Lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+  kfn<<<grid, 64 * kPfW, S::Lds, st>>>((const uint8_t*)w, n, k, rb, estride, num_experts, x, x_stride, chunks, ids,
                                        topk_w, topk, (int)size_m, dst, ldd);
   return hipGetLastError();
 }
 
 template <bool BF>
-hipError_t launch_pf_type(int type, bool aligned, const void* w, int num_experts, int64_t n, int64_t k,
-                          const uint16_t* x, int64_t x_stride, const int32_t* chunks, const int32_t* ids,
-                          const float* topk_w, int topk, int64_t size_m, float* dst, int64_t ldd, hipStream_t st) {
-#define QMM_PF(F, A) \
-  launch_pf<F, A, BF>(w, num_experts, n, k, x, x_stride, chunks, ids, topk_w, topk, size_m, dst, ldd, st)
+hipError_t launch_pf_type(int type, const void* w, int num_experts, int64_t n, int64_t k, const uint16_t* x,
+                          int64_t x_stride, const int32_t* chunks, const int32_t* ids, const float* topk_w, int topk,
+                          int64_t size_m, float* dst, int64_t ldd, hipStream_t st) {
+#define QMM_PF(F) launch_pf<F, BF>(w, num_experts, n, k, x, x_stride, chunks, ids, topk_w, topk, size_m, dst, ldd, st)
   switch (type) {
-    case T_Q4_K: return aligned ? QMM_PF(T_Q4_K, true) : QMM_PF(T_Q4_K, false);
-    case T_Q6_K: return QMM_PF(T_Q6_K, false);
-    case T_Q8_0: return QMM_PF(T_Q8_0, false);
-    case T_IQ4_NL: return aligned ? QMM_PF(T_IQ4_NL, true) : QMM_PF(T_IQ4_NL, false);
-    case T_MXFP4: return QMM_PF(T_MXFP4, false);
+    case T_Q4_K: return QMM_PF(T_Q4_K);
+    case T_Q6_K: return QMM_PF(T_Q6_K);
+    case T_Q8_0: return QMM_PF(T_Q8_0);
+    case T_IQ4_NL: return QMM_PF(T_IQ4_NL);
+    case T_MXFP4: return QMM_PF(T_MXFP4);
     default: return hipErrorInvalidValue;
   }
 #undef QMM_PF
@@ -432,6 +528,11 @@ hipError_t launch_pf_type(int type, bool aligned, const void* w, int num_experts
 bool moe_pf_supported(int type, int64_t k) {
   if (type == T_Q4_K || type == T_Q6_K) return k % 256 == 0 && k >= 256;
   return (type == T_Q8_0 || type == T_IQ4_NL || type == T_MXFP4) && k % 32 == 0 && k >= 32;
+}
+
+bool moe_pf_weights_ok(int type, const void* w) {
+  // Q4_K stages copy whole 16-byte pieces of the rows
+  return type != T_Q4_K || ((uintptr_t)w & 15) == 0;
 }
 
 int64_t moe_pf_row_bytes(int type, int64_t k) {
@@ -483,13 +584,11 @@ hipError_t launch_moe_pf_prep(const int32_t* expert_ids, int64_t size_m, int32_t
 hipError_t launch_moe_pf(int type, bool bf16, const void* w, int num_experts, int64_t n, int64_t k, const uint16_t* x,
                          int64_t x_stride, const int32_t* chunks, const int32_t* ids, const float* topk_w, int topk,
                          int64_t size_m, float* dst, int64_t ldd, hipStream_t st) {
-  // whole-piece stages: 16-byte aligned weights whose rows hold whole stages
-  // of a multiple of 16 bytes
-  const bool aligned = ((uintptr_t)w & 15) == 0 && k % 256 == 0;
-  return bf16 ? launch_pf_type<true>(type, aligned, w, num_experts, n, k, x, x_stride, chunks, ids, topk_w, topk,
-                                     size_m, dst, ldd, st)
-              : launch_pf_type<false>(type, aligned, w, num_experts, n, k, x, x_stride, chunks, ids, topk_w, topk,
-                                      size_m, dst, ldd, st);
+  if (!moe_pf_weights_ok(type, w)) return hipErrorInvalidValue;
+  return bf16 ? launch_pf_type<true>(type, w, num_experts, n, k, x, x_stride, chunks, ids, topk_w, topk, size_m, dst,
+                                     ldd, st)
+              : launch_pf_type<false>(type, w, num_experts, n, k, x, x_stride, chunks, ids, topk_w, topk, size_m, dst,
+                                      ldd, st);
 }
 
 }  // namespace qmm

@@ -13,6 +13,12 @@
 
 namespace qmm {
 
+// Entries go through in blocks of NT x kRunsPer: each thread loads its
+// kRunsPer consecutive ids (and the one before) at once, counts the run
+// starts among them, and one scan over the block numbers them, so a routing
+// of size_m entries costs size_m / (NT kRunsPer) dependent rounds.
+constexpr int kRunsPer = 8;
+
 template <int NT>
 __device__ __forceinline__ void moe_runs_block(const int32_t* __restrict__ expert_ids, int size_m,
                                                int32_t* __restrict__ runs) {
@@ -20,14 +26,26 @@ __device__ __forceinline__ void moe_runs_block(const int32_t* __restrict__ exper
   constexpr int kW = NT / 64;
   __shared__ int s_cnt[kW];
   const int t = (int)threadIdx.x, lane = t & 63, w = t >> 6;
-  int base = 0;  // runs started before this chunk
-  for (int c0 = 0; c0 < size_m; c0 += NT) {
-    const int i = c0 + t;
-    const bool in = i < size_m;
-    const int e = in ? expert_ids[i] : 0;
-    const bool f = in && (i == 0 || expert_ids[i - 1] != e);
-    const uint64_t m = __ballot(f);
-    if (lane == 0) s_cnt[w] = __popcll(m);
+  int base = 0;  // runs started before this block
+  for (int c0 = 0; c0 < size_m; c0 += NT * kRunsPer) {
+    const int i0 = c0 + t * kRunsPer;
+    int id[kRunsPer];
+#pragma unroll
+    for (int j = 0; j < kRunsPer; j++) id[j] = i0 + j < size_m ? expert_ids[i0 + j] : 0;
+    int prev = i0 > 0 && i0 <= size_m ? expert_ids[i0 - 1] : 0;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < kRunsPer; j++) {
+      cnt += (i0 + j < size_m && (i0 + j == 0 || id[j] != prev)) ? 1 : 0;
+      prev = id[j];
+    }
+    int v = cnt;  // inclusive sum over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int u = __shfl_up(v, d);
+      if (lane >= d) v += u;
+    }
+    if (lane == 63) s_cnt[w] = v;
     __syncthreads();
     int before = base, total = base;
 #pragma unroll
@@ -36,15 +54,20 @@ __device__ __forceinline__ void moe_runs_block(const int32_t* __restrict__ exper
       before += j < w ? c : 0;
       total += c;
     }
-    if (f) {
-      // this start's number: the chunk's earlier waves' starts, then this wave's below this lane
-      const int r = before + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-      runs[1 + 3 * r] = i;
-      runs[3 + 3 * r] = e;
+    // this thread's starts are numbered from before + (the wave's lanes below)
+    int r = before + v - cnt;
+    prev = i0 > 0 && i0 <= size_m ? expert_ids[i0 - 1] : 0;
+#pragma unroll
+    for (int j = 0; j < kRunsPer; j++) {
+      if (i0 + j < size_m && (i0 + j == 0 || id[j] != prev)) {
+        runs[1 + 3 * r] = i0 + j;
+        runs[3 + 3 * r] = id[j];
+        r++;
+      }
+      prev = id[j];
     }
     base = total;
-    __syncthreads();  // s_cnt is rewritten by the next chunk
+    __syncthreads();  // s_cnt is rewritten by the next block
   }
   // the starts are written (the barrier orders the workgroup's global
   // writes before these reads); run r ends where run r + 1 starts

@@ -641,7 +641,7 @@ int qmm_moe_forward_prefill(int type, const void* w, int num_experts, const void
   if (!launch) return QMM_OK;
   if (g_fail_next.exchange(false)) return QMM_NO_ROOM;
   if (workspace_bytes < *need || workspace == nullptr) return QMM_WORKSPACE_TOO_SMALL;
-  if (!w || !x || !dst || !sorted_ids || !expert_ids) return QMM_UNSUPPORTED;
+  if (!w || !x || !dst || !sorted_ids || !expert_ids || !qmm::moe_pf_weights_ok(type, w)) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
   int32_t* runs = (int32_t*)workspace;

@@ -135,6 +135,7 @@ hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64
 // or 1 bf16 copied, 2 f32 to f16, 3 f32 to bf16) and the grouped kernel over
 // 16-bit input rows (16-byte aligned, x_stride a multiple of 8).
 bool moe_pf_supported(int type, int64_t k);
+bool moe_pf_weights_ok(int type, const void* w);  // Q4_K: 16-byte aligned
 int64_t moe_pf_row_bytes(int type, int64_t k);
 size_t moe_pf_chunks_bytes(int64_t size_m);
 hipError_t launch_moe_pf_prep(const int32_t* expert_ids, int64_t size_m, int32_t* runs, int32_t* chunks,

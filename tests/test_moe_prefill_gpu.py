@@ -214,3 +214,59 @@ def test_prefill_status_paths():
     torch.cuda.synchronize()
     assert (out == 0).all()
     assert X_F16 == 0 and X_F32 == 2
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "MXFP4", "Q8_0"])
+def test_prefill_runs_longer_than_a_chunk(name):
+    """Two experts each chosen by all 100 tokens (runs of 100 entries: a
+    64-entry chunk and a 36-entry one) and a third expert chosen by 32 tokens
+    (exactly one row tile), per-pair inputs and routing weights."""
+    qtype = MOE_TYPES[name]
+    E, n, topk = 3, 160, 2
+    k = 512 if qtype in KQUANT else 384
+    tokens = 100
+    pairs = []
+    for t in range(tokens):
+        second = 2 if t < 32 else 1
+        pairs += [(0, t * topk), (second, t * topk + 1)]
+    pairs.sort()
+    expert_ids = np.array([e for e, _ in pairs], np.int32)
+    sorted_ids = np.array([p for _, p in pairs], np.int32)
+    rng = np.random.default_rng(123)
+    topk_w = rng.random(tokens * topk).astype(np.float32)
+    stack = expert_stack(qtype, E, n, k, 124)
+    x = rng.standard_normal((tokens * topk, k)).astype(np.float32)
+    xs = t32(x).half()
+    out = prefill_into(stack, xs, X_F16, k, sorted_ids, expert_ids, topk_w, topk, tokens * topk)
+    check_prefill(qtype, stack, xs.float().cpu().numpy(), out, sorted_ids, expert_ids, topk_w, topk, False)
+
+
+@pytest.mark.parametrize("xdt", ["f16", "bf16"])
+def test_prefill_mxfp4_every_code_at_extreme_scales(xdt):
+    """MXFP4 blocks with every E2M1 code under scale bytes 0, 1, 2, 100-160,
+    200, 254 and 255 (subnormal, overflowing and NaN-coded scales), read back
+    through one-hot input rows: each output equals the oracle's, bit for bit
+    (NaN where a zero input meets an infinite weight, in both)."""
+    from swarmllm_amd import GgmlDType
+
+    n, k = 32, 64
+    scales = [0, 1, 2, 254, 255] + list(range(100, 161, 3)) + [200]
+    rng = np.random.default_rng(5)
+    blocks = []
+    for j in range(n):
+        for b in range(k // 32):
+            e = scales[(2 * j + b) % len(scales)]
+            qs = rng.integers(0, 256, 16, dtype=np.uint8)
+            qs[:8] = np.arange(16, dtype=np.uint8)[::2] | (np.arange(16, dtype=np.uint8)[1::2] << 4)
+            blocks.append(np.concatenate([[e], qs]).astype(np.uint8))
+    wb = np.concatenate(blocks)
+    stack = QTensor(torch.from_numpy(wb).to(DEV), (1, n, k), GgmlDType(39))
+    x = np.eye(k, dtype=np.float32)
+    sorted_ids = np.arange(k, dtype=np.int32)
+    expert_ids = np.zeros(k, np.int32)
+    xs = torch.from_numpy(x).to(DEV).to(TORCH_X[xdt])
+    out = prefill_into(stack, xs, X_BF16 if xdt == "bf16" else X_F16, k, sorted_ids, expert_ids, None, 1, k)
+    want = qref.moe_prefill(39, wb, 1, n, k, x, xdt == "bf16", sorted_ids, expert_ids, None, 1)
+    assert np.array_equal(np.isnan(out), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal((out[fin] + np.float32(0)).view(np.uint32), (want[fin] + np.float32(0)).view(np.uint32))
