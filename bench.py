@@ -203,6 +203,22 @@ def time_gpu(fn, stream) -> float:
     return a.elapsed_time(b)
 
 
+SETTLE_MS = 40.0
+
+
+def settle(replay, stream, ms: float = SETTLE_MS) -> None:
+    """Untimed replays until about `ms` of GPU time has passed, so the timed
+    region that follows sees the GPU at its sustained clock (the first
+    ~10 ms of back-to-back launches run measurably slower while the clock
+    ramps)."""
+    import torch
+
+    spent, n = 0.0, 1
+    while spent < ms:
+        spent += time_gpu(lambda: [replay() for _ in range(n)], stream)
+        n = min(2 * n, 64)
+
+
 def single_matvec(layers, stream, reps: int) -> dict:
     """The product BASELINE.json's target names: ONE Q4_K 14336x4096 matvec
     at M = 1 (the gate projection alone, qmm_forward: one launch that
@@ -228,8 +244,7 @@ def single_matvec(layers, stream, reps: int) -> dict:
 
     g = capture(fn, stream)
     kernel = L.qmm_last_kernel().decode()
-    for _ in range(3):
-        g.replay()
+    settle(g.replay, stream)
     ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
     launches = reps * per_graph
     us = ms * 1e3 / launches
@@ -262,8 +277,7 @@ def dominant_kernel(layers, outs, stream, reps: int) -> dict:
                                                              ws.numel(), ctypes.byref(need), k, 1, 1, st))
 
     g = capture(fn, stream)
-    for _ in range(3):
-        g.replay()
+    settle(g.replay, stream)
     ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
     launches = reps * per_graph
     us = ms * 1e3 / launches
@@ -302,8 +316,7 @@ def gate_up_glu(layers, stream, reps: int) -> dict:
 
     g = capture(fn, stream)
     kernel = L.qmm_last_kernel().decode()
-    for _ in range(3):
-        g.replay()
+    settle(g.replay, stream)
     ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
     us = ms * 1e3 / (reps * per_graph)
     alg = 2 * 14336 * 16 * 144 + 4 * 4096 + 4 * 14336
@@ -357,8 +370,7 @@ def prefill_gemm(layers, stream, reps: int, name: str = "gate") -> dict:
     if L.qmm_gemm_launches() <= before:
         raise RuntimeError("the prefill product did not run the GEMM")
     kernel = L.qmm_last_kernel().decode()
-    for _ in range(2):
-        graph.replay()
+    settle(graph.replay, stream)
     ms = time_gpu(lambda: [graph.replay() for _ in range(reps)], stream)
     us = ms * 1e3 / (reps * len(layers))
     ops = 2.0 * M * n * k
@@ -396,8 +408,7 @@ def prefill_layer(layers, stream, reps: int) -> dict:
             enqueue_step(v, outs, st, rows=M)
 
     graph = capture(fn, stream)
-    for _ in range(2):
-        graph.replay()
+    settle(graph.replay, stream)
     ms = time_gpu(lambda: [graph.replay() for _ in range(reps)], stream)
     us = ms * 1e3 / (reps * len(layers))
     ops = 2.0 * M * sum(n * k for _, _, n, k in LAYER)
@@ -495,8 +506,7 @@ def c5_shard(stream, rows_list=(1, 8, 16), reps: int = 5) -> dict:
                 enqueue_step(lay, outs, s, C5_GROUPS, rows)
 
         g = capture(fn, stream)
-        for _ in range(2):
-            g.replay()
+        settle(g.replay, stream)
         ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream) / reps
         gbs = wbytes / (ms * 1e-3) / 1e9
         out["by_rows"][str(rows)] = {"ms_per_forward": round(ms, 4), "weight_gbs": round(gbs, 1),
@@ -574,8 +584,7 @@ def c4_moe(stream, reps: int = 20, copies: int = 2) -> dict:
     g = capture(fn, stream)
     if L.qmm_moe_launches() < before + 2 * copies:
         raise RuntimeError("the C4 step did not run the grouped expert kernels")
-    for _ in range(2):
-        g.replay()
+    settle(g.replay, stream)
     ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
     us = ms * 1e3 / (reps * copies)
     per_expert = 2 * inter * (hidden // 32) * 17 + hidden * (inter // 32) * 17
@@ -654,8 +663,7 @@ def moe_kquant(stream, reps: int = 10, copies: int = 2) -> dict:
         g = capture(fn, stream)
         if L.qmm_moe_launches() < before + 2 * copies:
             raise RuntimeError("the K-quant MoE step did not run the grouped kernels")
-        for _ in range(2):
-            g.replay()
+        settle(g.replay, stream)
         ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
         us = ms * 1e3 / (reps * copies)
         per_expert = 2 * inter * (hidden // 256) * 144 + hidden * (inter // 256) * 210
@@ -718,8 +726,7 @@ def moe_prompt_step(stream, qg, qd, gu, dn, E, hidden, inter, topk, tokens, sids
     g = capture(fn, stream)
     if L.qmm_moe_prefill_launches() < before + 2 * len(gu):
         raise RuntimeError("the prompt MoE step did not run the matrix-core grouped kernels")
-    for _ in range(2):
-        g.replay()
+    settle(g.replay, stream)
     ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
     us = ms * 1e3 / (reps * len(gu))
     wbytes = touched * (gu[0].numel() + dn[0].numel()) // E
@@ -794,8 +801,7 @@ def c1_q8_0(stream, reps: int = 50, copies: int = 16) -> dict:
                                                buf.data_ptr(), buf.numel(), ctypes.byref(need), k, n, 1, 1, s))
 
     g = capture(fn, stream)
-    for _ in range(2):
-        g.replay()
+    settle(g.replay, stream)
     ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
     us = ms * 1e3 / (reps * copies)
     alg = n * (k // 32) * 34 + 4 * k + 4 * n
@@ -832,8 +838,7 @@ def prefill_b32(stream, reps: int = 10, copies: int = 4) -> dict:
                 check("qmm_matmul", L.qmm_matmul(t, w.data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k, n, M, s))
 
         g = capture(fn, stream)
-        for _ in range(2):
-            g.replay()
+        settle(g.replay, stream)
         ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
         us = ms * 1e3 / (reps * copies)
         tops = 2.0 * M * n * k / (us * 1e-6) / 1e12
@@ -1002,10 +1007,15 @@ def main() -> int:
     rep = Replayer(layers, outs, stream)
     rep.prepare(args.warmup)
     rep.prepare(args.steps)
+    rep.prepare(len(layers))
+    # the GPU's clock settles first (untimed replays of whole rotations),
+    # then the W warmup steps, then exactly K timed steps
+    settle(lambda: rep.run(len(layers)), stream)
     with torch.cuda.stream(stream):
         rep.run(args.warmup)
     torch.cuda.synchronize()
-    log(f"warmup {args.warmup} steps done (graphs for {sorted(rep.graphs)} steps captured before timing)")
+    log(f"clock settled ({SETTLE_MS:.0f} ms of untimed replays), warmup {args.warmup} steps done "
+        f"(graphs for {sorted(rep.graphs)} steps captured before timing)")
 
     wall0 = time.perf_counter()
     ms = time_gpu(lambda: rep.run(args.steps), stream)
