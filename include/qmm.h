@@ -146,7 +146,11 @@ int qmm_force_dmmv(void);
  * quantized/cuda.rs:1653-1680). With launch == 0 nothing is enqueued and
  * *need is set to the workspace bytes the launch will want; with
  * launch != 0 the product is enqueued, and QMM_WORKSPACE_TOO_SMALL is
- * returned (nothing enqueued) when workspace_bytes < that size.
+ * returned (nothing enqueued) when workspace_bytes is less than the
+ * quantized activation. For a single-pass Q4_K GEMM whose tiles fill at
+ * most half the CUs, *need also counts the slots of a K split (the product
+ * cut into 2 or 4 parts along K, added in part order); with a workspace that
+ * holds the activation but not those slots the product runs uncut.
  * Replaces the plan/launch pair of swarm_mmq_matmul (mmq_entry.cu:162-203). */
 int qmm_forward(int type, const void *w, const float *x, int64_t x_stride, float *dst, int64_t ldd,
                 void *workspace, size_t workspace_bytes, size_t *need, int64_t k, int64_t n, int64_t rows,
@@ -157,8 +161,9 @@ int qmm_forward(int type, const void *w, const float *x, int64_t x_stride, float
  * (qmm_forward_noalloc_max_bytes()). No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc); the entry
- * point itself allocates nothing. Products whose planned workspace exceeds
- * the scratch return QMM_WORKSPACE_TOO_SMALL with nothing enqueued. All
+ * point itself allocates nothing. Products whose quantized activation
+ * exceeds the scratch return QMM_WORKSPACE_TOO_SMALL with nothing enqueued
+ * (a GEMM whose K-split slots do not fit beside it runs uncut). All
  * calls on one GPU share the scratch: calls that overlap on one GPU (other
  * streams, other threads) race on it. Results equal qmm_forward's bit for bit. */
 int qmm_forward_noalloc(int type, const void *w, const float *x, int64_t x_stride, float *dst, int64_t ldd,
@@ -172,7 +177,9 @@ size_t qmm_forward_noalloc_max_bytes(void);
  * rows the products run as one launch per 4 weights, each quantizing the
  * activation in LDS (workspace unused); otherwise the activation is
  * quantized once into the workspace and each weight's product reads it, the
- * weights the few-row matrix-core kernels take sharing one launch per 4. Plan (launch == 0) and
+ * weights the few-row matrix-core kernels or the single-pass Q4_K GEMM take
+ * sharing one launch per 4 (each weight's K split as its own forward would
+ * choose, so results equal qmm_forward's bit for bit). Plan (launch == 0) and
  * launch as qmm_forward. Replaces QMatMul::forward_shared with the CUDA
  * arm's shared activation (quantized/mod.rs:1221-1263,
  * quantized/cuda.rs:622-720). */

@@ -90,12 +90,26 @@ __device__ __forceinline__ float row_factor(float maxabs) {
   return __builtin_bit_cast(float, (uint32_t)(fe < 1 ? 1 : (fe > 254 ? 254 : fe)) << 23);
 }
 
-__global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const uint8_t* __restrict__ W, int64_t N, int nsb,
-                                                                  const int8_t* __restrict__ yq,
-                                                                  const float* __restrict__ yd,
-                                                                  const int16_t* __restrict__ ybs, int64_t M,
-                                                                  float* __restrict__ dst, int64_t ldd, int mtiles,
-                                                                  int remap) {
+// The launch's weights (up to kMaxTargets sharing one activation) and their
+// K splits; see launch_gemm_q4k_sp_targets.
+struct SpArgs {
+  const void* w[kMaxTargets];
+  float* dst[kMaxTargets];
+  int64_t ldd[kMaxTargets];
+  int64_t n[kMaxTargets];
+  int unit_end[kMaxTargets];   // workgroups of weights 0..t
+  int splits[kMaxTargets];     // K splits of weight t's tiles (1, 2 or 4)
+  int tile_base[kMaxTargets];  // the sum kernel's first workgroup for weight t (its split tiles before it)
+  int64_t part_off[kMaxTargets];  // its first slot in `part` (floats)
+  const int8_t* yq;
+  const float* yd;
+  const int16_t* ybs;
+  int64_t M;
+  float* part;    // split slots: tiles x splits x 256 x 128 f32
+  int nsb, mtiles, remap;
+};
+
+__global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a) {
   // Each half of each double buffer is its own object and the stage loop is
   // unrolled over two super-blocks, so every access names its buffer
   // statically (the compiler can tell reads of one half from writes of the other).
@@ -118,12 +132,34 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const uint8_t*
   const int wm = wv & 3, wn = wv >> 2;
   const int h = lane >> 5, r32 = lane & 31;
 
-  // workgroup -> tile; the row tiles of one weight tile on one XCD (its L2)
+  // workgroup -> (weight, tile, K split); the row tiles and splits of one
+  // weight tile on one XCD (its L2). Units are numbered weight after weight:
+  // weight t holds units [unit_end[t-1], unit_end[t]), each of its tiles
+  // `splits[t]` consecutive K ranges times the row tiles.
   const int total = (int)gridDim.x;
   const int b = (int)blockIdx.x;
-  const int idx = remap ? (b & 7) * (total >> 3) + (b >> 3) : b;
-  const int64_t m0 = (int64_t)(idx % mtiles) * kBM;
-  const int64_t n0 = (int64_t)(idx / mtiles) * kBN;
+  const int idx = a.remap ? (b & 7) * (total >> 3) + (b >> 3) : b;
+  const int t = idx < a.unit_end[0] ? 0 : idx < a.unit_end[1] ? 1 : idx < a.unit_end[2] ? 2 : 3;
+  // fields of weight t by selects (a dynamic index into the argument arrays
+  // would copy them to private memory)
+  auto pick = [&](const auto& arr) { return t == 0 ? arr[0] : t == 1 ? arr[1] : t == 2 ? arr[2] : arr[3]; };
+  const int u0 = t == 0 ? 0 : t == 1 ? a.unit_end[0] : t == 2 ? a.unit_end[1] : a.unit_end[2];
+  const int S = pick(a.splits);
+  const int mtiles = a.mtiles;
+  const int loc = idx - u0;
+  const int mt = loc % mtiles, rest = loc / mtiles;
+  const int split = rest % S, ct = rest / S;
+  const uint8_t* __restrict__ W = (const uint8_t*)pick(a.w);
+  const int64_t N = pick(a.n);
+  const int nsb = a.nsb;
+  const int8_t* __restrict__ yq = a.yq;
+  const float* __restrict__ yd = a.yd;
+  const int16_t* __restrict__ ybs = a.ybs;
+  const int64_t M = a.M;
+  const int64_t m0 = (int64_t)mt * kBM;
+  const int64_t n0 = (int64_t)ct * kBN;
+  // this workgroup's super-blocks
+  const int sb0 = split * nsb / S, sb1 = (split + 1) * nsb / S;
 
   const int64_t K = (int64_t)nsb * 256;
   const uint32_t rowbytes = (uint32_t)nsb * 144;
@@ -269,14 +305,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const uint8_t*
 
   // ---- prologue: row factors, stage 0 ----
 #pragma unroll
-  for (int u = 0; u < 4; u++) dma_a1(0, s_a0, u);
+  for (int u = 0; u < 4; u++) dma_a1(2 * sb0, s_a0, u);
 #pragma unroll
-  for (int u = 0; u < 3; u++) dma_w1(0, s_w0, u);
-  dma_rows(0, 0);
-  dma_rows(0, 1);
+  for (int u = 0; u < 3; u++) dma_w1(sb0, s_w0, u);
+  dma_rows(sb0, 0);
+  dma_rows(sb0, 1);
   if (tid < 256) {
     float mx = 0.0f;
-    for (int sb = 0; sb < nsb; sb++) mx = fmaxf(mx, fabsf(yd[prow * nsb + sb]));
+    for (int sb = sb0; sb < sb1; sb++) mx = fmaxf(mx, fabsf(yd[prow * nsb + sb]));
     s_rf[tid] = row_factor(mx);
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -292,9 +328,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const uint8_t*
   auto stage = [&](int sb, int half, const int8_t* sa, const int8_t* sbt, int8_t* na, int8_t* nbt,
                    const uint8_t* nw, int nhalf, const uint8_t* wcur, uint8_t* wnext) {
     const int g = 2 * sb + half;
-    const bool more = g + 1 < 2 * nsb;
-    const bool wmore = half == 0 && sb + 1 < nsb;  // the next super-block's raw weights
-    const bool rmore = half == 1 && sb + 1 < nsb;  // the next super-block's row inputs
+    const bool more = g + 1 < 2 * sb1;
+    const bool wmore = half == 0 && sb + 1 < sb1;  // the next super-block's raw weights
+    const bool rmore = half == 1 && sb + 1 < sb1;  // the next super-block's row inputs
     i4v a0 = frag(sa, arow0, 0), a1 = frag(sa, arow1, 0);
     i4v b0 = frag(sbt, bcol0, 0), b1 = frag(sbt, bcol1, 0);
 #pragma unroll
@@ -353,29 +389,79 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const uint8_t*
     __syncthreads();
   };
 
-  for (int sb = 0; sb < nsb; sb += 2) {
+  for (int sb = sb0; sb < sb1; sb += 2) {
     stage(sb, 0, s_a0, s_b0, s_a1, s_b1, s_w0, 1, s_w0, s_w1);
     stage(sb, 1, s_a1, s_b1, s_a0, s_b0, s_w1, 0, s_w0, s_w1);
-    if (sb + 1 < nsb) {
+    if (sb + 1 < sb1) {
       stage(sb + 1, 0, s_a0, s_b0, s_a1, s_b1, s_w1, 1, s_w1, s_w0);
       stage(sb + 1, 1, s_a1, s_b1, s_a0, s_b0, s_w0, 0, s_w1, s_w0);
     }
   }
 
   // ---- store, the row factor undone (exact powers of two) ----
+  float* __restrict__ dst = pick(a.dst);
+  const int64_t ldd = pick(a.ldd);
+  if (S == 1) {
 #pragma unroll
-  for (int tn = 0; tn < 2; tn++) {
-    const int64_t col = n0 + 64 * wn + 32 * tn + r32;
-    if (col >= N) continue;
+    for (int tn = 0; tn < 2; tn++) {
+      const int64_t col = n0 + 64 * wn + 32 * tn + r32;
+      if (col >= N) continue;
+#pragma unroll
+      for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const int lr = 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
+          const int64_t row = m0 + lr;
+          if (row < M) dst[row * ldd + col] = acc[tm][tn][i] / s_rf[lr];
+        }
+    }
+    return;
+  }
+  // Several K splits: each writes its partial tile to its slot, in register
+  // order (element e of thread tid at e * 512 + tid: every store a full line
+  // per wave); gemm_q4k_sp_sum_kernel adds the slots in split order.
+  const int tl = ct * mtiles + mt;  // the tile within its weight
+  float* __restrict__ mine = a.part + pick(a.part_off) + ((int64_t)tl * S + split) * (kBM * kBN);
+#pragma unroll
+  for (int tn = 0; tn < 2; tn++)
 #pragma unroll
     for (int tm = 0; tm < 2; tm++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const int lr = 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
-        const int64_t row = m0 + lr;
-        if (row < M) dst[row * ldd + col] = acc[tm][tn][i] / s_rf[lr];
+        mine[(32 * tn + 16 * tm + i) * kThreads + tid] = acc[tm][tn][i] / s_rf[lr];
       }
-  }
+}
+
+// dst of the split tiles: each thread adds 4 consecutive slot elements (4
+// neighbouring columns of one row) over the splits, in split order. Split
+// tile b of the launch is weight t's tile b - tile_base[t].
+constexpr int kSumThreads = 256;
+__global__ __launch_bounds__(kSumThreads) void gemm_q4k_sp_sum_kernel(const SpArgs a) {
+  const int64_t f = (int64_t)blockIdx.x * kSumThreads + threadIdx.x;  // a group of 4 elements
+  const int b = (int)(f >> 13);                                      // 8192 groups a tile
+  const int t = b < a.tile_base[1] ? 0 : b < a.tile_base[2] ? 1 : b < a.tile_base[3] ? 2 : 3;
+  auto pick = [&](const auto& arr) { return t == 0 ? arr[0] : t == 1 ? arr[1] : t == 2 ? arr[2] : arr[3]; };
+  const int S = pick(a.splits);
+  const int tl = b - pick(a.tile_base);
+  const int mt = tl % a.mtiles, ct = tl / a.mtiles;
+  const int64_t N = pick(a.n), ldd = pick(a.ldd), M = a.M;
+  const int o = 4 * (int)(f & 8191);  // element offset in the slot: e * 512 + tid
+  const float* __restrict__ base = a.part + pick(a.part_off) + (int64_t)tl * S * (kBM * kBN) + o;
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 sum = __builtin_nontemporal_load((const f4*)base);
+  for (int q = 1; q < S; q++) sum += __builtin_nontemporal_load((const f4*)(base + (int64_t)q * (kBM * kBN)));
+  // the slot position of element 0: e = o / 512, thread tid = o % 512 (the 4 share e, wave and h)
+  const int e = o >> 9, tid = o & 511, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv & 3, wn = wv >> 2, h = lane >> 5, r32 = lane & 31;
+  const int tn = e >> 5, tm = (e >> 4) & 1, i = e & 15;
+  const int64_t row = (int64_t)mt * kBM + 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
+  const int64_t col = (int64_t)ct * kBN + 64 * wn + 32 * tn + r32;
+  if (row >= M) return;
+  float* __restrict__ d = pick(a.dst) + row * ldd + col;
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    if (col + j < N) d[j] = sum[j];
 }
 
 }  // namespace
@@ -393,17 +479,98 @@ bool gemm_q4k_sp_fits(int64_t n, int64_t k, int64_t rows) {
          (rows + kBM) * k < ((int64_t)1 << 31) && rows < ((int64_t)1 << 24);
 }
 
+// K splits of one weight's product: while its tiles fill at most half the
+// CUs, the K range is cut in two (to 4), each part at least 4 super-blocks.
+// Chosen per weight, so a weight's result does not depend on the weights it
+// shares a launch with.
+int gemm_q4k_sp_splits(int64_t n, int64_t k, int64_t rows, int cus) {
+  const int64_t nsb = k / 256;
+  const int64_t tiles = ((rows + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
+  int S = 1;
+  while (S < 4 && tiles * S * 2 <= cus && nsb % (2 * S) == 0 && nsb / (2 * S) >= 4) S *= 2;
+  return S;
+}
+
+static size_t split_slot_bytes(int64_t n, int64_t rows, int S) {
+  return S > 1 ? (size_t)(((rows + kBM - 1) / kBM) * ((n + kBN - 1) / kBN)) * S * kBM * kBN * 4 : 0;
+}
+static size_t split_tiles(int64_t n, int64_t rows, int S) {
+  return S > 1 ? (size_t)(((rows + kBM - 1) / kBM) * ((n + kBN - 1) / kBN)) : 0;
+}
+
+size_t gemm_q4k_sp_split_bytes(const MvTargets& t, int64_t k, int64_t rows, int cus) {
+  size_t slots = 0, tiles = 0;
+  int64_t prev = 0;
+  for (int i = 0; i < t.count; i++) {
+    const int64_t n = t.row_end[i] - prev;
+    prev = t.row_end[i];
+    const int S = gemm_q4k_sp_splits(n, k, rows, cus);
+    slots += split_slot_bytes(n, rows, S);
+    tiles += split_tiles(n, rows, S);
+  }
+  (void)tiles;
+  return slots;
+}
+
+hipError_t launch_gemm_q4k_sp_targets(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, void* split_ws,
+                                      size_t split_bytes, int cus, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  if (t.count < 1 || t.count > kMaxTargets) return hipErrorInvalidValue;
+  const size_t need = gemm_q4k_sp_split_bytes(t, k, rows, cus);
+  const bool split = need > 0 && split_ws != nullptr && split_bytes >= need;
+  SpArgs a{};
+  a.yq = p.codes;
+  a.yd = p.d;
+  a.ybs = (const int16_t*)p.sums;
+  a.M = rows;
+  a.nsb = (int)(k / 256);
+  a.mtiles = (int)((rows + kBM - 1) / kBM);
+  int64_t units = 0, prev = 0, slot_floats = 0;
+  int tiles = 0;
+  for (int i = 0; i < kMaxTargets; i++) {
+    const int j = i < t.count ? i : t.count - 1;  // unused entries repeat the last weight, with no units
+    const int64_t n = t.row_end[j] - (j ? t.row_end[j - 1] : 0);
+    a.w[i] = t.w[j];
+    a.dst[i] = t.dst[j];
+    a.ldd[i] = t.ldd[j];
+    a.n[i] = n;
+    const int S = split ? gemm_q4k_sp_splits(n, k, rows, cus) : 1;
+    a.splits[i] = S;
+    a.tile_base[i] = tiles;
+    a.part_off[i] = slot_floats;
+    if (i < t.count) {
+      const int64_t wt = (int64_t)a.mtiles * ((n + kBN - 1) / kBN);
+      units += wt * S;
+      if (S > 1) {
+        tiles += (int)wt;
+        slot_floats += wt * S * kBM * kBN;
+      }
+    }
+    a.unit_end[i] = (int)units;
+    prev = t.row_end[j];
+  }
+  (void)prev;
+  if (units >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  a.remap = units % 8 == 0 ? 1 : 0;
+  a.part = tiles > 0 ? (float*)split_ws : nullptr;
+  gemm_q4k_sp_kernel<<<dim3((unsigned)units), kThreads, 0, st>>>(a);
+  if (tiles > 0) {
+    // unused entries past the last weight start at the end (no workgroups)
+    for (int i = t.count; i < kMaxTargets; i++) a.tile_base[i] = tiles;
+    gemm_q4k_sp_sum_kernel<<<dim3((unsigned)(tiles * (kBM * kBN / 4 / kSumThreads))), kSumThreads, 0, st>>>(a);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_q4k_sp(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
                               int64_t ldd, hipStream_t st) {
-  QMM_NOTE_LAUNCH();
-  const int mt = (int)((rows + kBM - 1) / kBM);
-  const int64_t nt = (n + kBN - 1) / kBN;
-  const int64_t total = nt * mt;
-  if (total >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
-  const int remap = total % 8 == 0 ? 1 : 0;
-  gemm_q4k_sp_kernel<<<dim3((unsigned)total), kThreads, 0, st>>>((const uint8_t*)w, n, (int)(k / 256), p.codes, p.d,
-                                                                 (const int16_t*)p.sums, rows, dst, ldd, mt, remap);
-  return hipGetLastError();
+  MvTargets t{};
+  t.w[0] = w;
+  t.dst[0] = dst;
+  t.ldd[0] = ldd;
+  t.row_end[0] = n;
+  t.count = 1;
+  return launch_gemm_q4k_sp_targets(t, k, p, rows, nullptr, 0, 256, st);
 }
 
 }  // namespace qmm

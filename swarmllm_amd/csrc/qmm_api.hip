@@ -225,6 +225,23 @@ hipError_t launch_gemm(int type, const void* w, int64_t n, int64_t k, const qmm:
   return qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st);
 }
 
+// Products the single-pass Q4_K GEMM takes: those it can cut along K and
+// launch several of at once (launch_gemm_q4k_sp_targets).
+bool sp_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows, hipStream_t st) {
+  return type == qmm::T_Q4_K && gemm_takes(type, w, xq, n, k, rows, st) && rows >= qmm::gemm_q4k_sp_min_rows() &&
+         qmm::gemm_q4k_sp_fits(n, k, rows);
+}
+
+qmm::MvTargets one_target(const void* w, int64_t n, float* dst, int64_t ldd) {
+  qmm::MvTargets t{};
+  t.w[0] = w;
+  t.dst[0] = dst;
+  t.ldd[0] = ldd;
+  t.row_end[0] = n;
+  t.count = 1;
+  return t;
+}
+
 // The streaming decode kernels (Q4_K, Q6_K at 1-2 activation rows).
 bool stream_supported(int type, int64_t k, int64_t rows) {
   if (qmm::mv_b32_rows_supported(type, k, rows)) return true;
@@ -428,12 +445,18 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   if (!shape_ok(type, k, n, rows) || need == nullptr || ldd < n || x_stride < k) return QMM_UNSUPPORTED;
   const int layout = qmm_act_layout(type, rows);
   const size_t bytes = qmm::act_bytes(layout, k, rows);
-  *need = bytes;
+  const hipStream_t st = (hipStream_t)stream;
+  // a single-pass GEMM that leaves CUs idle is cut along K when the
+  // workspace also holds its split slots (need reports them; with only the
+  // activation's bytes it runs uncut)
+  const size_t split = sp_takes(type, w, workspace, n, k, rows, st)
+                           ? qmm::gemm_q4k_sp_split_bytes(one_target(w, n, dst, ldd), k, rows, (int)cu_count())
+                           : 0;
+  *need = split ? qmm::align_up(bytes, 256) + split : bytes;
   if (!launch) return QMM_OK;
   if (g_fail_next.exchange(false)) return QMM_NO_ROOM;
   if (workspace_bytes < bytes || workspace == nullptr) return QMM_WORKSPACE_TOO_SMALL;
   if (!w || !x || !dst) return QMM_UNSUPPORTED;
-  const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
   if (g_force_dmmv.load(std::memory_order_relaxed))
     return status_of(qmm::launch_dmmv(type, w, n, k, x, x_stride, rows, dst, ldd, st));
@@ -448,6 +471,16 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   if (qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st) != hipSuccess)
     return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
+  if (sp_takes(type, w, workspace, n, k, rows, st)) {
+    const size_t off = qmm::align_up(bytes, 256);
+    void* sws = workspace_bytes > off ? (char*)workspace + off : nullptr;
+    if (qmm::launch_gemm_q4k_sp_targets(one_target(w, n, dst, ldd), k, p, rows, sws,
+                                        workspace_bytes > off ? workspace_bytes - off : 0, (int)cu_count(),
+                                        st) != hipSuccess)
+      return QMM_DEVICE_ERROR;
+    g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+    return QMM_OK;
+  }
   return launch_product(type, w, n, k, workspace, p, layout, rows, dst, ldd, st);
 }
 
@@ -459,13 +492,36 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
     if (!shape_ok(type, k, n[i], rows) || ldd[i] < n[i]) return QMM_UNSUPPORTED;
   const int layout = qmm_act_layout(type, rows);
   const size_t bytes = qmm::act_bytes(layout, k, rows);
-  *need = bytes;
+  const hipStream_t st = (hipStream_t)stream;
+  // the single-pass GEMM's products go kMaxTargets to a launch; their split
+  // slots follow the activation (one launch's worth, reused launch after launch)
+  size_t split = 0;
+  {
+    qmm::MvTargets g{};
+    int64_t end = 0;
+    for (int i = 0; i <= count; i++) {
+      if (i < count && sp_takes(type, w[i], workspace, n[i], k, rows, st)) {
+        g.w[g.count] = w[i];
+        g.dst[g.count] = dst[i];
+        g.ldd[g.count] = ldd[i];
+        end += n[i];
+        g.row_end[g.count] = end;
+        g.count++;
+      }
+      if (g.count == qmm::kMaxTargets || (i == count && g.count > 0)) {
+        const size_t b = qmm::gemm_q4k_sp_split_bytes(g, k, rows, (int)cu_count());
+        split = b > split ? b : split;
+        g = qmm::MvTargets{};
+        end = 0;
+      }
+    }
+  }
+  *need = split ? qmm::align_up(bytes, 256) + split : bytes;
   if (!launch) return QMM_OK;
   if (g_fail_next.exchange(false)) return QMM_NO_ROOM;
   if (!x) return QMM_UNSUPPORTED;
   for (int i = 0; i < count; i++)
     if (!w[i] || !dst[i]) return QMM_UNSUPPORTED;
-  const hipStream_t st = (hipStream_t)stream;
   clear_stale_error();
   if (g_force_dmmv.load(std::memory_order_relaxed)) {
     for (int i = 0; i < count; i++)
@@ -491,9 +547,10 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
   if (qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st) != hipSuccess)
     return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
-  // the weights the skinny kernel takes share its launches (kMaxTargets each)
-  qmm::MvTargets grp{};
-  int64_t end = 0;
+  // the weights the skinny kernel takes share its launches (kMaxTargets
+  // each), and so do those the single-pass GEMM takes
+  qmm::MvTargets grp{}, spg{};
+  int64_t end = 0, spend = 0;
   auto flush = [&]() -> int {
     if (grp.count == 0) return QMM_OK;
     if (launch_skinny(type, grp, k, p, rows, st) != hipSuccess) return QMM_DEVICE_ERROR;
@@ -502,7 +559,28 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
     end = 0;
     return QMM_OK;
   };
+  const size_t off = qmm::align_up(bytes, 256);
+  void* sws = workspace_bytes > off ? (char*)workspace + off : nullptr;
+  const size_t sbytes = workspace_bytes > off ? workspace_bytes - off : 0;
+  auto flush_sp = [&]() -> int {
+    if (spg.count == 0) return QMM_OK;
+    if (qmm::launch_gemm_q4k_sp_targets(spg, k, p, rows, sws, sbytes, (int)cu_count(), st) != hipSuccess)
+      return QMM_DEVICE_ERROR;
+    g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
+    spg = qmm::MvTargets{};
+    spend = 0;
+    return QMM_OK;
+  };
   for (int i = 0; i < count; i++) {
+    if (sp_takes(type, w[i], workspace, n[i], k, rows, st)) {
+      spg.w[spg.count] = w[i];
+      spg.dst[spg.count] = dst[i];
+      spg.ldd[spg.count] = ldd[i];
+      spend += n[i];
+      spg.row_end[spg.count] = spend;
+      if (++spg.count == qmm::kMaxTargets && flush_sp() != QMM_OK) return QMM_DEVICE_ERROR;
+      continue;
+    }
     if (!gemm_takes(type, w[i], workspace, n[i], k, rows, st) &&
         skinny_takes(type, w[i], workspace, n[i], k, rows, st)) {
       grp.w[grp.count] = w[i];
@@ -516,6 +594,7 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
     const int r = launch_product(type, w[i], n[i], k, workspace, p, layout, rows, dst[i], ldd[i], st);
     if (r != QMM_OK) return r;
   }
+  if (flush_sp() != QMM_OK) return QMM_DEVICE_ERROR;
   return flush();
 }
 

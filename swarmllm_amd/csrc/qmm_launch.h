@@ -180,6 +180,16 @@ int gemm_q4k_sp_min_rows();
 bool gemm_q4k_sp_fits(int64_t n, int64_t k, int64_t rows);
 hipError_t launch_gemm_q4k_sp(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
                               int64_t ldd, hipStream_t s);
+// K splits for one weight's product (1, 2 or 4), the workspace the splits of
+// a launch over `t` need (0: none split), and the launch itself: up to
+// kMaxTargets weights sharing one activation in one launch; with split_ws of
+// at least gemm_q4k_sp_split_bytes bytes the products that leave CUs idle are
+// cut along K (their results the same whatever weights share the launch),
+// otherwise none is.
+int gemm_q4k_sp_splits(int64_t n, int64_t k, int64_t rows, int cus);
+size_t gemm_q4k_sp_split_bytes(const MvTargets& t, int64_t k, int64_t rows, int cus);
+hipError_t launch_gemm_q4k_sp_targets(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, void* split_ws,
+                                      size_t split_bytes, int cus, hipStream_t st);
 
 int gemm_q4k_min_rows();
 // The GEMM indexes with 32-bit byte offsets: the weight below 2 GiB and

@@ -61,7 +61,10 @@ int qmm_forward_noalloc(int type, const void* w, const float* x, int64_t x_strid
   size_t need = 0;
   const int plan = qmm_forward(type, w, x, x_stride, dst, ldd, nullptr, 0, &need, k, n, rows, 0, stream);
   if (plan != QMM_OK) return plan;
-  if (need > kScratchBytes) return QMM_WORKSPACE_TOO_SMALL;  // beyond the static scratch: nothing enqueued
+  // `need` may count a GEMM's K-split slots, which it goes without when the
+  // scratch holds only the quantized activation
+  const size_t least = qmm_act_bytes(qmm_act_layout(type, rows), k, rows);
+  if (need > kScratchBytes && least > kScratchBytes) return QMM_WORKSPACE_TOO_SMALL;  // nothing enqueued
   void* ws = scratch_on_current_device();
   if (ws == nullptr) return QMM_DEVICE_ERROR;
   return qmm_forward(type, w, x, x_stride, dst, ldd, ws, kScratchBytes, &need, k, n, rows, 1, stream);

@@ -171,6 +171,90 @@ def test_q4k_gemm_through_forward_shared():
         assert torch.equal(y, m.forward(x))
 
 
+def plan_bytes(qt, k, n, rows):
+    import ctypes
+
+    need = ctypes.c_size_t(0)
+    assert lib().qmm_forward(qref.Q4_K, None, None, k, None, n, None, 0, ctypes.byref(need), k, n, rows, 0, 0) == 0
+    return need.value
+
+
+@pytest.mark.parametrize("n,rows", [(1024, 512), (4096, 512), (200, 300)])
+def test_q4k_gemm_cut_along_k(n, rows):
+    """Products whose tiles fill at most half the CUs (q/k/v/o of a prefill)
+    are cut along K when the workspace holds the split slots (forward plans
+    them): each part writes its partial tile to a slot and the last part to
+    finish adds the slots in part order. Against the oracle; bit-identical
+    run to run; within 1e-5 of the uncut product from the same quantized
+    activation (qmm_matmul: the same integers and f32 steps, only the order
+    of the partial sums differs)."""
+    from swarmllm_amd import _lib
+    from swarmllm_amd.qtensor import quantize_act
+
+    k = 4096
+    rng = np.random.default_rng(zlib.crc32(f"gemm-split-{n}-{rows}".encode()))
+    w = weights(rng, n, k)
+    x = activations(rng, rows, k, outliers=True)
+    qt, wq = q4k(w)
+    L = lib()
+    assert plan_bytes(qt, k, n, rows) > L.qmm_act_bytes(_lib.ACT_Q8K, k, rows), "no split slots planned"
+    mm = QMatMul(qt)
+    xt = upload(x)
+    y1 = mm.forward(xt).clone()
+    assert "gemm_q4k_sp" in L.qmm_last_kernel().decode()
+    y2 = mm.forward(xt)
+    assert torch.equal(y1, y2)
+    xq = quantize_act(xt, _lib.ACT_Q8K)
+    uncut = torch.empty((rows, n), dtype=torch.float32, device=DEV)
+    assert L.qmm_matmul(qref.Q4_K, qt.data_.data_ptr(), xq.data_ptr(), uncut.data_ptr(), n, k, n, rows,
+                        torch.cuda.current_stream().cuda_stream) == 0
+    wdeq = qref.to_float(qref.Q4_K, wq, n * k).reshape(n, k)
+    y = y1.cpu().numpy()
+    assert normalised_error(y, uncut.cpu().numpy(), wdeq, x) <= 1e-5
+    want = qref.matmul(qref.Q4_K, x, wq, n)
+    err = normalised_error(y, want, wdeq, x)
+    assert err <= TOL_GEMM
+    assert err <= TIGHT_SP, err
+
+
+def test_q4k_gemm_cut_along_k_shared_equals_forward():
+    """q, k and v of a prefill (4096 + 1024 + 1024 weight rows, M = 512) in
+    one launch give each weight's own forward bits: a weight's K split does
+    not depend on the weights sharing its launch."""
+    k, rows = 4096, 512
+    rng = np.random.default_rng(15)
+    mats = [QMatMul(q4k(weights(rng, n, k))[0]) for n in (4096, 1024, 1024)]
+    x = upload(activations(rng, rows, k, outliers=True))
+    before = lib().qmm_gemm_launches()
+    shared = QMatMul.forward_shared(x, mats)
+    assert lib().qmm_gemm_launches() == before + 1, "q/k/v did not share one launch"
+    for m, y in zip(mats, shared):
+        assert torch.equal(y, m.forward(x))
+
+
+def test_q4k_gemm_uncut_with_only_the_activation_workspace():
+    """qmm_forward_noalloc's 16 MiB scratch holds the activation of an
+    o-shaped product at M = 512 but not its split slots: the product runs
+    uncut, with qmm_matmul's bits."""
+    from swarmllm_amd import _lib
+    from swarmllm_amd.qtensor import quantize_act
+
+    n, k, rows = 4096, 4096, 512
+    rng = np.random.default_rng(16)
+    qt, _ = q4k(weights(rng, n, k))
+    L = lib()
+    assert plan_bytes(qt, k, n, rows) > L.qmm_forward_noalloc_max_bytes()
+    x = upload(activations(rng, rows, k))
+    st = torch.cuda.current_stream().cuda_stream
+    out = torch.empty((rows, n), dtype=torch.float32, device=DEV)
+    assert L.qmm_forward_noalloc(qref.Q4_K, qt.data_.data_ptr(), x.data_ptr(), k, out.data_ptr(), n, k, n, rows,
+                                 st) == 0
+    xq = quantize_act(x, _lib.ACT_Q8K)
+    uncut = torch.empty((rows, n), dtype=torch.float32, device=DEV)
+    assert L.qmm_matmul(qref.Q4_K, qt.data_.data_ptr(), xq.data_ptr(), uncut.data_ptr(), n, k, n, rows, st) == 0
+    assert torch.equal(out, uncut)
+
+
 @pytest.mark.parametrize("rows", [1, 2, 5, 8, 9, 40])
 def test_matmul_from_a_quantized_activation_equals_forward(rows):
     """qmm_matmul (the product from qmm_quantize_act's planes, the
