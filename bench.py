@@ -376,8 +376,31 @@ def prefill_gemm(layers, stream, reps: int, name: str = "gate") -> dict:
     ops = 2.0 * M * n * k
     tops = ops / (us * 1e-6) / 1e12
     tname = "Q4_K" if t == Q4K else "Q6_K"
+    # the same product as the layer runs it: qmm_forward with its planned
+    # workspace (quantizer + GEMM, cut along K when its tiles leave CUs idle)
+    import torch
+
+    from swarmllm_amd import fill_normal
+
+    x = fill_normal(M * k, seed=(3 << 40) | 0xB1).reshape(M, k)
+    need = ctypes.c_size_t(0)
+    check("qmm_forward", L.qmm_forward(t, None, None, k, None, n, None, 0, ctypes.byref(need), k, n, M, 0, 0))
+    ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device="cuda")
+
+    def fwd(st):
+        for lay in layers:
+            check("qmm_forward", L.qmm_forward(t, lay.w[name].data_.data_ptr(), x.data_ptr(), k, out.data_ptr(), n,
+                                               ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, M, 1, st))
+
+    g2 = capture(fwd, stream)
+    fkernel = L.qmm_last_kernel().decode()
+    settle(g2.replay, stream)
+    fus = time_gpu(lambda: [g2.replay() for _ in range(reps)], stream) * 1e3 / (reps * len(layers))
     return {"workload": f"C3: {tname} {name} {n}x{k} at M=512, int8 MFMA GEMM (activation quantized once, Q8_K)",
             "us_per_launch": round(us, 3), "ops_per_launch": int(ops), "tops": round(tops, 2),
+            "forward": {"us": round(fus, 3), "tops": round(ops / (fus * 1e-6) / 1e12, 2), "kernel": fkernel,
+                        "what": "qmm_forward with its planned workspace: activation quantizer + GEMM (cut along K "
+                                "when its tiles leave CUs idle), as the C3 layer runs the product"},
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": 5000.0, "unit": "TOP/s",
                          "frac": round(tops / 5000.0, 4), "kernel": kernel,
                          "traffic": measured_traffic("prefill_gemm" if name == "gate" else f"prefill_{name}")}}
@@ -1033,9 +1056,11 @@ def main() -> int:
     log(f"gate+up+GLU launch: {gl['us_per_launch']:.3f} us/launch, {gl['gbs']:.1f} GB/s")
 
     pre = prefill_gemm(layers, stream, max(2, args.kernel_reps // 5))
-    log(f"prefill GEMM (gate): {pre['us_per_launch']:.2f} us/launch, {pre['tops']:.1f} TOP/s")
+    log(f"prefill GEMM (gate): {pre['us_per_launch']:.2f} us/launch, {pre['tops']:.1f} TOP/s; "
+        f"through qmm_forward {pre['forward']['us']:.2f} us")
     pre_down = prefill_gemm(layers, stream, max(2, args.kernel_reps // 5), name="down")
-    log(f"prefill GEMM (down): {pre_down['us_per_launch']:.2f} us/launch, {pre_down['tops']:.1f} TOP/s")
+    log(f"prefill GEMM (down): {pre_down['us_per_launch']:.2f} us/launch, {pre_down['tops']:.1f} TOP/s; "
+        f"through qmm_forward {pre_down['forward']['us']:.2f} us")
     pre_layer = prefill_layer(layers, stream, max(2, args.kernel_reps // 10))
     log(f"prefill layer: {pre_layer['us_per_layer']:.2f} us/layer, {pre_layer['tops']:.1f} TOP/s")
 

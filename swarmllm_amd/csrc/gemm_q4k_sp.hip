@@ -81,6 +81,24 @@ __device__ __forceinline__ uint32_t word(const uint4& c, int e) {
 // (rows r0 .. r0+15, one piece each) cover the 64 LDS banks once.
 __device__ __forceinline__ uint32_t swz(uint32_t r) { return (r >> 1) & 7u; }
 
+// LDS access by byte address. The kernel keeps per-lane byte offsets that it
+// makes opaque once a stage (`opaque`), so the compiler forms each address
+// as offset + the buffer's constant address (an instruction immediate)
+// instead of keeping one precomputed address per buffer and K-step live.
+typedef int lds_i4 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ T lds_ld(uint32_t a) { return *(const __attribute__((address_space(3))) T*)(uintptr_t)a; }
+template <typename T>
+__device__ __forceinline__ void lds_st(uint32_t a, const T& v) { *(__attribute__((address_space(3))) T*)(uintptr_t)a = v; }
+__device__ __forceinline__ uint4 lds_ld4(uint32_t a) {
+  const lds_i4 v = lds_ld<lds_i4>(a);
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+__device__ __forceinline__ void lds_st4(uint32_t a, const uint4& v) {
+  lds_st<lds_i4>(a, lds_i4{(int)v.x, (int)v.y, (int)v.z, (int)v.w});
+}
+__device__ __forceinline__ void opaque(uint32_t& v) { asm volatile("" : "+v"(v)); }
+
 // 2^-e with |v| in [2^(e-1), 2^e) for the largest |v| of a row: the factor
 // that brings the row's scales into [0.5, 1); 1 for a zero or non-finite row.
 __device__ __forceinline__ float row_factor(float maxabs) {
@@ -109,21 +127,88 @@ struct SpArgs {
   int nsb, mtiles, remap;
 };
 
-__global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a) {
+// The raw bytes of one weight row's super-block in LDS: Q4_K's 144-byte
+// blocks (9 aligned pieces), Q6_K's 210-byte blocks as the 14 aligned
+// 16-byte pieces around them (rows 16-byte aligned: k a multiple of 2048).
+template <int FMT>
+struct SpFmt {
+  static constexpr bool kQ6 = FMT == T_Q6_K;
+  static constexpr int kBlock = kQ6 ? 210 : 144;  // bytes of a super-block
+  static constexpr int kRaw = kQ6 ? 224 : 144;    // LDS bytes of a row's super-block
+  static constexpr int kPieces = kRaw / 16;       // 16-byte copies a row
+  static constexpr int kCopies = kBN * kPieces / 64;  // 64-lane copies a super-block: 18 / 28
+  static constexpr int kWaveCopies = (kCopies + 7) / 8;  // a wave's share: 3 / 4
+};
+// Q6_K's weight enters as w8 = round(m_j (q - 32) / 256) with the integer
+// multiplier m_j = round(127 sc_j / 16): |m_j (q - 32)| <= 1016 * 32 fits the
+// 16-bit lanes for every int8 sc_j (-128 included), and the super-block's
+// scale becomes d * 256 * 16 / 127.
+constexpr float kQ6Eff = 4096.0f / 127.0f;
+
+// One thread's 32 values of a Q6_K stage (half `half` of super-block sbx,
+// positions 32 g .. 32 g + 31, the layout of BlockQ6K::to_float,
+// vendor/candle/candle-core/src/quantized/k_quants.rs:2657-2727): 6-bit codes
+// from ql (low or high nibble) and qh (bits 2g, 2g + 1), the multipliers of
+// their two 16-value sub-blocks, into int8 pieces 2g and 2g + 1 of the row.
+// wr: the row's window in LDS (the block at byte (2 sbx) mod 16 of it).
+__device__ __forceinline__ void build_q6(uint32_t wr, int half, uint32_t w0, uint32_t w1, int sbx, int g) {
+  const uint32_t boff = (2u * (uint32_t)sbx) & 15u;
+  const uint32_t al = boff & 3u;  // 0 or 2: the blocks sit 2-byte aligned in their windows
+  const uint32_t wb = wr + (boff & 12u);  // the dword holding the block's first byte
+  const uint32_t ql4 = wb + 64u * (uint32_t)half + 32u * ((uint32_t)g & 1u);
+  const uint32_t qh4 = wb + 128u + 32u * (uint32_t)half;
+  // sub-block scales 8 half + 2g and the next: bytes o and o + 1 past the
+  // scales' first dword (o even and at most 8, so both in the dword at o & ~3)
+  const uint32_t o = al + 2u * (uint32_t)g;
+  const uint32_t scw = lds_ld<uint32_t>(wb + 192u + 8u * (uint32_t)half + (o & ~3u)) >> (8u * (o & 3u));
+  const int sc0 = (int)(int8_t)(scw & 0xFFu), sc1 = (int)(int8_t)((scw >> 8) & 0xFFu);
+  const int m0 = (127 * sc0 + 8) >> 4, m1 = (127 * sc1 + 8) >> 4;  // round(127 sc / 16)
+  const uint32_t hs = 2u * (uint32_t)g;
+  // the two 16-value sub-blocks in turn (5 dwords of ql and qh each)
+#pragma unroll
+  for (int part = 0; part < 2; part++) {
+    const int m = part ? m1 : m0;
+    // per 16-bit lane: m (q - 32) + 128, whose high byte is w8
+    const uint32_t M = ((uint32_t)m & 0xFFFFu) * 0x10001u, C = ((uint32_t)(128 - 32 * m) & 0xFFFFu) * 0x10001u;
+    uint32_t ql[5], qh[5], out[4];
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+      ql[i] = lds_ld<uint32_t>(ql4 + 16u * (uint32_t)part + 4u * (uint32_t)i);
+      qh[i] = lds_ld<uint32_t>(qh4 + 16u * (uint32_t)part + 4u * (uint32_t)i);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t lw = __builtin_amdgcn_alignbyte(ql[i + 1], ql[i], al);
+      const uint32_t hw = __builtin_amdgcn_alignbyte(qh[i + 1], qh[i], al);
+      const uint32_t qlv = g < 2 ? (lw & 0x0F0F0F0Fu) : ((lw >> 4) & 0x0F0F0F0Fu);
+      const uint32_t q = qlv | (((hw >> hs) & 0x03030303u) << 4);
+      const uint32_t e = pkmad(q & 0x00FF00FFu, M, C), od = pkmad((q >> 8) & 0x00FF00FFu, M, C);
+      out[i] = __builtin_amdgcn_perm(od, e, 0x07030501u);
+    }
+    lds_st<lds_i4>(part ? w1 : w0, lds_i4{(int)out[0], (int)out[1], (int)out[2], (int)out[3]});
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a) {
+  using F = SpFmt<FMT>;
+  constexpr bool Q6 = F::kQ6;
   // Each half of each double buffer is its own object and the stage loop is
   // unrolled over two super-blocks, so every access names its buffer
   // statically (the compiler can tell reads of one half from writes of the other).
   __shared__ __attribute__((aligned(16))) int8_t s_a0[kBM * kStage], s_a1[kBM * kStage];
   __shared__ __attribute__((aligned(16))) int8_t s_b0[kBN * kStage], s_b1[kBN * kStage];
-  __shared__ __attribute__((aligned(16))) uint8_t s_w0[kBN * 144], s_w1[kBN * 144];
-  __shared__ __attribute__((aligned(16))) _Float16 s_rop[kBM][16];  // f16 product A operands of a super-block
-  __shared__ __attribute__((aligned(16))) _Float16 s_cop[kBN][16];  // and B operands
-  __shared__ __attribute__((aligned(16))) float s_dy[kBM];          // dy_m 2^-e_m
-  __shared__ __attribute__((aligned(16))) float s_d4[kBN];          // 4 d_n
+  __shared__ __attribute__((aligned(16))) uint8_t s_w0[kBN * F::kRaw], s_w1[kBN * F::kRaw];
+  // Q4_K: the f16 product's operands of a super-block (Q6_K forms its
+  // operands from s_dy and s_d4 in registers)
+  __shared__ __attribute__((aligned(16))) _Float16 s_rop[Q6 ? 1 : kBM][16];
+  __shared__ __attribute__((aligned(16))) _Float16 s_cop[Q6 ? 1 : kBN][16];
+  __shared__ __attribute__((aligned(16))) float s_dy[kBM];          // Q4_K dy_m 2^-e_m; Q6_K its f16 value
+  __shared__ __attribute__((aligned(16))) float s_d4[kBN];          // Q4_K 4 d_n; Q6_K dq_n (f16 value)
   __shared__ __attribute__((aligned(16))) float s_rf[kBM];          // 2^-e_m
   // a super-block's activation sums (bsums) and scales, copied one stage
   // ahead of the stage that turns them into the f16 operands
-  __shared__ __attribute__((aligned(16))) int16_t s_bsr[kBM * 16];
+  __shared__ __attribute__((aligned(16))) int16_t s_bsr[Q6 ? 8 : kBM * 16];
   __shared__ __attribute__((aligned(16))) float s_ydr[kBM];
 
   const int tid = threadIdx.x;
@@ -162,7 +247,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
   const int sb0 = split * nsb / S, sb1 = (split + 1) * nsb / S;
 
   const int64_t K = (int64_t)nsb * 256;
-  const uint32_t rowbytes = (uint32_t)nsb * 144;
+  const uint32_t rowbytes = (uint32_t)nsb * F::kBlock;
 
   // ---- per-lane byte offsets of the copies (stage 0 / super-block 0) ----
   // activation: 32 copies a stage, 8 rows each; wave wv takes copies wv + 8u
@@ -176,16 +261,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
     const uint32_t rk = a_rowk + (uint32_t)(64 * u) * (uint32_t)K;
     return (rk < a_lastk ? rk : a_lastk) + a_piece;
   };
-  // weights: 18 copies a super-block (128 rows x 9 pieces), copy i = wv + 8u
-  uint32_t woff[3];
-#pragma unroll
-  for (int u = 0; u < 3; u++) {
+  // weights: F::kCopies copies a super-block (128 rows x F::kPieces pieces),
+  // copy i = wv + 8u; Q6_K's copies past the last repeat it (same LDS bytes)
+  auto woff_of = [&](int u, uint32_t ln) -> uint32_t {
     const uint32_t i = (uint32_t)(wv + 8 * u);
-    const uint32_t f = 64u * (i < 18u ? i : 17u) + (uint32_t)lane;
-    const uint32_t col = (f * 7282u) >> 16;  // f / 9 for f < 2^14
+    const uint32_t f = 64u * (i < (uint32_t)F::kCopies ? i : (uint32_t)F::kCopies - 1u) + ln;
+    const uint32_t col = f / (uint32_t)F::kPieces;
     const int64_t gc = n0 + col < N ? n0 + col : N - 1;
-    woff[u] = (uint32_t)gc * rowbytes + 16u * (f - 9u * col);
-  }
+    return (uint32_t)gc * rowbytes + 16u * (f - (uint32_t)F::kPieces * col);
+  };
+  // Q4_K keeps its three offsets; Q6_K forms its four at each use (from a
+  // lane value the compiler cannot hoist), which keeps them out of registers
+  uint32_t woff[F::kWaveCopies];
+#pragma unroll
+  for (int u = 0; u < F::kWaveCopies; u++) woff[u] = Q6 ? 0u : woff_of(u, (uint32_t)lane);
   // the per-super-block row inputs: bsums (32 bytes a row, 8 copies, one a
   // wave) and dy (4 bytes a row, 4 dword copies, waves 0-3)
   const uint32_t bsr = 32u * (uint32_t)wv + ((uint32_t)lane >> 1);
@@ -198,9 +287,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
     dma16(yq + 128 * (int64_t)g, aoff(u), lds_addr(sa + 1024 * (wv + 8 * u)));
   };
   auto dma_w1 = [&](int sb, uint8_t* sw, int u) {
-    if (wv + 8 * u < 18) dma16(W + 144 * (int64_t)sb, woff[u], lds_addr(sw + 1024 * (wv + 8 * u)));
+    if constexpr (Q6) {
+      const int i = wv + 8 * u < F::kCopies ? wv + 8 * u : F::kCopies - 1;
+      uint32_t ln = (uint32_t)lane;
+      asm volatile("" : "+v"(ln));
+      dma16(W + 16 * ((210 * (int64_t)sb) >> 4), woff_of(u, ln), lds_addr(sw + 1024 * i));
+    } else if (wv + 8 * u < F::kCopies) {
+      dma16(W + 144 * (int64_t)sb, woff[u], lds_addr(sw + 1024 * (wv + 8 * u)));
+    }
   };
   auto dma_rows = [&](int sb, int part) {
+    if (Q6 && part == 0) return;  // Q6_K has no min term: no code sums
     if (part == 0)
       dma16((const uint8_t*)ybs + 32 * (int64_t)sb, bsoff, lds_addr((uint8_t*)s_bsr + 1024 * wv));
     else if (wv < 4)
@@ -209,10 +306,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
 
   // ---- expansion of a stage's weights: thread -> (weight row, piece) ----
   const int bn = tid & (kBN - 1), bpi = tid >> 7;  // 16 consecutive lanes: 16 rows, one piece
-  auto build = [&](const uint8_t* sw, int half, int8_t* sbt) {
-    const uint8_t* wr = sw + bn * 144;
-    const uint4 hdr = *(const uint4*)wr;
-    const uint4 raw = *(const uint4*)(wr + 16 * (1 + 4 * half + bpi));
+  // lane offsets of the expansion (made opaque once a stage): the raw row,
+  // and the two 16-byte pieces it writes in the expanded row
+  const uint32_t plo = Q6 ? 2u * (uint32_t)(wv >> 1) : 4u * ((uint32_t)bpi >> 1) + ((uint32_t)bpi & 1u);
+  uint32_t x_raw = (uint32_t)bn * F::kRaw;
+  uint32_t x_w0 = (uint32_t)bn * kStage + 16u * (plo ^ swz(bn));
+  uint32_t x_w1 = (uint32_t)bn * kStage + 16u * ((plo + (Q6 ? 1u : 2u)) ^ swz(bn));
+  auto build = [&](const uint8_t* sw, int half, int8_t* sbt, int sbx) {
+    const uint32_t wr = lds_addr(sw) + x_raw, bt = lds_addr(sbt);
+    if constexpr (Q6) {
+      build_q6(wr, half, bt + x_w0, bt + x_w1, sbx, wv >> 1);
+      return;
+    }
+    const uint4 hdr = lds_ld4(wr);
+    const uint4 raw = lds_ld4(wr + 16u * (uint32_t)(1 + 4 * half + bpi));
     // 6-bit scales of sub-blocks 4 half + 2 (bpi >> 1) and the next
     // (get_scale_min_k4, vendor/candle/candle-core/src/quantized/utils.rs:50-60)
     const uint32_t scw = half == 0 ? (hdr.y & 0x3f3f3f3fu)
@@ -233,15 +340,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
       lo[e] = __builtin_amdgcn_perm(ol, el, 0x07030501u);
       hi[e] = __builtin_amdgcn_perm(oh, eh, 0x07030501u);
     }
-    const uint32_t plo = 4u * ((uint32_t)bpi >> 1) + ((uint32_t)bpi & 1u);
-    int8_t* rowp = sbt + bn * kStage;
-    *(uint4*)(rowp + 16 * (plo ^ swz(bn))) = olo;
-    *(uint4*)(rowp + 16 * ((plo + 2u) ^ swz(bn))) = ohi;
+    lds_st4(bt + x_w0, olo);
+    lds_st4(bt + x_w1, ohi);
   };
 
   // ---- per-super-block scales: rows (threads 0-255), weight rows (256-383) ----
   const int64_t prow = m0 + (tid & 255) < M ? m0 + (tid & 255) : M - 1;
-  auto prep = [&](const uint8_t* sw) {
+  auto prep = [&](const uint8_t* sw, int sbp) {
+    if constexpr (Q6) {
+      // rows: dy in f16 (row factor 2^-e / 2: at most 0.5, so dy 2^16 fits
+      // f16); weight rows: dq = f16(d * 256 * 16 / 127 * 2^7)
+      uint32_t t4 = 4u * (uint32_t)tid;  // opaque: the addresses are formed here, not kept live
+      opaque(t4);
+      if (tid < 256) {
+        const float y = lds_ld<float>(lds_addr(s_ydr) + t4) * lds_ld<float>(lds_addr(s_rf) + t4);
+        lds_st<float>(lds_addr(s_dy) + t4, (float)(_Float16)(y * 0.5f));
+      } else if (tid < 256 + kBN) {
+        const uint32_t n4 = t4 - 1024u;
+        const uint16_t dh = lds_ld<uint16_t>(lds_addr(sw) + (n4 >> 2) * F::kRaw + ((2u * (uint32_t)sbp) & 15u) + 208u);
+        lds_st<float>(lds_addr(s_d4) + n4, (float)(_Float16)(h2f(dh) * (kQ6Eff * 128.0f)));
+      }
+      return;
+    }
     if (tid < 256) {
       const float dy = s_ydr[tid] * s_rf[tid];
       const uint4 pbs0 = *(const uint4*)&s_bsr[16 * tid], pbs1 = *(const uint4*)&s_bsr[16 * tid + 8];
@@ -299,15 +419,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
   // the lane's operand rows within the staged tiles
   const int arow0 = 64 * wm + r32, arow1 = arow0 + 32;
   const int bcol0 = 64 * wn + r32, bcol1 = bcol0 + 32;
-  auto frag = [&](const int8_t* base, int row, int ks) -> i4v {
-    return *(const i4v*)(base + row * kStage + 16 * ((uint32_t)(2 * ks + h) ^ swz(row)));
+  // fragment lane offsets for K-step ks (rows 32 apart share a swizzle, and
+  // the A and B rows of a lane share it too)
+  uint32_t fa[4], fb[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++) {
+    const uint32_t pc = 16u * ((uint32_t)(2 * ks + h) ^ swz((uint32_t)r32));
+    fa[ks] = (uint32_t)arow0 * kStage + pc;
+    fb[ks] = (uint32_t)bcol0 * kStage + pc;
+  }
+  auto frag = [&](const int8_t* base, int t2, int ks, bool a_side) -> i4v {
+    return lds_ld<i4v>(lds_addr(base) + (a_side ? fa[ks] : fb[ks]) + 32u * kStage * (uint32_t)t2);
   };
 
   // ---- prologue: row factors, stage 0 ----
 #pragma unroll
   for (int u = 0; u < 4; u++) dma_a1(2 * sb0, s_a0, u);
 #pragma unroll
-  for (int u = 0; u < 3; u++) dma_w1(sb0, s_w0, u);
+  for (int u = 0; u < F::kWaveCopies; u++) dma_w1(sb0, s_w0, u);
   dma_rows(sb0, 0);
   dma_rows(sb0, 1);
   if (tid < 256) {
@@ -317,7 +446,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  build(s_w0, 0, s_b0);
+  build(s_w0, 0, s_b0, sb0);
   __syncthreads();
 
   // One stage: MFMAs on (sa, sbt); the next stage's weights expanded into
@@ -331,8 +460,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
     const bool more = g + 1 < 2 * sb1;
     const bool wmore = half == 0 && sb + 1 < sb1;  // the next super-block's raw weights
     const bool rmore = half == 1 && sb + 1 < sb1;  // the next super-block's row inputs
-    i4v a0 = frag(sa, arow0, 0), a1 = frag(sa, arow1, 0);
-    i4v b0 = frag(sbt, bcol0, 0), b1 = frag(sbt, bcol1, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+      opaque(fa[ks]);
+      opaque(fb[ks]);
+    }
+    opaque(x_raw);
+    opaque(x_w0);
+    opaque(x_w1);
+    i4v a0 = frag(sa, 0, 0, true), a1 = frag(sa, 1, 0, true);
+    i4v b0 = frag(sbt, 0, 0, false), b1 = frag(sbt, 1, 0, false);
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
       const bool first = half == 0 && ks == 0;
@@ -344,24 +481,37 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
       // its operands when it issues, so the reads overlap the four MFMAs
       // without a second register set.
       if (ks < 3) {
-        a0 = frag(sa, arow0, ks + 1);
-        a1 = frag(sa, arow1, ks + 1);
-        b0 = frag(sbt, bcol0, ks + 1);
-        b1 = frag(sbt, bcol1, ks + 1);
+        a0 = frag(sa, 0, ks + 1, true);
+        a1 = frag(sa, 1, ks + 1, true);
+        b0 = frag(sbt, 0, ks + 1, false);
+        b1 = frag(sbt, 1, ks + 1, false);
       }
       // this K-step's share of the next stage's copies
       if (more) dma_a1(g + 1, na, ks);
-      if (wmore && ks < 3) dma_w1(sb + 1, wnext, ks);
+      if (wmore && ks < F::kWaveCopies) dma_w1(sb + 1, wnext, ks);
       if (rmore && ks < 2) dma_rows(sb + 1, ks);
-      if (ks == 1 && more) build(nw, nhalf, nbt);
+      if (ks == 1 && more) build(nw, nhalf, nbt, (g + 1) >> 1);
     }
     if (half == 0) {
-      prep(wcur);
+      prep(wcur, sb);
     } else {
       // epilogue of super-block sb: the f16 product (min term, offset, and
       // the magic correction), then acc += (1.5 2^23 + T) * 4 d dy
-      const h8 ra0 = *(const h8*)&s_rop[arow0][8 * h], ra1 = *(const h8*)&s_rop[arow1][8 * h];
-      const h8 cb0 = *(const h8*)&s_cop[bcol0][8 * h], cb1 = *(const h8*)&s_cop[bcol1][8 * h];
+      h8 ra0, ra1, cb0, cb1;
+      if constexpr (Q6) {
+        // the magic correction only: A = dy_h (2^16, 2^15), B = -dq 2^7 (twice)
+        const float y0 = h ? 0.0f : s_dy[arow0], y1 = h ? 0.0f : s_dy[arow1];
+        const float q0 = h ? 0.0f : -128.0f * s_d4[bcol0], q1 = h ? 0.0f : -128.0f * s_d4[bcol1];
+        ra0 = h8{(_Float16)(y0 * 65536.0f), (_Float16)(y0 * 32768.0f), 0, 0, 0, 0, 0, 0};
+        ra1 = h8{(_Float16)(y1 * 65536.0f), (_Float16)(y1 * 32768.0f), 0, 0, 0, 0, 0, 0};
+        cb0 = h8{(_Float16)q0, (_Float16)q0, 0, 0, 0, 0, 0, 0};
+        cb1 = h8{(_Float16)q1, (_Float16)q1, 0, 0, 0, 0, 0, 0};
+      } else {
+        ra0 = *(const h8*)&s_rop[arow0][8 * h];
+        ra1 = *(const h8*)&s_rop[arow1][8 * h];
+        cb0 = *(const h8*)&s_cop[bcol0][8 * h];
+        cb1 = *(const h8*)&s_cop[bcol1][8 * h];
+      }
       acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra0, cb0, acc[0][0], 0, 0, 0);
       acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra0, cb1, acc[0][1], 0, 0, 0);
       acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ra1, cb0, acc[1][0], 0, 0, 0);
@@ -399,6 +549,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
   }
 
   // ---- store, the row factor undone (exact powers of two) ----
+  constexpr float kOutScale = Q6 ? 1.0f / 64.0f : 1.0f;  // Q6_K: its extra 1/2 and the 2^7 of dq
   float* __restrict__ dst = pick(a.dst);
   const int64_t ldd = pick(a.ldd);
   if (S == 1) {
@@ -412,7 +563,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
         for (int i = 0; i < 16; i++) {
           const int lr = 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
           const int64_t row = m0 + lr;
-          if (row < M) dst[row * ldd + col] = acc[tm][tn][i] / s_rf[lr];
+          if (row < M) dst[row * ldd + col] = acc[tm][tn][i] / s_rf[lr] * kOutScale;
         }
     }
     return;
@@ -429,7 +580,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4k_sp_kernel(const SpArgs a
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const int lr = 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
-        mine[(32 * tn + 16 * tm + i) * kThreads + tid] = acc[tm][tn][i] / s_rf[lr];
+        mine[(32 * tn + 16 * tm + i) * kThreads + tid] = acc[tm][tn][i] / s_rf[lr] * kOutScale;
       }
 }
 
@@ -512,9 +663,9 @@ size_t gemm_q4k_sp_split_bytes(const MvTargets& t, int64_t k, int64_t rows, int 
   return slots;
 }
 
-hipError_t launch_gemm_q4k_sp_targets(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, void* split_ws,
-                                      size_t split_bytes, int cus, hipStream_t st) {
-  QMM_NOTE_LAUNCH();
+template <int FMT>
+hipError_t launch_sp(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, void* split_ws, size_t split_bytes,
+                     int cus, hipStream_t st) {
   if (t.count < 1 || t.count > kMaxTargets) return hipErrorInvalidValue;
   const size_t need = gemm_q4k_sp_split_bytes(t, k, rows, cus);
   const bool split = need > 0 && split_ws != nullptr && split_bytes >= need;
@@ -553,13 +704,43 @@ hipError_t launch_gemm_q4k_sp_targets(const MvTargets& t, int64_t k, const ActPl
   if (units >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   a.remap = units % 8 == 0 ? 1 : 0;
   a.part = tiles > 0 ? (float*)split_ws : nullptr;
-  gemm_q4k_sp_kernel<<<dim3((unsigned)units), kThreads, 0, st>>>(a);
+  gemm_kq_sp_kernel<FMT><<<dim3((unsigned)units), kThreads, 0, st>>>(a);
   if (tiles > 0) {
     // unused entries past the last weight start at the end (no workgroups)
     for (int i = t.count; i < kMaxTargets; i++) a.tile_base[i] = tiles;
     gemm_q4k_sp_sum_kernel<<<dim3((unsigned)(tiles * (kBM * kBN / 4 / kSumThreads))), kSumThreads, 0, st>>>(a);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_q4k_sp_targets(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, void* split_ws,
+                                      size_t split_bytes, int cus, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  return launch_sp<T_Q4_K>(t, k, p, rows, split_ws, split_bytes, cus, st);
+}
+
+hipError_t launch_gemm_q6k_sp_targets(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, void* split_ws,
+                                      size_t split_bytes, int cus, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  return launch_sp<T_Q6_K>(t, k, p, rows, split_ws, split_bytes, cus, st);
+}
+
+bool gemm_q6k_sp_fits(int64_t n, int64_t k, int64_t rows) {
+  // rows 16-byte aligned (210 (k / 256) a multiple of 16) and the single
+  // pass's rounding small against ||w|| ||x|| (k >= 2048, as for Q4_K)
+  return k % 2048 == 0 && n * (k / 256) * 210 < ((int64_t)1 << 31) && (rows + kBM) * k < ((int64_t)1 << 31) &&
+         rows < ((int64_t)1 << 24);
+}
+
+hipError_t launch_gemm_q6k_sp(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
+                              int64_t ldd, hipStream_t st) {
+  MvTargets t{};
+  t.w[0] = w;
+  t.dst[0] = dst;
+  t.ldd[0] = ldd;
+  t.row_end[0] = n;
+  t.count = 1;
+  return launch_gemm_q6k_sp_targets(t, k, p, rows, nullptr, 0, 256, st);
 }
 
 hipError_t launch_gemm_q4k_sp(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,

@@ -218,7 +218,15 @@ bool matrix_takes(int type, const void* w, const void* xq, int64_t n, int64_t k,
 // the exact two-pass kernel, whose 128-row tiles waste less on short batches.
 hipError_t launch_gemm(int type, const void* w, int64_t n, int64_t k, const qmm::ActPlanes& p, int64_t rows,
                        float* dst, int64_t ldd, hipStream_t st) {
-  if (type == qmm::T_Q6_K) return qmm::launch_gemm_q6k(w, n, k, p, rows, dst, ldd, st);
+  if (type == qmm::T_Q6_K) {
+    // without a workspace for K splits, the single-pass Q6_K GEMM only where
+    // its tiles fill the CUs (uncut, its per-super-block work is ~1.5x the
+    // exact kernel's share of a narrow product)
+    if (rows >= qmm::gemm_q4k_sp_min_rows() && qmm::gemm_q6k_sp_fits(n, k, rows) &&
+        qmm::gemm_q4k_sp_splits(n, k, rows, (int)cu_count()) == 1)
+      return qmm::launch_gemm_q6k_sp(w, n, k, p, rows, dst, ldd, st);
+    return qmm::launch_gemm_q6k(w, n, k, p, rows, dst, ldd, st);
+  }
   if (type != qmm::T_Q4_K) return qmm::launch_gemm_b32(type, w, n, k, p, rows, dst, ldd, st);
   if (rows >= qmm::gemm_q4k_sp_min_rows() && qmm::gemm_q4k_sp_fits(n, k, rows))
     return qmm::launch_gemm_q4k_sp(w, n, k, p, rows, dst, ldd, st);
@@ -228,8 +236,15 @@ hipError_t launch_gemm(int type, const void* w, int64_t n, int64_t k, const qmm:
 // Products the single-pass Q4_K GEMM takes: those it can cut along K and
 // launch several of at once (launch_gemm_q4k_sp_targets).
 bool sp_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows, hipStream_t st) {
-  return type == qmm::T_Q4_K && gemm_takes(type, w, xq, n, k, rows, st) && rows >= qmm::gemm_q4k_sp_min_rows() &&
-         qmm::gemm_q4k_sp_fits(n, k, rows);
+  if (type != qmm::T_Q4_K && type != qmm::T_Q6_K) return false;
+  if (!gemm_takes(type, w, xq, n, k, rows, st) || rows < qmm::gemm_q4k_sp_min_rows()) return false;
+  return type == qmm::T_Q4_K ? qmm::gemm_q4k_sp_fits(n, k, rows) : qmm::gemm_q6k_sp_fits(n, k, rows);
+}
+
+hipError_t launch_sp(int type, const qmm::MvTargets& t, int64_t k, const qmm::ActPlanes& p, int64_t rows, void* ws,
+                     size_t ws_bytes, hipStream_t st) {
+  return type == qmm::T_Q6_K ? qmm::launch_gemm_q6k_sp_targets(t, k, p, rows, ws, ws_bytes, (int)cu_count(), st)
+                             : qmm::launch_gemm_q4k_sp_targets(t, k, p, rows, ws, ws_bytes, (int)cu_count(), st);
 }
 
 qmm::MvTargets one_target(const void* w, int64_t n, float* dst, int64_t ldd) {
@@ -471,12 +486,14 @@ int qmm_forward(int type, const void* w, const float* x, int64_t x_stride, float
   if (qmm::launch_act_quantize(layout, x, x_stride, k, rows, workspace, q8k_scale(), st) != hipSuccess)
     return QMM_DEVICE_ERROR;
   const qmm::ActPlanes p = qmm::act_planes(layout, workspace, k, rows);
-  if (sp_takes(type, w, workspace, n, k, rows, st)) {
+  // Q6_K takes the single-pass GEMM only cut as planned (uncut, a narrow
+  // product runs faster on the exact kernel)
+  if (sp_takes(type, w, workspace, n, k, rows, st) &&
+      (type == qmm::T_Q4_K || split == 0 || workspace_bytes >= *need)) {
     const size_t off = qmm::align_up(bytes, 256);
     void* sws = workspace_bytes > off ? (char*)workspace + off : nullptr;
-    if (qmm::launch_gemm_q4k_sp_targets(one_target(w, n, dst, ldd), k, p, rows, sws,
-                                        workspace_bytes > off ? workspace_bytes - off : 0, (int)cu_count(),
-                                        st) != hipSuccess)
+    if (launch_sp(type, one_target(w, n, dst, ldd), k, p, rows, sws, workspace_bytes > off ? workspace_bytes - off : 0,
+                  st) != hipSuccess)
       return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
@@ -564,15 +581,16 @@ int qmm_forward_shared(int type, int count, const void* const* w, const int64_t*
   const size_t sbytes = workspace_bytes > off ? workspace_bytes - off : 0;
   auto flush_sp = [&]() -> int {
     if (spg.count == 0) return QMM_OK;
-    if (qmm::launch_gemm_q4k_sp_targets(spg, k, p, rows, sws, sbytes, (int)cu_count(), st) != hipSuccess)
+    if (launch_sp(type, spg, k, p, rows, sws, sbytes, st) != hipSuccess)
       return QMM_DEVICE_ERROR;
     g_gemm_launches.fetch_add(1, std::memory_order_relaxed);
     spg = qmm::MvTargets{};
     spend = 0;
     return QMM_OK;
   };
+  const bool sp_ok = type == qmm::T_Q4_K || split == 0 || workspace_bytes >= *need;
   for (int i = 0; i < count; i++) {
-    if (sp_takes(type, w[i], workspace, n[i], k, rows, st)) {
+    if (sp_ok && sp_takes(type, w[i], workspace, n[i], k, rows, st)) {
       spg.w[spg.count] = w[i];
       spg.dst[spg.count] = dst[i];
       spg.ldd[spg.count] = ldd[i];

@@ -190,6 +190,14 @@ int gemm_q4k_sp_splits(int64_t n, int64_t k, int64_t rows, int cus);
 size_t gemm_q4k_sp_split_bytes(const MvTargets& t, int64_t k, int64_t rows, int cus);
 hipError_t launch_gemm_q4k_sp_targets(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, void* split_ws,
                                       size_t split_bytes, int cus, hipStream_t st);
+// The same single-pass GEMM for Q6_K weights (k a multiple of 2048, from
+// gemm_q4k_sp_min_rows() rows): w8 = round(m_j (q - 32) / 256) with
+// m_j = round(127 sc_j / 16); same tiles, K splits and launches.
+bool gemm_q6k_sp_fits(int64_t n, int64_t k, int64_t rows);
+hipError_t launch_gemm_q6k_sp(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
+                              int64_t ldd, hipStream_t s);
+hipError_t launch_gemm_q6k_sp_targets(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, void* split_ws,
+                                      size_t split_bytes, int cus, hipStream_t st);
 
 int gemm_q4k_min_rows();
 // The GEMM indexes with 32-bit byte offsets: the weight below 2 GiB and

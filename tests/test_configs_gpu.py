@@ -109,8 +109,8 @@ def test_c3_q6k_down_projection_m512():
     x[:, ch] *= np.float32(20.0)
     y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
     kernel = lib().qmm_last_kernel().decode()
-    assert "launch_gemm_q6k(" in kernel, kernel
+    assert "launch_gemm_q6k_sp" in kernel, kernel  # the single-pass GEMM (k a multiple of 2048)
     want = qref.matmul(Q6K, x, np.frombuffer(qt.data(), np.uint8), n)
     err = normalised(y, want, row_norms(qt), x)
     assert err <= TOL_GEMM, f"{kernel}: {err}"
-    assert err <= 1e-5, f"{kernel}: {err}"  # the reference's exact integers, scaled in f32
+    assert err <= 1e-3, f"{kernel}: {err}"  # its one rounding: sc (q - 32) into an int8 operand

@@ -421,12 +421,14 @@ def test_q6k_gemm_parity(k, n, rows):
     before = L.qmm_gemm_launches()
     y = QMatMul(qt).forward(upload(x)).cpu().numpy()
     assert L.qmm_gemm_launches() == before + 1, "the MFMA GEMM did not run"
-    assert "launch_gemm_q6k(" in L.qmm_last_kernel().decode()
+    kernel = L.qmm_last_kernel().decode()
+    single_pass = rows >= 129 and k % 2048 == 0
+    assert ("launch_gemm_q6k_sp" if single_pass else "launch_gemm_q6k(") in kernel, kernel
     want = qref.matmul(qref.Q6_K, x, wq, n)
     wdeq = qref.to_float(qref.Q6_K, wq, n * k).reshape(n, k)
     err = normalised_error(y, want, wdeq, x)
     assert err <= TOL_GEMM, f"k={k} n={n} rows={rows}: {err}"
-    assert err <= TIGHT_Q6K, f"k={k} n={n} rows={rows}: {err}"
+    assert err <= (TIGHT_SP if single_pass else TIGHT_Q6K), f"k={k} n={n} rows={rows}: {err}"
 
 
 def test_q6k_gemm_special_activation_rows():
@@ -476,6 +478,86 @@ def test_q6k_gemm_shared_activation_and_prequantized_equal_forward():
     assert st == 0
     assert "launch_gemm_q6k(" in lib().qmm_last_kernel().decode()
     assert torch.equal(out, shared[0])
+
+
+# ---------------------------------------------------------------------------
+# Q6_K in one int8 pass (from 129 rows, k a multiple of 2048): the weight enters
+# as round(m_j (q - 32) / 256) with m_j = round(127 sc_j / 16); held to 1e-3
+# of ||w|| ||x|| (the 2e-3 bound)
+# ---------------------------------------------------------------------------
+Q6K_SP_SHAPES = [  # (k, n, rows): one and two row tiles, row and weight-row tails, cut along K and not
+    (2048, 7, 129), (4096, 300, 256), (6144, 1000, 300), (14336, 200, 512), (2048, 4100, 383),
+]
+
+
+@pytest.mark.parametrize("k,n,rows", Q6K_SP_SHAPES)
+def test_q6k_single_pass_gemm_parity(k, n, rows):
+    rng = np.random.default_rng(zlib.crc32(f"q6sp-{k}-{n}-{rows}".encode()))
+    w = weights(rng, n, k)
+    x = activations(rng, rows, k, outliers=True)
+    qt, wq = q6k(w)
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert "launch_gemm_q6k_sp" in lib().qmm_last_kernel().decode()
+    want = qref.matmul(qref.Q6_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q6_K, wq, n * k).reshape(n, k)
+    err = normalised_error(y, want, wdeq, x)
+    assert err <= TOL_GEMM
+    assert err <= TIGHT_SP, f"k={k} n={n} rows={rows}: {err}"
+
+
+def test_q6k_single_pass_gemm_extreme_scales_and_rows():
+    """Weight rows with one large value per 16-value group (scales -128 and
+    127 next to small codes, codes 0 and 63), a zero weight row; activation
+    rows of the quantizer's edge cases and scaled by 1e-30, 1e-6, 1e3, 1e30."""
+    from helpers import special_rows
+
+    k, n, rows = 2048, 96, 160
+    rng = np.random.default_rng(94)
+    w = weights(rng, n, k)
+    w[5, ::16] = 3.0
+    w[7, ::16] = -3.0
+    w[6] = 0.0
+    qt, wq = q6k(w)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    sp = special_rows(k)
+    x[: len(sp)] = sp
+    for r, sc in zip(range(len(sp), len(sp) + 4), (1e-30, 1e-6, 1e3, 1e30)):
+        x[r] *= np.float32(sc)
+    y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert "launch_gemm_q6k_sp" in lib().qmm_last_kernel().decode()
+    assert np.all(y[0] == 0.0) and np.all(y[:, 6] == 0.0)
+    want = qref.matmul(qref.Q6_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q6_K, wq, n * k).reshape(n, k)
+    assert normalised_error(y, want, wdeq, x) <= TIGHT_SP
+
+
+def test_q6k_single_pass_gemm_shared_and_prequantized():
+    """Q6_K weights sharing an activation at 512 rows (one launch, each cut
+    along K as its own forward cuts it) give each forward's bits, and forward
+    is bit-identical run to run. Without a workspace for the cut (qmm_matmul
+    from a quantized activation) a narrow Q6_K product runs on the exact
+    kernel: within the single pass's bound of it."""
+    from swarmllm_amd import _lib
+    from swarmllm_amd.qtensor import quantize_act
+
+    rng = np.random.default_rng(95)
+    k, rows = 4096, 512
+    mats = [QMatMul(q6k(weights(rng, n, k))[0]) for n in (1024, 300)]
+    x = upload(activations(rng, rows, k, outliers=True))
+    before = lib().qmm_gemm_launches()
+    shared = QMatMul.forward_shared(x, mats)
+    assert lib().qmm_gemm_launches() == before + 1
+    for m, y in zip(mats, shared):
+        assert torch.equal(y, m.forward(x))
+        assert torch.equal(y, m.forward(x))
+    xq = quantize_act(x, _lib.ACT_Q8K)
+    n = 1024
+    out = torch.empty((rows, n), dtype=torch.float32, device=DEV)
+    assert lib().qmm_matmul(qref.Q6_K, mats[0].qtensor.data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k, n, rows,
+                            torch.cuda.current_stream().cuda_stream) == 0
+    assert "launch_gemm_q6k(" in lib().qmm_last_kernel().decode()
+    wdeq = mats[0].qtensor.dequantize().cpu().numpy()
+    assert normalised_error(out.cpu().numpy(), shared[0].cpu().numpy(), wdeq, x.cpu().numpy()) <= TIGHT_SP
 
 
 # ---------------------------------------------------------------------------
