@@ -107,6 +107,12 @@ __device__ __forceinline__ float row_factor(float maxabs) {
   const int fe = 253 - (int)E;  // biased exponent of 2^(126 - E)
   return __builtin_bit_cast(float, (uint32_t)(fe < 1 ? 1 : (fe > 254 ? 254 : fe)) << 23);
 }
+// 1 / r for a row factor r = 2^p (biased exponent 1..252): 2^-p, a normal
+// float, so x * inv_pow2(r) is x / r exactly (both scale x by 2^-p and round
+// once), without a division.
+__device__ __forceinline__ float inv_pow2(float r) {
+  return __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, r));
+}
 
 // The launch's weights (up to kMaxTargets sharing one activation) and their
 // K splits; see launch_gemm_q4k_sp_targets.
@@ -117,6 +123,7 @@ struct SpArgs {
   int64_t n[kMaxTargets];
   int unit_end[kMaxTargets];   // workgroups of weights 0..t
   int splits[kMaxTargets];     // K splits of weight t's tiles (1, 2 or 4)
+  int per[kMaxTargets];        // consecutive splits a workgroup computes (1, or 2 / 4 for Q4_K)
   int tile_base[kMaxTargets];  // the sum kernel's first workgroup for weight t (its split tiles before it)
   int64_t part_off[kMaxTargets];  // its first slot in `part` (floats)
   const int8_t* yq;
@@ -230,10 +237,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
   auto pick = [&](const auto& arr) { return t == 0 ? arr[0] : t == 1 ? arr[1] : t == 2 ? arr[2] : arr[3]; };
   const int u0 = t == 0 ? 0 : t == 1 ? a.unit_end[0] : t == 2 ? a.unit_end[1] : a.unit_end[2];
   const int S = pick(a.splits);
+  const int P = Q6 ? 1 : pick(a.per);
   const int mtiles = a.mtiles;
   const int loc = idx - u0;
   const int mt = loc % mtiles, rest = loc / mtiles;
-  const int split = rest % S, ct = rest / S;
+  const int split = (rest % (S / P)) * P, ct = rest / (S / P);
   const uint8_t* __restrict__ W = (const uint8_t*)pick(a.w);
   const int64_t N = pick(a.n);
   const int nsb = a.nsb;
@@ -243,8 +251,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
   const int64_t M = a.M;
   const int64_t m0 = (int64_t)mt * kBM;
   const int64_t n0 = (int64_t)ct * kBN;
-  // this workgroup's super-blocks
-  const int sb0 = split * nsb / S, sb1 = (split + 1) * nsb / S;
+  // this workgroup's super-blocks: splits split .. split + P - 1, each
+  // plen super-blocks (nsb is a multiple of 2 S when S > 1)
+  const int plen = nsb / S;
+  const int sb0 = split * nsb / S, sb1 = (split + P) * nsb / S;
 
   const int64_t K = (int64_t)nsb * 256;
   const uint32_t rowbytes = (uint32_t)nsb * F::kBlock;
@@ -439,10 +449,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
   for (int u = 0; u < F::kWaveCopies; u++) dma_w1(sb0, s_w0, u);
   dma_rows(sb0, 0);
   dma_rows(sb0, 1);
+  // each split's row factors (the maximum over its own super-blocks, so a
+  // split's result does not depend on the workgroup that computes it); 8
+  // loads in flight at a time, and the maximum does not depend on the order
+  // (fmaxf skips NaN)
+  float rfp[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   if (tid < 256) {
-    float mx = 0.0f;
-    for (int sb = sb0; sb < sb1; sb++) mx = fmaxf(mx, fabsf(yd[prow * nsb + sb]));
-    s_rf[tid] = row_factor(mx);
+    const float* __restrict__ yr = yd + prow * nsb;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      if (q >= P) break;
+      const int e0 = sb0 + q * plen, e1 = e0 + (P == 1 ? sb1 - sb0 : plen);
+      float mx = 0.0f;
+      for (int sb = e0; sb < e1; sb += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = sb + j < e1 ? yr[sb + j] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
+      }
+      rfp[q] = row_factor(mx);
+    }
+    s_rf[tid] = rfp[0];
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -539,6 +567,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
     __syncthreads();
   };
 
+  constexpr float kOutScale = Q6 ? 1.0f / 64.0f : 1.0f;  // Q6_K: its extra 1/2 and the 2^7 of dq
+  const int tl = ct * mtiles + mt;  // the tile within its weight
+  auto store_slot = [&](int sp) {
+    float* __restrict__ mine = a.part + pick(a.part_off) + ((int64_t)tl * S + sp) * (kBM * kBN);
+#pragma unroll
+    for (int tn = 0; tn < 2; tn++)
+#pragma unroll
+      for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const int lr = 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
+          mine[(32 * tn + 16 * tm + i) * kThreads + tid] = acc[tm][tn][i] * inv_pow2(s_rf[lr]) * kOutScale;
+        }
+  };
+
   for (int sb = sb0; sb < sb1; sb += 2) {
     stage(sb, 0, s_a0, s_b0, s_a1, s_b1, s_w0, 1, s_w0, s_w1);
     stage(sb, 1, s_a1, s_b1, s_a0, s_b0, s_w1, 0, s_w0, s_w1);
@@ -546,10 +589,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
       stage(sb + 1, 0, s_a0, s_b0, s_a1, s_b1, s_w1, 1, s_w1, s_w0);
       stage(sb + 1, 1, s_a1, s_b1, s_a0, s_b0, s_w0, 0, s_w1, s_w0);
     }
+    if constexpr (!Q6) {
+      // the end of a split that is not the workgroup's last: its partial to
+      // its slot, the accumulators cleared, the next split's row factors
+      const int q = (sb + 2 - sb0) / plen;
+      if (P > 1 && sb + 2 < sb1 && sb + 2 - sb0 == q * plen) {
+        store_slot(split + q - 1);
+#pragma unroll
+        for (int x = 0; x < 2; x++)
+#pragma unroll
+          for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[x][c][i] = 0.0f;
+        __syncthreads();
+        if (tid < 256) s_rf[tid] = q == 1 ? rfp[1] : q == 2 ? rfp[2] : rfp[3];
+        __syncthreads();
+      }
+    }
   }
 
   // ---- store, the row factor undone (exact powers of two) ----
-  constexpr float kOutScale = Q6 ? 1.0f / 64.0f : 1.0f;  // Q6_K: its extra 1/2 and the 2^7 of dq
   float* __restrict__ dst = pick(a.dst);
   const int64_t ldd = pick(a.ldd);
   if (S == 1) {
@@ -563,7 +622,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
         for (int i = 0; i < 16; i++) {
           const int lr = 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
           const int64_t row = m0 + lr;
-          if (row < M) dst[row * ldd + col] = acc[tm][tn][i] / s_rf[lr] * kOutScale;
+          if (row < M) dst[row * ldd + col] = acc[tm][tn][i] * inv_pow2(s_rf[lr]) * kOutScale;
         }
     }
     return;
@@ -571,48 +630,68 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
   // Several K splits: each writes its partial tile to its slot, in register
   // order (element e of thread tid at e * 512 + tid: every store a full line
   // per wave); gemm_q4k_sp_sum_kernel adds the slots in split order.
-  const int tl = ct * mtiles + mt;  // the tile within its weight
-  float* __restrict__ mine = a.part + pick(a.part_off) + ((int64_t)tl * S + split) * (kBM * kBN);
-#pragma unroll
-  for (int tn = 0; tn < 2; tn++)
-#pragma unroll
-    for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int lr = 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
-        mine[(32 * tn + 16 * tm + i) * kThreads + tid] = acc[tm][tn][i] / s_rf[lr] * kOutScale;
-      }
+  store_slot(split + P - 1);
 }
 
-// dst of the split tiles: each thread adds 4 consecutive slot elements (4
-// neighbouring columns of one row) over the splits, in split order. Split
-// tile b of the launch is weight t's tile b - tile_base[t].
+// dst of the split tiles: each thread adds, for 2 groups of 4 consecutive
+// slot elements (4 neighbouring columns of one row), the splits' partials in
+// split order ((p0 + p1) + p2) + p3, every slot's loads issued before the
+// first add. Split tile b of the launch is weight t's tile b - tile_base[t];
+// a workgroup covers 512 groups of one tile, so b, t and S are uniform.
 constexpr int kSumThreads = 256;
+constexpr int kSumBlocksPerTile = kBM * kBN / 4 / (2 * kSumThreads);  // 16
 __global__ __launch_bounds__(kSumThreads) void gemm_q4k_sp_sum_kernel(const SpArgs a) {
-  const int64_t f = (int64_t)blockIdx.x * kSumThreads + threadIdx.x;  // a group of 4 elements
-  const int b = (int)(f >> 13);                                      // 8192 groups a tile
+  const int b = (int)blockIdx.x / kSumBlocksPerTile;
   const int t = b < a.tile_base[1] ? 0 : b < a.tile_base[2] ? 1 : b < a.tile_base[3] ? 2 : 3;
   auto pick = [&](const auto& arr) { return t == 0 ? arr[0] : t == 1 ? arr[1] : t == 2 ? arr[2] : arr[3]; };
-  const int S = pick(a.splits);
+  const int S = pick(a.splits);  // 2 or 4
   const int tl = b - pick(a.tile_base);
   const int mt = tl % a.mtiles, ct = tl / a.mtiles;
   const int64_t N = pick(a.n), ldd = pick(a.ldd), M = a.M;
-  const int o = 4 * (int)(f & 8191);  // element offset in the slot: e * 512 + tid
-  const float* __restrict__ base = a.part + pick(a.part_off) + (int64_t)tl * S * (kBM * kBN) + o;
+  float* __restrict__ dbase = pick(a.dst);
+  const bool vec = (ldd & 3) == 0 && ((uintptr_t)dbase & 15) == 0;
+  const float* __restrict__ tile = a.part + pick(a.part_off) + (int64_t)tl * S * (kBM * kBN);
   typedef float f4 __attribute__((ext_vector_type(4)));
-  f4 sum = __builtin_nontemporal_load((const f4*)base);
-  for (int q = 1; q < S; q++) sum += __builtin_nontemporal_load((const f4*)(base + (int64_t)q * (kBM * kBN)));
-  // the slot position of element 0: e = o / 512, thread tid = o % 512 (the 4 share e, wave and h)
-  const int e = o >> 9, tid = o & 511, lane = tid & 63, wv = tid >> 6;
-  const int wm = wv & 3, wn = wv >> 2, h = lane >> 5, r32 = lane & 31;
-  const int tn = e >> 5, tm = (e >> 4) & 1, i = e & 15;
-  const int64_t row = (int64_t)mt * kBM + 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
-  const int64_t col = (int64_t)ct * kBN + 64 * wn + 32 * tn + r32;
-  if (row >= M) return;
-  float* __restrict__ d = pick(a.dst) + row * ldd + col;
+  constexpr int kSlot = kBM * kBN;
+  int o[2];
+  f4 v[2][4];
 #pragma unroll
-  for (int j = 0; j < 4; j++)
-    if (col + j < N) d[j] = sum[j];
+  for (int j = 0; j < 2; j++) {
+    // element offset in the slot: e * 512 + tid of the GEMM's register order
+    o[j] = 4 * (((int)blockIdx.x % kSumBlocksPerTile) * (2 * kSumThreads) + j * kSumThreads + (int)threadIdx.x);
+    v[j][0] = __builtin_nontemporal_load((const f4*)(tile + o[j]));
+    v[j][1] = __builtin_nontemporal_load((const f4*)(tile + kSlot + o[j]));
+  }
+  if (S > 2) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      v[j][2] = __builtin_nontemporal_load((const f4*)(tile + 2 * kSlot + o[j]));
+      v[j][3] = __builtin_nontemporal_load((const f4*)(tile + 3 * kSlot + o[j]));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    f4 sum = v[j][0] + v[j][1];
+    if (S > 2) {
+      sum += v[j][2];
+      sum += v[j][3];
+    }
+    // the slot position of element 0: e = o / 512, thread tid = o % 512 (the 4 share e, wave and h)
+    const int e = o[j] >> 9, tid = o[j] & 511, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv & 3, wn = wv >> 2, h = lane >> 5, r32 = lane & 31;
+    const int tn = e >> 5, tm = (e >> 4) & 1, i = e & 15;
+    const int64_t row = (int64_t)mt * kBM + 64 * wm + 32 * tm + 8 * (i >> 2) + 4 * h + (i & 3);
+    const int64_t col = (int64_t)ct * kBN + 64 * wn + 32 * tn + r32;
+    if (row >= M) continue;
+    float* __restrict__ d = dbase + row * ldd + col;
+    if (vec && col + 3 < N) {
+      *(f4*)d = sum;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (col + q < N) d[q] = sum[q];
+    }
+  }
 }
 
 }  // namespace
@@ -676,7 +755,32 @@ hipError_t launch_sp(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t 
   a.M = rows;
   a.nsb = (int)(k / 256);
   a.mtiles = (int)((rows + kBM - 1) / kBM);
-  int64_t units = 0, prev = 0, slot_floats = 0;
+  // K splits per weight (from its own shape), then, where the launch's
+  // workgroups exceed the CUs (several weights), Q4_K workgroups that
+  // compute 2 or 4 consecutive splits of a tile: the same partial tiles, so
+  // the same bits, in one round of workgroups
+  int S_[kMaxTargets], P_[kMaxTargets];
+  int64_t wt_[kMaxTargets];
+  for (int i = 0; i < t.count; i++) {
+    const int64_t n = t.row_end[i] - (i ? t.row_end[i - 1] : 0);
+    S_[i] = split ? gemm_q4k_sp_splits(n, k, rows, cus) : 1;
+    P_[i] = 1;
+    wt_[i] = (int64_t)a.mtiles * ((n + kBN - 1) / kBN);
+  }
+  if (FMT == T_Q4_K) {
+    for (;;) {
+      int64_t total = 0;
+      int best = -1;
+      for (int i = 0; i < t.count; i++) {
+        const int64_t u = wt_[i] * (S_[i] / P_[i]);
+        total += u;
+        if (S_[i] / P_[i] >= 2 && (best < 0 || u > wt_[best] * (S_[best] / P_[best]))) best = i;
+      }
+      if (total <= cus || best < 0) break;
+      P_[best] *= 2;
+    }
+  }
+  int64_t units = 0, slot_floats = 0;
   int tiles = 0;
   for (int i = 0; i < kMaxTargets; i++) {
     const int j = i < t.count ? i : t.count - 1;  // unused entries repeat the last weight, with no units
@@ -685,22 +789,19 @@ hipError_t launch_sp(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t 
     a.dst[i] = t.dst[j];
     a.ldd[i] = t.ldd[j];
     a.n[i] = n;
-    const int S = split ? gemm_q4k_sp_splits(n, k, rows, cus) : 1;
-    a.splits[i] = S;
+    a.splits[i] = S_[j];
+    a.per[i] = P_[j];
     a.tile_base[i] = tiles;
     a.part_off[i] = slot_floats;
     if (i < t.count) {
-      const int64_t wt = (int64_t)a.mtiles * ((n + kBN - 1) / kBN);
-      units += wt * S;
-      if (S > 1) {
-        tiles += (int)wt;
-        slot_floats += wt * S * kBM * kBN;
+      units += wt_[i] * (S_[i] / P_[i]);
+      if (S_[i] > 1) {
+        tiles += (int)wt_[i];
+        slot_floats += wt_[i] * S_[i] * kBM * kBN;
       }
     }
     a.unit_end[i] = (int)units;
-    prev = t.row_end[j];
   }
-  (void)prev;
   if (units >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   a.remap = units % 8 == 0 ? 1 : 0;
   a.part = tiles > 0 ? (float*)split_ws : nullptr;
@@ -708,7 +809,7 @@ hipError_t launch_sp(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t 
   if (tiles > 0) {
     // unused entries past the last weight start at the end (no workgroups)
     for (int i = t.count; i < kMaxTargets; i++) a.tile_base[i] = tiles;
-    gemm_q4k_sp_sum_kernel<<<dim3((unsigned)(tiles * (kBM * kBN / 4 / kSumThreads))), kSumThreads, 0, st>>>(a);
+    gemm_q4k_sp_sum_kernel<<<dim3((unsigned)(tiles * kSumBlocksPerTile)), kSumThreads, 0, st>>>(a);
   }
   return hipGetLastError();
 }

@@ -217,13 +217,16 @@ def test_q4k_gemm_cut_along_k(n, rows):
     assert err <= TIGHT_SP, err
 
 
-def test_q4k_gemm_cut_along_k_shared_equals_forward():
-    """q, k and v of a prefill (4096 + 1024 + 1024 weight rows, M = 512) in
-    one launch give each weight's own forward bits: a weight's K split does
-    not depend on the weights sharing its launch."""
+@pytest.mark.parametrize("ns", [(4096, 1024, 1024), (4096, 4096), (4096, 4096, 4096, 4096), (2048, 2048)])
+def test_q4k_gemm_cut_along_k_shared_equals_forward(ns):
+    """Weights sharing one launch at M = 512 give each weight's own forward
+    bits: a weight's K split does not depend on the weights sharing its
+    launch, nor on how many of a tile's splits one workgroup computes (q+k+v
+    and the 4096-row pairs and quadruples have more split workgroups than
+    CUs, so workgroups there take 2 or 4 consecutive splits)."""
     k, rows = 4096, 512
     rng = np.random.default_rng(15)
-    mats = [QMatMul(q4k(weights(rng, n, k))[0]) for n in (4096, 1024, 1024)]
+    mats = [QMatMul(q4k(weights(rng, n, k))[0]) for n in ns]
     x = upload(activations(rng, rows, k, outliers=True))
     before = lib().qmm_gemm_launches()
     shared = QMatMul.forward_shared(x, mats)
