@@ -153,46 +153,47 @@ struct SpFmt {
 constexpr float kQ6Eff = 4096.0f / 127.0f;
 
 // One thread's 32 values of a Q6_K stage (half `half` of super-block sbx,
-// positions 32 g .. 32 g + 31, the layout of BlockQ6K::to_float,
-// vendor/candle/candle-core/src/quantized/k_quants.rs:2657-2727): 6-bit codes
-// from ql (low or high nibble) and qh (bits 2g, 2g + 1), the multipliers of
-// their two 16-value sub-blocks, into int8 pieces 2g and 2g + 1 of the row.
+// the layout of BlockQ6K::to_float,
+// vendor/candle/candle-core/src/quantized/k_quants.rs:2657-2727): the 16
+// values of sub-block part p of 32-value group c (low nibbles of ql chunk c,
+// qh bits 2c) and of group c + 2 (high nibbles of the same ql bytes, qh bits
+// 2c + 4), into int8 pieces 2c + p and 2c + p + 4 of the row at w0 and w1.
+// The four dwords of each piece are formed in the order rho, rho + 1, ...
+// (rho = (row / 4) mod 4): the 16 rows a wave expands lie 224 bytes apart
+// in LDS, and reading the same dword of each would put them on 8 banks;
+// rotated, they spread over all of them.
 // wr: the row's window in LDS (the block at byte (2 sbx) mod 16 of it).
-__device__ __forceinline__ void build_q6(uint32_t wr, int half, uint32_t w0, uint32_t w1, int sbx, int g) {
+// t: the thread's index (c = bit 1, p = bit 0, its row t / 4).
+__device__ __forceinline__ void build_q6(uint32_t wr, int half, uint32_t w0, uint32_t w1, int sbx, uint32_t t) {
+  const uint32_t c = (t >> 1) & 1u, p = t & 1u, rho = (t >> 4) & 3u;
   const uint32_t boff = (2u * (uint32_t)sbx) & 15u;
   const uint32_t al = boff & 3u;  // 0 or 2: the blocks sit 2-byte aligned in their windows
   const uint32_t wb = wr + (boff & 12u);  // the dword holding the block's first byte
-  const uint32_t ql4 = wb + 64u * (uint32_t)half + 32u * ((uint32_t)g & 1u);
-  const uint32_t qh4 = wb + 128u + 32u * (uint32_t)half;
-  // sub-block scales 8 half + 2g and the next: bytes o and o + 1 past the
-  // scales' first dword (o even and at most 8, so both in the dword at o & ~3)
-  const uint32_t o = al + 2u * (uint32_t)g;
-  const uint32_t scw = lds_ld<uint32_t>(wb + 192u + 8u * (uint32_t)half + (o & ~3u)) >> (8u * (o & 3u));
-  const int sc0 = (int)(int8_t)(scw & 0xFFu), sc1 = (int)(int8_t)((scw >> 8) & 0xFFu);
+  const uint32_t ql4 = wb + 64u * (uint32_t)half + 32u * c + 16u * p;
+  const uint32_t qh4 = wb + 128u + 32u * (uint32_t)half + 16u * p;
+  // sub-block scales 8 half + 2c + p and 8 half + 2c + p + 4: bytes o and
+  // o + 4 past the scales' first dword (o <= 5), the same byte of two dwords
+  const uint32_t o = al + 2u * c + p;
+  const uint32_t sa = wb + 192u + 8u * (uint32_t)half + (o & ~3u);
+  const uint32_t sh = 8u * (o & 3u);
+  const int sc0 = (int)(int8_t)((lds_ld<uint32_t>(sa) >> sh) & 0xFFu);
+  const int sc1 = (int)(int8_t)((lds_ld<uint32_t>(sa + 4u) >> sh) & 0xFFu);
   const int m0 = (127 * sc0 + 8) >> 4, m1 = (127 * sc1 + 8) >> 4;  // round(127 sc / 16)
-  const uint32_t hs = 2u * (uint32_t)g;
-  // the two 16-value sub-blocks in turn (5 dwords of ql and qh each)
+  // per 16-bit lane: m (q - 32) + 128, whose high byte is w8
+  const uint32_t M0 = ((uint32_t)m0 & 0xFFFFu) * 0x10001u, C0 = ((uint32_t)(128 - 32 * m0) & 0xFFFFu) * 0x10001u;
+  const uint32_t M1 = ((uint32_t)m1 & 0xFFFFu) * 0x10001u, C1 = ((uint32_t)(128 - 32 * m1) & 0xFFFFu) * 0x10001u;
+  const uint32_t lsh = 4u - 2u * c, hsh = 2u * c;  // qh bits 2c and 2c + 4 to bits 4-5
 #pragma unroll
-  for (int part = 0; part < 2; part++) {
-    const int m = part ? m1 : m0;
-    // per 16-bit lane: m (q - 32) + 128, whose high byte is w8
-    const uint32_t M = ((uint32_t)m & 0xFFFFu) * 0x10001u, C = ((uint32_t)(128 - 32 * m) & 0xFFFFu) * 0x10001u;
-    uint32_t ql[5], qh[5], out[4];
-#pragma unroll
-    for (int i = 0; i < 5; i++) {
-      ql[i] = lds_ld<uint32_t>(ql4 + 16u * (uint32_t)part + 4u * (uint32_t)i);
-      qh[i] = lds_ld<uint32_t>(qh4 + 16u * (uint32_t)part + 4u * (uint32_t)i);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t lw = __builtin_amdgcn_alignbyte(ql[i + 1], ql[i], al);
-      const uint32_t hw = __builtin_amdgcn_alignbyte(qh[i + 1], qh[i], al);
-      const uint32_t qlv = g < 2 ? (lw & 0x0F0F0F0Fu) : ((lw >> 4) & 0x0F0F0F0Fu);
-      const uint32_t q = qlv | (((hw >> hs) & 0x03030303u) << 4);
-      const uint32_t e = pkmad(q & 0x00FF00FFu, M, C), od = pkmad((q >> 8) & 0x00FF00FFu, M, C);
-      out[i] = __builtin_amdgcn_perm(od, e, 0x07030501u);
-    }
-    lds_st<lds_i4>(part ? w1 : w0, lds_i4{(int)out[0], (int)out[1], (int)out[2], (int)out[3]});
+  for (int i = 0; i < 4; i++) {
+    const uint32_t d4 = 4u * (((uint32_t)i + rho) & 3u);
+    const uint32_t lw = __builtin_amdgcn_alignbyte(lds_ld<uint32_t>(ql4 + d4 + 4u), lds_ld<uint32_t>(ql4 + d4), al);
+    const uint32_t hw = __builtin_amdgcn_alignbyte(lds_ld<uint32_t>(qh4 + d4 + 4u), lds_ld<uint32_t>(qh4 + d4), al);
+    const uint32_t qa = (lw & 0x0F0F0F0Fu) | ((hw << lsh) & 0x30303030u);
+    const uint32_t qb = ((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> hsh) & 0x30303030u);
+    const uint32_t ea = pkmad(qa & 0x00FF00FFu, M0, C0), oa = pkmad((qa >> 8) & 0x00FF00FFu, M0, C0);
+    const uint32_t eb = pkmad(qb & 0x00FF00FFu, M1, C1), ob = pkmad((qb >> 8) & 0x00FF00FFu, M1, C1);
+    lds_st<uint32_t>(w0 + d4, __builtin_amdgcn_perm(oa, ea, 0x07030501u));
+    lds_st<uint32_t>(w1 + d4, __builtin_amdgcn_perm(ob, eb, 0x07030501u));
   }
 }
 
@@ -315,17 +316,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
   };
 
   // ---- expansion of a stage's weights: thread -> (weight row, piece) ----
-  const int bn = tid & (kBN - 1), bpi = tid >> 7;  // 16 consecutive lanes: 16 rows, one piece
+  // Q4_K: 16 consecutive lanes: 16 rows, one piece. Q6_K: 4 consecutive
+  // lanes a row (groups c, c + 2 of sub-block part p), 16 rows a wave.
+  const int bn = Q6 ? tid >> 2 : tid & (kBN - 1), bpi = tid >> 7;
   // lane offsets of the expansion (made opaque once a stage): the raw row,
   // and the two 16-byte pieces it writes in the expanded row
-  const uint32_t plo = Q6 ? 2u * (uint32_t)(wv >> 1) : 4u * ((uint32_t)bpi >> 1) + ((uint32_t)bpi & 1u);
+  const uint32_t plo = Q6 ? (uint32_t)tid & 3u : 4u * ((uint32_t)bpi >> 1) + ((uint32_t)bpi & 1u);
   uint32_t x_raw = (uint32_t)bn * F::kRaw;
   uint32_t x_w0 = (uint32_t)bn * kStage + 16u * (plo ^ swz(bn));
-  uint32_t x_w1 = (uint32_t)bn * kStage + 16u * ((plo + (Q6 ? 1u : 2u)) ^ swz(bn));
+  // (Q6_K: piece plo + 4, x_w0 ^ 64 since plo < 4; formed at each use)
+  uint32_t x_w1 = Q6 ? 0u : (uint32_t)bn * kStage + 16u * ((plo + 2u) ^ swz(bn));
   auto build = [&](const uint8_t* sw, int half, int8_t* sbt, int sbx) {
     const uint32_t wr = lds_addr(sw) + x_raw, bt = lds_addr(sbt);
     if constexpr (Q6) {
-      build_q6(wr, half, bt + x_w0, bt + x_w1, sbx, wv >> 1);
+      build_q6(wr, half, bt + x_w0, bt + (x_w0 ^ 64u), sbx, (uint32_t)tid);
       return;
     }
     const uint4 hdr = lds_ld4(wr);
@@ -438,8 +442,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
     fa[ks] = (uint32_t)arow0 * kStage + pc;
     fb[ks] = (uint32_t)bcol0 * kStage + pc;
   }
+  // (fa[ks] = fa[0] ^ 32 ks: bits 5-6 of a row's offset are its swizzled
+  // K-step; Q6_K forms them so at each use, which keeps 6 registers free)
   auto frag = [&](const int8_t* base, int t2, int ks, bool a_side) -> i4v {
-    return lds_ld<i4v>(lds_addr(base) + (a_side ? fa[ks] : fb[ks]) + 32u * kStage * (uint32_t)t2);
+    const uint32_t f = Q6 ? (a_side ? fa[0] : fb[0]) ^ (32u * (uint32_t)ks) : (a_side ? fa[ks] : fb[ks]);
+    return lds_ld<i4v>(lds_addr(base) + f + 32u * kStage * (uint32_t)t2);
   };
 
   // ---- prologue: row factors, stage 0 ----
@@ -489,13 +496,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
     const bool wmore = half == 0 && sb + 1 < sb1;  // the next super-block's raw weights
     const bool rmore = half == 1 && sb + 1 < sb1;  // the next super-block's row inputs
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
+    for (int ks = 0; ks < (Q6 ? 1 : 4); ks++) {
       opaque(fa[ks]);
       opaque(fb[ks]);
     }
     opaque(x_raw);
     opaque(x_w0);
-    opaque(x_w1);
+    if constexpr (!Q6) opaque(x_w1);
     i4v a0 = frag(sa, 0, 0, true), a1 = frag(sa, 1, 0, true);
     i4v b0 = frag(sbt, 0, 0, false), b1 = frag(sbt, 1, 0, false);
 #pragma unroll
