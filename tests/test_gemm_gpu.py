@@ -217,13 +217,15 @@ def test_q4k_gemm_cut_along_k(n, rows):
     assert err <= TIGHT_SP, err
 
 
-@pytest.mark.parametrize("ns", [(4096, 1024, 1024), (4096, 4096), (4096, 4096, 4096, 4096), (2048, 2048)])
+@pytest.mark.parametrize("ns", [(4096, 1024, 1024), (4096, 4096), (4096, 4096, 4096, 4096), (2048, 2048),
+                                (14336, 14336)])
 def test_q4k_gemm_cut_along_k_shared_equals_forward(ns):
     """Weights sharing one launch at M = 512 give each weight's own forward
     bits: a weight's K split does not depend on the weights sharing its
     launch, nor on how many of a tile's splits one workgroup computes (q+k+v
     and the 4096-row pairs and quadruples have more split workgroups than
-    CUs, so workgroups there take 2 or 4 consecutive splits)."""
+    CUs, so workgroups there take 2 or 4 consecutive splits; gate+up's 448
+    unsplit tiles run as they do alone)."""
     k, rows = 4096, 512
     rng = np.random.default_rng(15)
     mats = [QMatMul(q4k(weights(rng, n, k))[0]) for n in ns]
