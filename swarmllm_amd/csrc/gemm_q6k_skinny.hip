@@ -37,8 +37,24 @@ namespace qmm {
 namespace {
 
 typedef int i4v __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// two 16-bit multiply-adds in one instruction (v_pk_mad_u16)
+__device__ __forceinline__ uint32_t pkmad16(uint32_t a, uint32_t b, uint32_t c) {
+  const u16x2 x = __builtin_bit_cast(u16x2, a), y = __builtin_bit_cast(u16x2, b), z = __builtin_bit_cast(u16x2, c);
+  return __builtin_bit_cast(uint32_t, x * y + z);
+}
+// ONE: the weight as w8 = round(m_j (q - 32) / 256) with m_j = round(127
+// sc_j / 16), so sc_j (q - 32) ~ (4096 / 127) w8 (the single-pass GEMM's
+// form, gemm_q4k_sp.hip): one product a 64-deep chunk instead of five
+constexpr float kQ6One = 4096.0f / 127.0f;
 
 constexpr int kQ6Win = 224;  // bytes staged a row: 14 pieces cover the 210-byte block at any offset
+// LDS bytes between staged rows: 57 dwords, so the same dword of the 16 rows
+// a read spans falls on 16 different banks (at 224 bytes, 56 dwords, the 16
+// rows share 4 of them and each of the block's dword reads waited 4 times as
+// long). The pieces are then only 4-byte aligned and go in as dwords.
+constexpr int kQ6Row = kQ6Win + 4;
 
 template <int NB>
 struct Q6Pieces {
@@ -53,14 +69,14 @@ struct Q6Act {
   float dy[MT][4];
 };
 
-template <int MT, int NB, int kWaves>
+template <int MT, int NB, int kWaves, bool ONE>
 __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets tg, int nsb,
                                                                       const int8_t* __restrict__ yq,
                                                                       const float* __restrict__ yd, int M) {
   constexpr int ROWS = 16 * NB;
   using Pieces = Q6Pieces<NB>;
   constexpr int L = Pieces::L;
-  constexpr int kBuf = ROWS * kQ6Win + 16 > NB * MT * 4 * 64 * 4 ? ROWS * kQ6Win + 16 : NB * MT * 4 * 64 * 4;
+  constexpr int kBuf = ROWS * kQ6Row + 16 > NB * MT * 4 * 64 * 4 ? ROWS * kQ6Row + 16 : NB * MT * 4 * 64 * 4;
   __shared__ __attribute__((aligned(16))) uint8_t sbuf[kWaves][kBuf];
 
   const int lane = threadIdx.x & 63;
@@ -111,7 +127,11 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
     for (int t = 0; t < L; t++) {
       const int p = lane + 64 * t;
       const int pp = p < Pieces::P ? p : Pieces::P - 1;
-      *(uint4*)(buf + (pp / 14) * kQ6Win + 16 * (pp % 14)) = pc.v[t];
+      uint32_t* const d = (uint32_t*)(buf + (pp / 14) * kQ6Row + 16 * (pp % 14));
+      d[0] = pc.v[t].x;
+      d[1] = pc.v[t].y;
+      d[2] = pc.v[t].z;
+      d[3] = pc.v[t].w;
     }
   };
   // the block offset of the lane's own rows within their staged windows
@@ -157,7 +177,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
   auto compute = [&](const Q6Act<MT>& act, int sb) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-      const uint8_t* rowp = buf + (16 * b + r16) * kQ6Win;
+      const uint8_t* rowp = buf + (16 * b + r16) * kQ6Row;
       const int o = (rlo[b] + 210 * sb) & 15;
       uint32_t ql[2][4], qh[2][4], scw[4];
       lds_words<4>(rowp, o + 16 * kq, ql[0]);
@@ -167,8 +187,40 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
       lds_words<4>(rowp, o + 192, scw);
       const float dw = h2f((uint16_t)lds_u16(rowp, o + 208));
 
-      i4v tot[MT], S[MT];
       const i4v zero = {0, 0, 0, 0};
+      if constexpr (ONE) {
+        i4v T[MT];
+#pragma unroll
+        for (int m = 0; m < MT; m++) T[m] = zero;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const int hh = c >> 1, nib = 4 * (c & 1);
+          const int qsh = 4 * (c & 1) + 2 * (kq >> 1);
+          // this lane's group 4c + L/16 of its weight row: multiplier m and
+          // per 16-bit lane m (q - 32) + 128, whose high byte is w8
+          const int sc = (int)(int8_t)((scw[c] >> (8 * kq)) & 0xFF);
+          const int mj = (127 * sc + 8) >> 4;
+          const uint32_t Mw = ((uint32_t)mj & 0xFFFFu) * 0x10001u, Cw = ((uint32_t)(128 - 32 * mj) & 0xFFFFu) * 0x10001u;
+          i4v w8;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const uint32_t q = ((ql[hh][e] >> nib) & 0x0F0F0F0Fu) | (((qh[hh][e] >> qsh) & 0x03030303u) << 4);
+            const uint32_t ev = pkmad16(q & 0x00FF00FFu, Mw, Cw), od = pkmad16((q >> 8) & 0x00FF00FFu, Mw, Cw);
+            w8[e] = (int)__builtin_amdgcn_perm(od, ev, 0x07030501u);
+          }
+#pragma unroll
+          for (int m = 0; m < MT; m++) T[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(act.a[m][c], w8, T[m], 0, 0, 0);
+        }
+        // |T| <= 256 * 127 * 127 < 2^24: exact in f32
+        const float dq = __fmul_rn(dw, kQ6One);
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc[b][m][i] = __fadd_rn(acc[b][m][i], __fmul_rn(__fmul_rn(dq, act.dy[m][i]), (float)T[m][i]));
+        continue;
+      }
+      i4v tot[MT], S[MT];
 #pragma unroll
       for (int m = 0; m < MT; m++) tot[m] = zero;
 #pragma unroll
@@ -283,12 +335,12 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
   }
 }
 
-template <int MT, int NB, int W>
+template <int MT, int NB, int W, bool ONE>
 hipError_t launch_q6(const MvTargets& t, int nsb, const ActPlanes& p, int64_t rows, hipStream_t st) {
   QMM_NOTE_LAUNCH();
   const int64_t n_total = t.row_end[t.count - 1];
   const dim3 grid((unsigned)((n_total + 16 * NB - 1) / (16 * NB)));
-  gemm_q6k_skinny_kernel<MT, NB, W><<<grid, 64 * W, 0, st>>>(t, nsb, p.codes, p.d, (int)rows);
+  gemm_q6k_skinny_kernel<MT, NB, W, ONE><<<grid, 64 * W, 0, st>>>(t, nsb, p.codes, p.d, (int)rows);
   return hipGetLastError();
 }
 
@@ -300,8 +352,14 @@ hipError_t launch_gemm_q6k_skinny(const MvTargets& t, int64_t k, const ActPlanes
                                   hipStream_t st) {
   (void)cus;
   const int nsb = (int)(k / 256);
-  if (rows <= 16) return launch_q6<1, 1, 4>(t, nsb, p, rows, st);
-  return launch_q6<2, 1, 4>(t, nsb, p, rows, st);
+  // the single-product form from k = 2048 (its rounding stays well inside
+  // the 2e-3 bound there); shorter rows keep the exact form
+  if (k >= 2048) {
+    if (rows <= 16) return launch_q6<1, 1, 4, true>(t, nsb, p, rows, st);
+    return launch_q6<2, 1, 4, true>(t, nsb, p, rows, st);
+  }
+  if (rows <= 16) return launch_q6<1, 1, 4, false>(t, nsb, p, rows, st);
+  return launch_q6<2, 1, 4, false>(t, nsb, p, rows, st);
 }
 
 }  // namespace qmm

@@ -344,10 +344,17 @@ def test_q4k_skinny_shared_activation_equals_forward(rows):
 
 
 # ---------------------------------------------------------------------------
-# the Q6_K few-row matrix-core kernel: every inner sum an exact int32, so the
-# gap to the oracle is the order of the f32 scaling (~1e-7)
+# the Q6_K few-row matrix-core kernel: below k = 2048 every inner sum an exact
+# int32, so the gap to the oracle is the order of the f32 scaling (~1e-7);
+# from k = 2048 the weight enters as w8 = round(m_j (q - 32) / 256), one
+# product a chunk, held to 1e-3 (the GEMM bound is 2e-3)
 # ---------------------------------------------------------------------------
 TIGHT_Q6K = 1e-5
+ONE_Q6K = 1e-3
+
+
+def q6k_skinny_bound(k):
+    return ONE_Q6K if k >= 2048 else TIGHT_Q6K
 
 Q6K_SKINNY_SHAPES = [  # (k, n, rows): past the 2 MiB line at 4-8 rows; rows of 3 and 5 super-blocks
     # (210-byte blocks at every 2-byte offset); ragged n; one and two 16-row tiles
@@ -374,7 +381,7 @@ def test_q6k_skinny_parity(k, n, rows):
     want = qref.matmul(qref.Q6_K, x, wq, n)
     wdeq = qref.to_float(qref.Q6_K, wq, n * k).reshape(n, k)
     err = normalised_error(y, want, wdeq, x)
-    assert err <= TIGHT_Q6K, f"k={k} n={n} rows={rows}: {err}"
+    assert err <= q6k_skinny_bound(k), f"k={k} n={n} rows={rows}: {err}"
 
 
 @pytest.mark.parametrize("rows", [8, 16])
@@ -388,7 +395,7 @@ def test_q6k_skinny_c5_down_projection(rows):
     y = QMatMul(qt).forward(upload(x)).cpu().numpy()
     want = qref.matmul(qref.Q6_K, x, wq, 8192)
     wdeq = qref.to_float(qref.Q6_K, wq, 8192 * 28672).reshape(8192, 28672)
-    assert normalised_error(y, want, wdeq, x) <= TIGHT_Q6K
+    assert normalised_error(y, want, wdeq, x) <= ONE_Q6K
 
 
 def test_q6k_skinny_shared_activation_equals_forward():
