@@ -284,15 +284,14 @@ def test_forward_shared_equals_forward(name, rows):
         assert torch.equal(y, m.forward(x))
 
 
-@pytest.mark.parametrize("k", [256, 1024, 4096, 8192, 14336, 16384])
-@pytest.mark.parametrize("rows", [1, 2])
+# (two rows stream, and quantize in the kernel, up to k = 8192)
+@pytest.mark.parametrize("k,rows", [(k, 1) for k in (256, 1024, 4096, 8192, 14336, 16384)] +
+                         [(k, 2) for k in (256, 1024, 4096, 8192)])
 def test_q4k_in_kernel_quantization_matches_standalone(k, rows):
     """The decode kernel quantizing its activation in LDS gives the same bits
     as the same kernel reading the standalone quantizer's planes (which are
     bit-exact to BlockQ8K::from_float): the in-kernel quantization is that
     quantization. Also within tolerance of the oracle."""
-    if rows == 2 and k > 8192:
-        pytest.skip("two rows stream up to k = 8192")
     n = 300
     rng = np.random.default_rng(k + rows)
     w = weights(rng, n, k)
