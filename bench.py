@@ -920,10 +920,26 @@ def profile_only(which: str, layers, outs, stream, reps: int) -> None:
         torch.cuda.synchronize()
         log(f"profile dominant: {reps} gate+up launches over {len(layers)} copies")
         return
-    name = "down" if which == "prefill_down" else "gate"
+    name = "down" if which in ("prefill_down", "prefill_down_forward") else "gate"
     t, n, k = {nm: (tt, nn, kk) for nm, tt, nn, kk in LAYER}[name]
     M = 512
     xq, out = prefill_inputs(M, n, k)
+    if which == "prefill_down_forward":
+        # the down product as the C3 layer runs it: qmm_forward with its
+        # planned workspace (quantizer, the GEMM cut along K, the slot sum)
+        from swarmllm_amd import fill_normal
+
+        x = fill_normal(M * k, seed=(3 << 40) | 0xB1).reshape(M, k)
+        need = ctypes.c_size_t(0)
+        check("qmm_forward", L.qmm_forward(t, None, None, k, None, n, None, 0, ctypes.byref(need), k, n, M, 0, 0))
+        ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device="cuda")
+        for i in range(reps):
+            lay = layers[i % len(layers)]
+            check("qmm_forward", L.qmm_forward(t, lay.w[name].data_.data_ptr(), x.data_ptr(), k, out.data_ptr(), n,
+                                               ws.data_ptr(), ws.numel(), ctypes.byref(need), k, n, M, 1, s))
+        torch.cuda.synchronize()
+        log(f"profile {which}: {reps} qmm_forward products over {len(layers)} copies")
+        return
     for i in range(reps):
         lay = layers[i % len(layers)]
         check("qmm_matmul", L.qmm_matmul(t, lay.w[name].data_.data_ptr(), xq.data_ptr(), out.data_ptr(), n, k,
@@ -990,7 +1006,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="skip the C1 / C4 / C5 sections")
-    ap.add_argument("--profile", choices=["single", "dominant", "prefill", "prefill_down", "copy"],
+    ap.add_argument("--profile", choices=["single", "dominant", "prefill", "prefill_down", "prefill_down_forward", "copy"],
                     help="launch only this kernel --steps times (for rocprofv3 counter passes), print no JSON")
     args = ap.parse_args()
 
