@@ -179,20 +179,22 @@ def plan_bytes(qt, k, n, rows):
     return need.value
 
 
-@pytest.mark.parametrize("n,rows", [(1024, 512), (4096, 512), (200, 300)])
-def test_q4k_gemm_cut_along_k(n, rows):
+# (n, rows, k): cut in 4 (k = 4096), and in 2 (k = 2048 and 6144: parts of at
+# least 4 super-blocks, a whole number of pairs each)
+@pytest.mark.parametrize("n,rows,k", [(1024, 512, 4096), (4096, 512, 4096), (200, 300, 4096), (1024, 512, 2048),
+                                      (512, 300, 6144)])
+def test_q4k_gemm_cut_along_k(n, rows, k):
     """Products whose tiles fill at most half the CUs (q/k/v/o of a prefill)
     are cut along K when the workspace holds the split slots (forward plans
-    them): each part writes its partial tile to a slot and the last part to
-    finish adds the slots in part order. Against the oracle; bit-identical
-    run to run; within 1e-5 of the uncut product from the same quantized
+    them): each part writes its partial tile to a slot and a second launch
+    adds the slots in part order. Against the oracle; bit-identical run to
+    run; within 1e-5 of the uncut product from the same quantized
     activation (qmm_matmul: the same integers and f32 steps, only the order
     of the partial sums differs)."""
     from swarmllm_amd import _lib
     from swarmllm_amd.qtensor import quantize_act
 
-    k = 4096
-    rng = np.random.default_rng(zlib.crc32(f"gemm-split-{n}-{rows}".encode()))
+    rng = np.random.default_rng(zlib.crc32(f"gemm-split-{n}-{rows}-{k}".encode()))
     w = weights(rng, n, k)
     x = activations(rng, rows, k, outliers=True)
     qt, wq = q4k(w)
