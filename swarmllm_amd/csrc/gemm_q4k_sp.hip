@@ -332,8 +332,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
       build_q6(wr, half, bt + x_w0, bt + (x_w0 ^ 64u), sbx, (uint32_t)tid);
       return;
     }
+    // both reads in flight together: the second address is formed (opaque)
+    // before the first read, else the compiler put it in the register of the
+    // first read's unused dword 0 and waited for that read before issuing it
+    uint32_t ra = wr + 16u * (uint32_t)(1 + 4 * half + bpi);
+    opaque(ra);
     const uint4 hdr = lds_ld4(wr);
-    const uint4 raw = lds_ld4(wr + 16u * (uint32_t)(1 + 4 * half + bpi));
+    const uint4 raw = lds_ld4(ra);
     // 6-bit scales of sub-blocks 4 half + 2 (bpi >> 1) and the next
     // (get_scale_min_k4, vendor/candle/candle-core/src/quantized/utils.rs:50-60)
     const uint32_t scw = half == 0 ? (hdr.y & 0x3f3f3f3fu)
