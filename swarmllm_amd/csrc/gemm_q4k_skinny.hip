@@ -33,6 +33,7 @@
 // One launch covers up to kMaxTargets weights sharing the activation (q/k/v,
 // gate/up): their rows are numbered one after another. Rows past a target's
 // end, and activation rows past M, are read clamped and never stored.
+#include "lds_copy.h"
 #include "mv_common.h"
 
 namespace qmm {
@@ -309,6 +310,257 @@ hipError_t launch_sk(const MvTargets& t, int nsb, const ActPlanes& p, int64_t ro
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// The same product for wide weights, its weights and activation copied
+// straight to LDS (global_load_lds), SBS super-blocks of each row a stage,
+// two stages in flight. A wave owns a 16-row tile over the whole of K (no sum
+// across waves); the 4 waves of a workgroup share each stage's activation.
+// The copies read SBS x 144 contiguous bytes of a row at once, which HBM
+// streams faster than the 144-byte pieces of the register-staged kernel
+// (plain reads of C5's gate+up: 4.3 TB/s in 144-byte pieces of 32 rows,
+// 5.8 in 288-byte pieces of 16). Tiles are numbered weight after weight, so
+// a tile never spans two weights; a ragged last tile reads its weight's last
+// row again and stores only its own rows.
+// ---------------------------------------------------------------------------
+template <int MT, int SBS>
+struct SkDma {
+  static constexpr int kWSlots = 9 * SBS + 1;                  // 16-byte slots a staged weight row (+1: banks)
+  static constexpr int kWCopies = (16 * kWSlots + 63) / 64;    // a wave's weight copies a stage
+  static constexpr int kWStage = kWCopies * 1024;
+  static constexpr int AR = 16 * MT;                           // activation rows staged
+  static constexpr int kASlots = 16 * SBS + 1;                 // slots a staged activation row (+1: banks)
+  static constexpr int kACopies = (AR * kASlots + 255) / 256;  // a wave's activation copies a stage
+  static constexpr int kAStage = 4 * kACopies * 1024;
+  static constexpr int kDStage = 4 * 256;                      // dy: one dword copy a wave (AR x SBS used)
+  static constexpr int kStage = 4 * kWStage + kAStage + kDStage;
+  static constexpr int kCopies = kWCopies + kACopies + 1;      // copies a wave issues a stage
+  static_assert(AR * SBS <= 256, "dy of a stage fits the four dword copies");
+  static_assert(kCopies <= 63, "vmcnt");
+};
+
+struct SkDmaArgs {
+  MvTargets tg;
+  int tile_end[kMaxTargets];  // 16-row tiles of weights 0..t
+};
+
+// A workgroup barrier that waits for nothing but (with lds) the wave's own
+// LDS reads: __syncthreads' release fence would also wait for every copy in
+// flight, the next stage's included.
+template <bool kLds>
+__device__ __forceinline__ void copy_barrier() {
+  if (kLds) __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  // s_waitcnt vmcnt(N), the other counters left alone (gfx9 encoding)
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int MT, int SBS>
+__global__ __launch_bounds__(256) void gemm_q4k_skinny_dma_kernel(const SkDmaArgs a, int nsb,
+                                                                  const int8_t* __restrict__ yq,
+                                                                  const float* __restrict__ yd, int M) {
+  using D = SkDma<MT, SBS>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+  const bool hin = kq >= 2;
+  const int hb = 16 * (kq & 1);
+  const uint32_t K = (uint32_t)nsb * 256u;
+  const uint32_t rowbytes = (uint32_t)nsb * 144u;
+
+  // the wave's tile: weight t (selects: a dynamic index into the argument
+  // arrays would copy them to private memory), its first row there
+  const int tile = (int)blockIdx.x * 4 + wv;
+  const bool live = tile < a.tile_end[kMaxTargets - 1];
+  // (a dead tile of the last workgroup copies rows of the last weight)
+  const int t = !live ? a.tg.count - 1
+                      : tile < a.tile_end[0] ? 0 : tile < a.tile_end[1] ? 1 : tile < a.tile_end[2] ? 2 : 3;
+  auto pick = [&](const auto& arr) { return t == 0 ? arr[0] : t == 1 ? arr[1] : t == 2 ? arr[2] : arr[3]; };
+  const int tb = t == 0 ? 0 : t == 1 ? a.tile_end[0] : t == 2 ? a.tile_end[1] : a.tile_end[2];
+  const int64_t wbeg = t == 0 ? 0 : t == 1 ? a.tg.row_end[0] : t == 2 ? a.tg.row_end[1] : a.tg.row_end[2];
+  const int64_t wrows = pick(a.tg.row_end) - wbeg;
+  const int64_t r0 = live ? (int64_t)(tile - tb) * 16 : 0;  // within weight t
+  const uint8_t* __restrict__ W = (const uint8_t*)pick(a.tg.w);
+
+  // per-lane copy offsets (fixed over the stages; the stage adds its
+  // super-block to the uniform base)
+  uint32_t woff[D::kWCopies];
+#pragma unroll
+  for (int u = 0; u < D::kWCopies; u++) {
+    const int sl = 64 * u + lane;
+    const int row = sl / D::kWSlots, q = sl - row * D::kWSlots;
+    int64_t gr = r0 + (row < 16 ? row : 0);
+    gr = gr < wrows ? gr : wrows - 1;
+    woff[u] = (uint32_t)gr * rowbytes + 16u * (uint32_t)(q < 9 * SBS ? q : 0);
+  }
+  uint32_t aoff[D::kACopies];
+#pragma unroll
+  for (int u = 0; u < D::kACopies; u++) {
+    const int sl = 64 * (wv * D::kACopies + u) + lane;
+    const int row = sl / D::kASlots, q = sl - row * D::kASlots;
+    const int ar = row < D::AR ? (row < M ? row : M - 1) : 0;
+    aoff[u] = (uint32_t)ar * K + 16u * (uint32_t)(q < 16 * SBS ? q : 0);
+  }
+  uint32_t doff;
+  {
+    const int d = 64 * wv + lane;
+    const int row = d / SBS, j = d - row * SBS;
+    const int ar = row < D::AR ? (row < M ? row : M - 1) : 0;
+    doff = 4u * ((uint32_t)ar * (uint32_t)nsb + (uint32_t)j);
+  }
+  auto issue = [&](int st, int sb) {
+    uint8_t* const base = smem + st * D::kStage;
+#pragma unroll
+    for (int u = 0; u < D::kWCopies; u++)
+      dma16(W + 144 * (int64_t)sb, woff[u], lds_addr(base + wv * D::kWStage + 1024 * u));
+#pragma unroll
+    for (int u = 0; u < D::kACopies; u++)
+      dma16(yq + 256 * (int64_t)sb, aoff[u], lds_addr(base + 4 * D::kWStage + 1024 * (wv * D::kACopies + u)));
+    dma4(yd + sb, doff, lds_addr(base + 4 * D::kWStage + D::kAStage + 256 * wv));
+  };
+
+  float accD[MT][4], accM[MT][4];
+#pragma unroll
+  for (int m = 0; m < MT; m++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) accD[m][i] = accM[m][i] = 0.0f;
+
+  // one super-block j of stage st: both passes, the min pass, the f32 epilogue
+  // (the register-staged kernel's arithmetic)
+  auto compute1 = [&](int st, int j) {
+    const uint8_t* const base = smem + st * D::kStage;
+    const uint8_t* rowp = base + wv * D::kWStage + r16 * (16 * D::kWSlots) + 144 * j;
+    const uint4 hdr = *(const uint4*)rowp;
+    uint4 code[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) code[c] = *(const uint4*)(rowp + 16 + 32 * c + hb);
+    i4v am[MT][4];
+    float dy[MT][4];
+    const uint8_t* const ab = base + 4 * D::kWStage;
+    const float* const db = (const float*)(ab + D::kAStage);
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        am[m][c] = *(const i4v*)(ab + (16 * m + r16) * (16 * D::kASlots) + 256 * j + 64 * c + 16 * kq);
+#pragma unroll
+      for (int i = 0; i < 4; i++) dy[m][i] = db[(16 * m + 4 * kq + i) * SBS + j];
+    }
+    // scales and mins (get_scale_min_k4, utils.rs:50-60)
+    const uint32_t u0 = hdr.y, u1 = hdr.z, u2 = hdr.w;
+    const uint32_t s03 = u0 & 0x3f3f3f3fu, m03 = u1 & 0x3f3f3f3fu;
+    const uint32_t s47 = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+    const uint32_t m47 = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+    const float dw = h2f((uint16_t)(hdr.x & 0xFFFF));
+    const float dmin = h2f((uint16_t)(hdr.x >> 16));
+    i4v T[MT], Tm[MT];
+    const i4v zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int sj = 2 * c + (hin ? 1 : 0);
+        const uint32_t scv = ((sj < 4 ? s03 : s47) >> (8 * (sj & 3))) & 0xFF;
+        const uint32_t f = sk_dup16(pass == 0 ? scv >> 3 : scv & 7);
+        i4v bq;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t w = sk_word(code[c], e);
+          bq[e] = (int)sk_pkmul(hin ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu, f);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+          T[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[m][c], bq, (pass == 0 && c == 0) ? zero : T[m], 0, 0, 0);
+      }
+      if (pass == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) T[m][i] <<= 3;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int sj = 2 * c + (hin ? 1 : 0);
+      const uint32_t mv = ((sj < 4 ? m03 : m47) >> (8 * (sj & 3))) & 0xFF;
+      const int mb = (int)(mv * 0x01010101u);
+      const i4v bm = {mb, mb, mb, mb};
+#pragma unroll
+      for (int m = 0; m < MT; m++)
+        Tm[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[m][c], bm, c == 0 ? zero : Tm[m], 0, 0, 0);
+    }
+#pragma unroll
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        accD[m][i] = __fadd_rn(accD[m][i], __fmul_rn(__fmul_rn(dw, dy[m][i]), (float)T[m][i]));
+        accM[m][i] = __fadd_rn(accM[m][i], __fmul_rn(__fmul_rn(dmin, dy[m][i]), (float)Tm[m][i]));
+      }
+  };
+
+  // every wave issues the same copies every stage (a dead tile's copies read
+  // its weight's rows, clamped), so vmcnt counts whole stages
+  const int nst = nsb / SBS;
+  issue(0, 0);
+  if (nst > 1) issue(1, SBS);
+  for (int s = 0; s < nst; s++) {
+    if (s + 1 < nst)
+      wait_vm<D::kCopies>();
+    else
+      wait_vm<0>();
+    copy_barrier<false>();  // every wave's copies of stage s are in LDS
+#pragma unroll
+    for (int j = 0; j < SBS; j++) compute1(s & 1, j);
+    copy_barrier<true>();  // stage s read by every wave before its buffer is refilled
+    if (s + 2 < nst) issue(s & 1, (s + 2) * SBS);
+  }
+  if (!live) return;
+  float* const out = pick(a.tg.dst) + r0 + r16;
+  const int64_t ldd = pick(a.tg.ldd);
+  if (r0 + r16 < wrows) {
+#pragma unroll
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int ar = 16 * m + 4 * kq + i;
+        if (ar < M) out[(int64_t)ar * ldd] = __fsub_rn(accD[m][i], accM[m][i]);
+      }
+  }
+}
+
+template <int MT, int SBS>
+hipError_t launch_sk_dma(const MvTargets& t, int nsb, const ActPlanes& p, int64_t rows, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  using D = SkDma<MT, SBS>;
+  SkDmaArgs a{};
+  a.tg = t;
+  int tiles = 0;
+  for (int i = 0; i < kMaxTargets; i++) {
+    if (i < t.count) {
+      const int64_t n = t.row_end[i] - (i ? t.row_end[i - 1] : 0);
+      tiles += (int)((n + 15) / 16);
+    }
+    a.tile_end[i] = tiles;
+  }
+  // unused entries repeat the last weight (no tiles of their own)
+  for (int i = t.count; i < kMaxTargets; i++) {
+    a.tg.w[i] = t.w[t.count - 1];
+    a.tg.dst[i] = t.dst[t.count - 1];
+    a.tg.ldd[i] = t.ldd[t.count - 1];
+    a.tg.row_end[i] = t.row_end[t.count - 1];
+  }
+  const size_t lds = 2 * (size_t)D::kStage;
+  auto* kfn = &gemm_q4k_skinny_dma_kernel<MT, SBS>;
+  if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+  kfn<<<dim3((unsigned)((tiles + 3) / 4)), 256, lds, st>>>(a, nsb, p.codes, p.d, (int)rows);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 int gemm_q4k_skinny_max_rows() { return 32; }
@@ -317,15 +569,49 @@ bool gemm_q4k_skinny_fits(int64_t k, int64_t rows) {
   return k % 256 == 0 && rows >= 1 && rows <= 32;
 }
 
-// Two 16-row weight tiles a workgroup where the rows fill the CUs twice
-// over, else one; the super-blocks split over 4 waves.
-hipError_t launch_gemm_q4k_skinny(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, int cus,
-                                  hipStream_t st) {
-  const int nsb = (int)(k / 256);
+// the register-staged kernel (one or two 16-row tiles a workgroup, the
+// super-blocks split over 4 waves)
+static hipError_t launch_gemm_q4k_skinny_reg(const MvTargets& t, int nsb, const ActPlanes& p, int64_t rows, int cus,
+                                             hipStream_t st) {
+  // two 16-row tiles a workgroup where the rows fill the CUs twice over
   const int64_t n_total = t.row_end[t.count - 1];
   const bool wide = n_total >= (int64_t)cus * 32 * 2;
   if (rows <= 16) return wide ? launch_sk<1, 2, 4>(t, nsb, p, rows, st) : launch_sk<1, 1, 4>(t, nsb, p, rows, st);
   return wide ? launch_sk<2, 2, 4>(t, nsb, p, rows, st) : launch_sk<2, 1, 4>(t, nsb, p, rows, st);
+}
+
+hipError_t launch_gemm_q4k_skinny(const MvTargets& t, int64_t k, const ActPlanes& p, int64_t rows, int cus,
+                                  hipStream_t st) {
+  const int nsb = (int)(k / 256);
+  // weights of at least 64 rows a CU (C5's gate and up) take the
+  // copy-staged kernel, two super-blocks a stage (C5 at 8 / 16 rows: 6.75 /
+  // 7.68 -> 6.68 / 7.30 ms a forward; four a stage hold 122 KiB of LDS, one
+  // workgroup a CU, 7.51 / 8.19; one a stage 6.75 / 7.41); the choice is each
+  // weight's own, so a weight's bits do not depend on the weights it shares
+  // a launch with
+  constexpr int kDmaSbs = 2;
+  MvTargets wide{}, narrow{};
+  if (rows <= 16 && nsb % kDmaSbs == 0) {
+    int64_t prev = 0, we = 0, ne = 0;
+    for (int i = 0; i < t.count; i++) {
+      const int64_t n = t.row_end[i] - prev;
+      prev = t.row_end[i];
+      MvTargets& g = n >= (int64_t)64 * cus ? wide : narrow;
+      int64_t& e = n >= (int64_t)64 * cus ? we : ne;
+      e += n;
+      g.w[g.count] = t.w[i];
+      g.dst[g.count] = t.dst[i];
+      g.ldd[g.count] = t.ldd[i];
+      g.row_end[g.count] = e;
+      g.count++;
+    }
+    if (wide.count > 0) {
+      const hipError_t e1 = launch_sk_dma<1, kDmaSbs>(wide, nsb, p, rows, st);
+      if (e1 != hipSuccess || narrow.count == 0) return e1;
+      return launch_gemm_q4k_skinny_reg(narrow, nsb, p, rows, cus, st);
+    }
+  }
+  return launch_gemm_q4k_skinny_reg(t, nsb, p, rows, cus, st);
 }
 
 }  // namespace qmm

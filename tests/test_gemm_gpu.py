@@ -345,6 +345,22 @@ def test_q4k_skinny_shared_activation_equals_forward(rows):
         assert torch.equal(y, m.forward(x))
 
 
+@pytest.mark.parametrize("rows", [8, 16])
+def test_q4k_skinny_wide_weights_shared_equals_forward(rows):
+    """C5's gate and up (28672 x 8192 each, at least 64 rows a CU: the
+    copy-staged kernel) plus a narrow weight through one qmm_forward_shared
+    give each weight's own forward bits: the kernel is chosen per weight."""
+    from swarmllm_amd import GgmlDType, fill_normal
+
+    k = 8192
+    mats = [QMatMul(QTensor.quantize(fill_normal(n * k, seed=90 + i, std=0.02).reshape(n, k), GgmlDType.Q4K))
+            for i, n in enumerate((28672, 28672, 1024))]
+    x = fill_normal(rows * k, seed=99).reshape(rows, k)
+    shared = QMatMul.forward_shared(x, mats)
+    for m, y in zip(mats, shared):
+        assert torch.equal(y, m.forward(x))
+
+
 # ---------------------------------------------------------------------------
 # the Q6_K few-row matrix-core kernel: below k = 2048 every inner sum an exact
 # int32, so the gap to the oracle is the order of the f32 scaling (~1e-7);
