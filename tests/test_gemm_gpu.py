@@ -317,10 +317,11 @@ def test_q4k_small_weight_few_rows_stay_on_the_decode_kernels():
     assert L.qmm_gemm_launches() == before
 
 
-@pytest.mark.parametrize("rows", [8, 16])
+@pytest.mark.parametrize("rows", [4, 8, 13, 16])
 def test_q4k_skinny_c5_gate_projection(rows):
-    """BASELINE C5's gate projection (28672 x 8192 Q4_K) at the
-    speculative-verification widths."""
+    """BASELINE C5's gate projection (28672 x 8192 Q4_K, a wide weight: the
+    copy-staged kernel) at the speculative-verification widths and at the
+    few-rows line's 4 rows and a ragged 13."""
     rng = np.random.default_rng(50 + rows)
     w = weights(rng, 28672, 8192)
     x = activations(rng, rows, 8192)
@@ -345,7 +346,7 @@ def test_q4k_skinny_shared_activation_equals_forward(rows):
         assert torch.equal(y, m.forward(x))
 
 
-@pytest.mark.parametrize("rows", [8, 16])
+@pytest.mark.parametrize("rows", [4, 8, 16])
 def test_q4k_skinny_wide_weights_shared_equals_forward(rows):
     """C5's gate and up (28672 x 8192 each, at least 64 rows a CU: the
     copy-staged kernel) plus a narrow weight through one qmm_forward_shared
