@@ -924,9 +924,9 @@ def profile_only(which: str, layers, outs, stream, reps: int) -> None:
     t, n, k = {nm: (tt, nn, kk) for nm, tt, nn, kk in LAYER}[name]
     M = 512
     xq, out = prefill_inputs(M, n, k)
-    if which == "prefill_down_forward":
-        # the down product as the C3 layer runs it: qmm_forward with its
-        # planned workspace (quantizer, the GEMM cut along K, the slot sum)
+    if which in ("prefill_forward", "prefill_down_forward"):
+        # the product as the C3 layer runs it: qmm_forward with its planned
+        # workspace (quantizer, the GEMM, cut along K where planned, the slot sum)
         from swarmllm_amd import fill_normal
 
         x = fill_normal(M * k, seed=(3 << 40) | 0xB1).reshape(M, k)
@@ -1006,7 +1006,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="skip the C1 / C4 / C5 sections")
-    ap.add_argument("--profile", choices=["single", "dominant", "prefill", "prefill_down", "prefill_down_forward", "copy"],
+    ap.add_argument("--profile", choices=["single", "dominant", "prefill", "prefill_forward", "prefill_down",
+                                          "prefill_down_forward", "copy"],
                     help="launch only this kernel --steps times (for rocprofv3 counter passes), print no JSON")
     args = ap.parse_args()
 
