@@ -141,6 +141,28 @@ int qmm_mmq_captured(void);
 void qmm_set_force_dmmv(int on);
 int qmm_force_dmmv(void);
 
+/* Set-up a product's first launch would otherwise do, done ahead of a HIP
+ * graph capture: the current device's properties, the LDS limit of every
+ * kernel of the library that asks for more than 64 KiB, and the
+ * no-allocation scratch's address (qmm_forward_noalloc). Launches nothing.
+ * On a stream being captured, a product of at most qmm_matvec_max_rows()
+ * rows takes a matrix-core kernel only once its type is prepared on the
+ * current device (else the decode kernels serve it); the first such product
+ * outside a capture prepares its type itself. Returns QMM_UNSUPPORTED for a
+ * type not covered, QMM_NO_TILE off gfx950. qmm_prepared: 1 once `type` is
+ * prepared on the current device. Replaces swarm_mmq_prepare_few_rows
+ * (mmq_entry.cu:204-223) as mmq_prepare_few_rows_once calls it
+ * (quantized/cuda.rs:890-932). */
+int qmm_prepare(int type);
+int qmm_prepared(int type);
+
+/* QMatMul::accumulate_in_f32 / QCudaStorage::accumulate_in_f32
+ * (quantized/mod.rs:1187-1200, quantized/cuda.rs:1375-1380): keep a weight's
+ * products in f32 where a card's prompt pass would accumulate them in f16.
+ * Every product of this library sums in int32 and f32 already, so this
+ * changes nothing: QMM_OK for a covered type, QMM_UNSUPPORTED otherwise. */
+int qmm_accumulate_in_f32(int type);
+
 /* dst = x · Wᵀ for any rows, from an f32 activation: quantizes it into the
  * workspace and picks the kernel by rows (the QCudaStorage::fwd policy,
  * quantized/cuda.rs:1653-1680). With launch == 0 nothing is enqueued and
@@ -290,7 +312,8 @@ uint64_t qmm_gguf_data_offset(const qmm_gguf *g);
 /* Tensor infos (Content::tensor_infos): index by name (-1 when absent), name,
  * and type / dimensions (dims[0..3], outermost first, 1 past n_dims) / offset
  * from the data start / bytes (0 when the element count is not a whole
- * number of blocks, which qmm_gguf_load then refuses). */
+ * number of blocks or its bytes pass INT64_MAX, which qmm_gguf_load then
+ * refuses). */
 int64_t qmm_gguf_tensor_count(const qmm_gguf *g);
 int64_t qmm_gguf_find_tensor(const qmm_gguf *g, const char *name);
 const char *qmm_gguf_tensor_name(const qmm_gguf *g, int64_t i);
@@ -313,17 +336,73 @@ int qmm_gguf_kv_get(const qmm_gguf *g, int64_t i, int64_t j, int64_t *iv, double
 
 /* Bytes of a device buffer for `nelem` values of ggml type `type`: its
  * blocks plus MATRIX_ROW_PADDING = 512 values' worth of blocks
- * (quantized/cuda.rs:43, 1846-1870); 0 for an unknown type or a count that
- * is not a whole number of blocks. */
+ * (quantized/cuda.rs:43, 1846-1870); 0 for an unknown type, a count that
+ * is not a whole number of blocks, or a size past INT64_MAX. */
 size_t qmm_padded_bytes(int type, int64_t nelem);
 
 /* Tensor i's bytes from the file into device memory dst (dst_bytes >=
  * qmm_padded_bytes of the tensor), the padding zeroed: ggml_file::
  * qtensor_read + cuda::load_quantized_read (ggml_file.rs:220-256,
  * cuda.rs:2025-2075), read through two pinned staging buffers of 16 MiB the
- * library keeps (a chunk is read while the previous one copies). Returns when
- * the bytes are on the device; loads on one process are serialized. */
+ * library keeps (a chunk is read while the previous one copies;
+ * with_pinned_load_staging, cuda.rs:1966-2018). Returns when the bytes are
+ * on the device; loads on one process are serialized. A tensor whose bytes
+ * would run past the end of the file is refused (QMM_UNSUPPORTED) before
+ * anything is copied. The reference's switches, read once:
+ *   SWARMLLM_LOAD_PINNED=0: one pageable 16 MiB staging buffer, each chunk's
+ *     copy finished before the next read (cuda.rs:1979-1983); also where the
+ *     runtime refuses page-locked memory;
+ *   SWARMLLM_LOAD_READ=fresh: the tensor read through a fresh host buffer of
+ *     its whole size, copied at once (gguf_file.rs:57-63).
+ * qmm_pinned_load_chunks: chunks copied through the pinned pair since the
+ * process started (pinned_load_chunks, cuda.rs:1966-1972). */
 int qmm_gguf_load(const qmm_gguf *g, int64_t i, void *dst, size_t dst_bytes, int64_t stream);
+uint64_t qmm_pinned_load_chunks(void);
+
+/* A stack of expert weights with only the named entries loaded: tensor i of
+ * the file is [entries, ...] (dims[0] entries of one weight each, a whole
+ * number of blocks); slot slots[c] (c < count) is read from the file into
+ * dst at slot * entry bytes, every other slot and the padding zeroed
+ * (never to be read). dst_bytes >= qmm_padded_bytes of the whole tensor.
+ * A slot out of range is refused with nothing copied. The file-side form of
+ * load_quantized_entries (quantized/cuda.rs:2101-2127): a processor-held
+ * mixture-of-experts layer sends a chunk's chosen experts. */
+int qmm_gguf_load_entries(const qmm_gguf *g, int64_t i, int64_t count, const int64_t *slots, void *dst,
+                          size_t dst_bytes, int64_t stream);
+
+/* load_quantized_entries (quantized/cuda.rs:2101-2127): a stack of `entries`
+ * slots of entry_bytes (whole blocks of `type`) in dst, holding host bytes
+ * parts[c] at slot slots[c], every other slot and the padding (512 values'
+ * worth of blocks) zeroed; dst_bytes >= entries * entry_bytes + padding.
+ * Returns when the parts have been copied (they may be released). A slot out
+ * of range is refused with nothing copied. */
+int qmm_load_entries(int type, int64_t entries, size_t entry_bytes, int64_t count, const int64_t *slots,
+                     const void *const *parts, void *dst, size_t dst_bytes, int64_t stream);
+
+/* load_quantized_beside (quantized/cuda.rs:2082-2099): a weight's len host
+ * bytes (whole blocks of `type`) into dst, padded as a device weight, the
+ * copy issued on copy_stream beside the work on `stream`, which waits for it
+ * before its next work. Returns when the copy is done (the host bytes may be
+ * released); work already queued on `stream` is not waited for. */
+int qmm_load_beside(int type, const void *data, size_t len, void *dst, size_t dst_bytes, int64_t copy_stream,
+                    int64_t stream);
+
+/* The chosen rows of a table of GGUF blocks (an embedding lookup):
+ * out[r] = table[ids[r]], row r of n_ids, each row hidden / block_size
+ * blocks of `type` copied whole (the five formats, and F32 (0), F16 (1),
+ * BF16 (30)). hidden must be a whole number of blocks (else
+ * QMM_UNSUPPORTED), the table must hold vocab rows (table_bytes), and out
+ * n_ids rows (else QMM_WORKSPACE_TOO_SMALL); qmm_gather_row_bytes gives the
+ * bytes of a row. ids are u32 on the device: 0xFFFFFFFF writes a zero row
+ * (index_select's "no row"), and any other id >= vocab writes a zero row and
+ * adds 1 to *bad when `bad` (a u32 on the device the caller zeroes) is not
+ * NULL, for the caller to refuse, as the reference's host path refuses it
+ * (a row of zero bytes dequantizes to zeros in every format). Replaces
+ * QTensor::gather_rows / QCudaStorage::gather_rows (quantized/mod.rs:
+ * 1039-1091, quantized/cuda.rs:1478-1540). */
+int qmm_gather_row_bytes(int type, int64_t hidden, size_t *row_bytes);
+int qmm_gather_rows(int type, const void *table, size_t table_bytes, int64_t vocab, int64_t hidden,
+                    const uint32_t *ids, int64_t n_ids, void *out, size_t out_bytes, uint32_t *bad, int64_t stream);
 
 /* Dequantize `nelem` values of weight type `type` into f32 (out_f16 == 0)
  * or IEEE f16 (out_f16 != 0; each value is f16 of the f32 one).

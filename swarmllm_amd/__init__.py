@@ -5,8 +5,8 @@ AMD Instinct MI355X (gfx950), behind the C ABI of include/qmm.h."""
 from ._lib import QmmError, lib  # noqa: F401
 from .qtensor import (MOE_CARD_ONE_ROW_MAX_TOKENS, GgmlDType, QMatMul, QTensor, fill_normal,  # noqa: F401
                       forward_glu, glu, mmq_few_rows_line, moe_forward, moe_prompt_on_tensor_cores,
-                      moe_uses_prompt_kernel, set_force_dmmv)
+                      moe_uses_prompt_kernel, prepare, prepared, set_force_dmmv)
 
 __all__ = ["MOE_CARD_ONE_ROW_MAX_TOKENS", "GgmlDType", "QMatMul", "QTensor", "QmmError", "fill_normal", "forward_glu",
            "glu", "lib", "mmq_few_rows_line", "moe_forward", "moe_prompt_on_tensor_cores", "moe_uses_prompt_kernel",
-           "set_force_dmmv"]
+           "prepare", "prepared", "set_force_dmmv"]

@@ -87,6 +87,15 @@ SIGNATURES = {
                              ctypes.POINTER(ctypes.c_char_p)]),
     "qmm_padded_bytes": (_SZ, [_I, _I64]),
     "qmm_gguf_load": (_I, [_P, _I64, _P, _SZ, _I64]),
+    "qmm_pinned_load_chunks": (_U64, []),
+    "qmm_gguf_load_entries": (_I, [_P, _I64, _I64, ctypes.POINTER(_I64), _P, _SZ, _I64]),
+    "qmm_load_entries": (_I, [_I, _I64, _SZ, _I64, ctypes.POINTER(_I64), ctypes.POINTER(_P), _P, _SZ, _I64]),
+    "qmm_load_beside": (_I, [_I, _P, _SZ, _P, _SZ, _I64, _I64]),
+    "qmm_prepare": (_I, [_I]),
+    "qmm_prepared": (_I, [_I]),
+    "qmm_accumulate_in_f32": (_I, [_I]),
+    "qmm_gather_row_bytes": (_I, [_I, _I64, ctypes.POINTER(_SZ)]),
+    "qmm_gather_rows": (_I, [_I, _P, _SZ, _I64, _I64, _P, _I64, _P, _SZ, _P, _I64]),
 }
 
 _lib = None

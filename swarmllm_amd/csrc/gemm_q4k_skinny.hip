@@ -555,8 +555,8 @@ hipError_t launch_sk_dma(const MvTargets& t, int nsb, const ActPlanes& p, int64_
     a.tg.row_end[i] = t.row_end[t.count - 1];
   }
   const size_t lds = 2 * (size_t)D::kStage;
-  auto* kfn = &gemm_q4k_skinny_dma_kernel<MT, SBS>;
-  if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+  constexpr auto* kfn = &gemm_q4k_skinny_dma_kernel<MT, SBS>;
+  if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
   kfn<<<dim3((unsigned)((tiles + 3) / 4)), 256, lds, st>>>(a, nsb, p.codes, p.d, (int)rows);
   return hipGetLastError();
 }

@@ -14,11 +14,20 @@
 // file into a device buffer that holds MATRIX_ROW_PADDING = 512 values' worth
 // of blocks more, zeroed (cuda.rs:43). The read goes through two pinned
 // staging buffers the process keeps: chunk c is read into one while chunk
-// c - 1 is copied from the other.
+// c - 1 is copied from the other (with_pinned_load_staging, cuda.rs:1966-2018;
+// qmm_pinned_load_chunks counts the chunks). The reference's A/B switches,
+// read once: SWARMLLM_LOAD_PINNED=0 copies through one pageable staging
+// buffer instead, a chunk at a time, each copy done with its source before
+// the next read (load_quantized_read, cuda.rs:2025-2069);
+// SWARMLLM_LOAD_READ=fresh reads each tensor through a fresh host buffer of
+// its whole size and copies it at once (gguf_file.rs:57-63).
 #include <fcntl.h>
+#include <sys/stat.h>
 #include <unistd.h>
 
+#include <atomic>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -146,28 +155,113 @@ bool read_value(Reader& r, int type, int version, Value& v, int depth) {
   return r.ok;
 }
 
-// The pinned staging pair, allocated on first use and kept for the process.
+// The pinned staging pair, allocated on first use and kept for the process;
+// where the runtime refuses page-locked memory, loads copy through the
+// pageable staging buffer instead (as the reference's scope does).
 struct Staging {
-  std::mutex mu;
+  std::mutex mu;  // loads are serialized
   void* buf[2] = {nullptr, nullptr};
   hipEvent_t done[2] = {nullptr, nullptr};
-  bool ready = false;
+  bool recorded[2] = {false, false};  // done[b] marks a copy out of buf[b]
+  bool ready = false, refused = false;
+  std::vector<uint8_t> pageable;
   bool init() {
     if (ready) return true;
+    if (refused) return false;
     for (int b = 0; b < 2; b++) {
-      if (hipHostMalloc(&buf[b], kChunk, hipHostMallocDefault) != hipSuccess) return false;
-      if (hipEventCreateWithFlags(&done[b], hipEventDisableTiming) != hipSuccess) return false;
+      if (hipHostMalloc(&buf[b], kChunk, hipHostMallocDefault) != hipSuccess ||
+          hipEventCreateWithFlags(&done[b], hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        refused = true;
+        return false;
+      }
     }
     ready = true;
     return true;
   }
 };
 Staging g_staging;
+std::atomic<uint64_t> g_pinned_chunks{0};
+
+bool env_is(const char* name, const char* value) {
+  const char* v = std::getenv(name);
+  return v && std::strcmp(v, value) == 0;
+}
+bool load_pinned() {
+  static const bool on = !env_is("SWARMLLM_LOAD_PINNED", "0");
+  return on;
+}
+bool load_fresh() {
+  static const bool on = env_is("SWARMLLM_LOAD_READ", "fresh");
+  return on;
+}
+
+// n bytes of the file at `at` into host memory p; false when the file ends first.
+bool read_file(int fd, uint8_t* p, size_t n, uint64_t at) {
+  size_t got = 0;
+  while (got < n) {
+    const ssize_t r = pread(fd, p + got, n - got, (off_t)(at + got));
+    if (r <= 0) return false;
+    got += (size_t)r;
+  }
+  return true;
+}
+
+// len bytes of the file at `at` into device memory d, through the staging
+// the switches choose; returns with every copy issued on st (the pinned
+// path), or finished (the pageable and fresh paths). Called with
+// g_staging.mu held.
+int copy_span(int fd, uint64_t at, uint64_t len, uint8_t* d, hipStream_t st) {
+  if (len == 0) return QMM_OK;
+  if (load_fresh()) {
+    std::vector<uint8_t> whole;
+    try {
+      whole.resize((size_t)len);
+    } catch (...) {
+      return QMM_DEVICE_ERROR;
+    }
+    if (!read_file(fd, whole.data(), (size_t)len, at)) return QMM_UNSUPPORTED;
+    if (hipMemcpyAsync(d, whole.data(), (size_t)len, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+      return QMM_DEVICE_ERROR;
+    return QMM_OK;
+  }
+  if (!load_pinned() || !g_staging.init()) {
+    if (g_staging.pageable.size() < kChunk) g_staging.pageable.resize(kChunk);
+    for (uint64_t done = 0; done < len; done += kChunk) {
+      const size_t n = (size_t)(len - done < kChunk ? len - done : kChunk);
+      if (!read_file(fd, g_staging.pageable.data(), n, at + done)) return QMM_UNSUPPORTED;
+      if (hipMemcpyAsync(d + done, g_staging.pageable.data(), n, hipMemcpyHostToDevice, st) != hipSuccess ||
+          hipStreamSynchronize(st) != hipSuccess)
+        return QMM_DEVICE_ERROR;
+    }
+    return QMM_OK;
+  }
+  int c = 0;
+  for (uint64_t done = 0; done < len; done += kChunk, c++) {
+    const size_t n = (size_t)(len - done < kChunk ? len - done : kChunk);
+    const int b = c & 1;
+    // the copy that last read this staging buffer has finished (also one
+    // issued by an earlier span of this load)
+    if (g_staging.recorded[b] && hipEventSynchronize(g_staging.done[b]) != hipSuccess) return QMM_DEVICE_ERROR;
+    if (!read_file(fd, (uint8_t*)g_staging.buf[b], n, at + done)) return QMM_UNSUPPORTED;
+    if (hipMemcpyAsync(d + done, g_staging.buf[b], n, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipEventRecord(g_staging.done[b], st) != hipSuccess)
+      return QMM_DEVICE_ERROR;
+    g_staging.recorded[b] = true;
+    g_pinned_chunks.fetch_add(1, std::memory_order_relaxed);
+  }
+  return QMM_OK;
+}
+
+// Padding bytes past a device weight of `type`: MATRIX_ROW_PADDING values' worth of blocks.
+int64_t pad_bytes(int64_t bs, int64_t ts) { return kRowPadding / bs * ts; }
 
 }  // namespace
 
 struct qmm_gguf {
   int fd = -1;
+  uint64_t file_bytes = 0;
   int version = 0;
   uint64_t alignment = kDefaultAlignment;
   uint64_t data_offset = 0;
@@ -235,7 +329,8 @@ int qmm_gguf_open(const char* path, qmm_gguf** out) {
       t.nelem = nel;
       // a count that is not a whole number of blocks fails when the tensor
       // is read, not here (TensorInfo::read, gguf_file.rs:78-84)
-      t.whole = nel % bs == 0;
+      // (a byte count past INT64_MAX is refused the same way)
+      t.whole = nel % bs == 0 && nel / bs <= INT64_MAX / ts;
       t.bytes = t.whole ? (uint64_t)(nel / bs * ts) : 0;
       // a repeated name keeps its last info, as the reference's map insert does
       auto it = g->tensor_index.find(t.name);
@@ -265,6 +360,9 @@ int qmm_gguf_open(const char* path, qmm_gguf** out) {
   if (!ok) return QMM_UNSUPPORTED;
   g->fd = open(path, O_RDONLY);
   if (g->fd < 0) return QMM_UNSUPPORTED;
+  struct stat sb;
+  if (fstat(g->fd, &sb) != 0 || sb.st_size < 0) return QMM_UNSUPPORTED;
+  g->file_bytes = (uint64_t)sb.st_size;
   *out = g.release();
   return QMM_OK;
 }
@@ -346,7 +444,18 @@ int qmm_gguf_kv_get(const qmm_gguf* g, int64_t i, int64_t j, int64_t* iv, double
 size_t qmm_padded_bytes(int type, int64_t nelem) {
   int64_t bs = 0, ts = 0;
   if (!type_shape(type, bs, ts) || nelem < 0 || nelem % bs) return 0;
-  return (size_t)(nelem / bs * ts + kRowPadding / bs * ts);
+  if (nelem / bs > (INT64_MAX - pad_bytes(bs, ts)) / ts) return 0;  // the size does not fit
+  return (size_t)(nelem / bs * ts + pad_bytes(bs, ts));
+}
+
+uint64_t qmm_pinned_load_chunks(void) { return g_pinned_chunks.load(std::memory_order_relaxed); }
+
+// Where tensor t's bytes start in the file; false when they would run past
+// its end (a truncated or corrupt file: refused before anything is copied).
+static bool tensor_span(const qmm_gguf* g, const Tensor& t, uint64_t& base) {
+  if (t.offset > UINT64_MAX - g->data_offset) return false;
+  base = g->data_offset + t.offset;
+  return base <= g->file_bytes && t.bytes <= g->file_bytes - base;
 }
 
 int qmm_gguf_load(const qmm_gguf* g, int64_t i, void* dst, size_t dst_bytes, int64_t stream) {
@@ -354,35 +463,98 @@ int qmm_gguf_load(const qmm_gguf* g, int64_t i, void* dst, size_t dst_bytes, int
   const Tensor& t = g->tensors[i];
   if (!t.whole) return QMM_UNSUPPORTED;
   const size_t padded = qmm_padded_bytes(t.type, t.nelem);
+  if (padded == 0) return QMM_UNSUPPORTED;
   if (dst_bytes < padded) return QMM_WORKSPACE_TOO_SMALL;
+  uint64_t base = 0;
+  if (!tensor_span(g, t, base)) return QMM_UNSUPPORTED;
   const hipStream_t st = (hipStream_t)stream;
   std::lock_guard<std::mutex> lock(g_staging.mu);
-  if (!g_staging.init()) return QMM_DEVICE_ERROR;
   (void)hipGetLastError();
   uint8_t* d = (uint8_t*)dst;
   if (hipMemsetAsync(d + t.bytes, 0, padded - t.bytes, st) != hipSuccess) return QMM_DEVICE_ERROR;
-  const uint64_t base = g->data_offset + t.offset;
-  int c = 0;
-  for (uint64_t done = 0; done < t.bytes; done += kChunk, c++) {
-    const size_t n = (size_t)(t.bytes - done < kChunk ? t.bytes - done : kChunk);
-    const int b = c & 1;
-    // the copy that last read this staging buffer has finished
-    if (c >= 2 && hipEventSynchronize(g_staging.done[b]) != hipSuccess) return QMM_DEVICE_ERROR;
-    size_t got = 0;
-    while (got < n) {
-      const ssize_t r = pread(g->fd, (uint8_t*)g_staging.buf[b] + got, n - got, (off_t)(base + done + got));
-      if (r <= 0) {
-        (void)hipStreamSynchronize(st);
-        return QMM_UNSUPPORTED;  // the file ends inside the tensor
-      }
-      got += (size_t)r;
-    }
-    if (hipMemcpyAsync(d + done, g_staging.buf[b], n, hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipEventRecord(g_staging.done[b], st) != hipSuccess)
-      return QMM_DEVICE_ERROR;
-  }
+  const int rc = copy_span(g->fd, base, t.bytes, d, st);
   // the staging buffers are free for the next load, and the tensor is on the device
+  const bool synced = hipStreamSynchronize(st) == hipSuccess;
+  if (rc != QMM_OK) return rc;
+  return synced ? QMM_OK : QMM_DEVICE_ERROR;
+}
+
+int qmm_gguf_load_entries(const qmm_gguf* g, int64_t i, int64_t count, const int64_t* slots, void* dst,
+                          size_t dst_bytes, int64_t stream) {
+  if (!g || i < 0 || i >= (int64_t)g->tensors.size() || !dst || count < 0 || (count > 0 && !slots))
+    return QMM_UNSUPPORTED;
+  const Tensor& t = g->tensors[i];
+  int64_t bs = 0, ts = 0;
+  if (!t.whole || t.n_dims < 2 || t.dims[0] <= 0 || !type_shape(t.type, bs, ts)) return QMM_UNSUPPORTED;
+  const int64_t entries = t.dims[0];
+  const int64_t per = t.nelem / entries;  // values of one entry
+  if (per % bs) return QMM_UNSUPPORTED;   // an entry is a whole number of blocks
+  const uint64_t eb = (uint64_t)(per / bs * ts);
+  const size_t padded = qmm_padded_bytes(t.type, t.nelem);
+  if (padded == 0) return QMM_UNSUPPORTED;
+  if (dst_bytes < padded) return QMM_WORKSPACE_TOO_SMALL;
+  for (int64_t c = 0; c < count; c++)
+    if (slots[c] < 0 || slots[c] >= entries) return QMM_UNSUPPORTED;  // nothing copied
+  uint64_t base = 0;
+  if (!tensor_span(g, t, base)) return QMM_UNSUPPORTED;
+  const hipStream_t st = (hipStream_t)stream;
+  std::lock_guard<std::mutex> lock(g_staging.mu);
+  (void)hipGetLastError();
+  uint8_t* d = (uint8_t*)dst;
+  // every slot not named stays zero, as does the padding
+  if (hipMemsetAsync(d, 0, padded, st) != hipSuccess) return QMM_DEVICE_ERROR;
+  int rc = QMM_OK;
+  for (int64_t c = 0; c < count && rc == QMM_OK; c++)
+    rc = copy_span(g->fd, base + (uint64_t)slots[c] * eb, eb, d + (uint64_t)slots[c] * eb, st);
+  const bool synced = hipStreamSynchronize(st) == hipSuccess;
+  if (rc != QMM_OK) return rc;
+  return synced ? QMM_OK : QMM_DEVICE_ERROR;
+}
+
+int qmm_load_entries(int type, int64_t entries, size_t entry_bytes, int64_t count, const int64_t* slots,
+                     const void* const* parts, void* dst, size_t dst_bytes, int64_t stream) {
+  int64_t bs = 0, ts = 0;
+  if (!type_shape(type, bs, ts) || entries < 0 || count < 0 || !dst || (count > 0 && (!slots || !parts)))
+    return QMM_UNSUPPORTED;
+  if (entry_bytes % (size_t)ts) return QMM_UNSUPPORTED;  // whole blocks
+  if (entries > 0 && entry_bytes > (size_t)(INT64_MAX - pad_bytes(bs, ts)) / (size_t)entries) return QMM_UNSUPPORTED;
+  const size_t len = (size_t)entries * entry_bytes, padded = len + (size_t)pad_bytes(bs, ts);
+  if (dst_bytes < padded) return QMM_WORKSPACE_TOO_SMALL;
+  for (int64_t c = 0; c < count; c++)
+    if (slots[c] < 0 || slots[c] >= entries || (entry_bytes && !parts[c])) return QMM_UNSUPPORTED;  // nothing copied
+  const hipStream_t st = (hipStream_t)stream;
+  (void)hipGetLastError();
+  uint8_t* d = (uint8_t*)dst;
+  if (hipMemsetAsync(d, 0, padded, st) != hipSuccess) return QMM_DEVICE_ERROR;
+  for (int64_t c = 0; c < count; c++)
+    if (entry_bytes &&
+        hipMemcpyAsync(d + (size_t)slots[c] * entry_bytes, parts[c], entry_bytes, hipMemcpyHostToDevice, st) !=
+            hipSuccess)
+      return QMM_DEVICE_ERROR;
+  // the parts may be released when this returns
   return hipStreamSynchronize(st) == hipSuccess ? QMM_OK : QMM_DEVICE_ERROR;
+}
+
+int qmm_load_beside(int type, const void* data, size_t len, void* dst, size_t dst_bytes, int64_t copy_stream,
+                    int64_t stream) {
+  int64_t bs = 0, ts = 0;
+  if (!type_shape(type, bs, ts) || !dst || (len && !data) || len % (size_t)ts) return QMM_UNSUPPORTED;
+  if (len > (size_t)(INT64_MAX - pad_bytes(bs, ts))) return QMM_UNSUPPORTED;
+  const size_t padded = len + (size_t)pad_bytes(bs, ts);
+  if (dst_bytes < padded) return QMM_WORKSPACE_TOO_SMALL;
+  const hipStream_t cs = (hipStream_t)copy_stream, st = (hipStream_t)stream;
+  (void)hipGetLastError();
+  uint8_t* d = (uint8_t*)dst;
+  hipEvent_t ev = nullptr;
+  if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return QMM_DEVICE_ERROR;
+  bool ok = (len == 0 || hipMemcpyAsync(d, data, len, hipMemcpyHostToDevice, cs) == hipSuccess) &&
+            hipMemsetAsync(d + len, 0, padded - len, cs) == hipSuccess && hipEventRecord(ev, cs) == hipSuccess &&
+            hipStreamWaitEvent(st, ev, 0) == hipSuccess;
+  // the host bytes may be released when this returns: wait for the copy
+  // alone (work queued on `stream` keeps running meanwhile)
+  ok = hipEventSynchronize(ev) == hipSuccess && ok;
+  (void)hipEventDestroy(ev);
+  return ok ? QMM_OK : QMM_DEVICE_ERROR;
 }
 
 }  // extern "C"

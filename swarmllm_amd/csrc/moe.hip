@@ -376,8 +376,8 @@ hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, co
   const int64_t rows_per_wg = (int64_t)kMoeSWaves * rpw;
   const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
   const size_t lds = ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)kMoeSWaves * MoeSpan<FMT>::kStage;
-  auto* kfn = &moe_b32s_kernel<FMT>;
-  if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+  constexpr auto* kfn = &moe_b32s_kernel<FMT>;
+  if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
   kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
                                           topk_w, topk, (int)size_m, dst, ldd, (int)rpw);
   return hipGetLastError();

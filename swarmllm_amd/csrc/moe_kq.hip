@@ -383,8 +383,8 @@ hipError_t launch_kq(const void* w, int num_experts, int64_t n, int64_t k, const
   const int64_t rows_per_wg = (int64_t)kKqWaves * rpw;
   const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
   const size_t lds = kq_act_bytes(nsb, (int)pairs) + kq_stage_bytes<TYPE>();
-  auto* kfn = &moe_kq_kernel<TYPE, T, P>;
-  if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+  constexpr auto* kfn = &moe_kq_kernel<TYPE, T, P>;
+  if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
   kfn<<<grid, 64 * kKqWaves, lds, st>>>((const uint8_t*)w, n, nsb, estride, num_experts, p.codes, p.d,
                                         (const int16_t*)p.sums, runs, ids, topk_w, topk, (int)size_m, dst, ldd,
                                         (int)rpw, (int)pairs);

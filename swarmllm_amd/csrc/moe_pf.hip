@@ -500,8 +500,8 @@ hipError_t launch_pf(const void* w, int num_experts, int64_t n, int64_t k, const
   int64_t gy = (size_m + kPfM - 1) / kPfM + runs_max;
   gy = gy < 1 ? 1 : gy > 65535 ? 65535 : gy;
   const dim3 grid((unsigned)((n + kPfNT - 1) / kPfNT), (unsigned)gy);
-  auto* kfn = &moe_pf_kernel<FMT, BF>;
-  if (S::Lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+  constexpr auto* kfn = &moe_pf_kernel<FMT, BF>;
+  if (S::Lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
   kfn<<<grid, 64 * kPfW, S::Lds, st>>>((const uint8_t*)w, n, k, rb, estride, num_experts, x, x_stride, chunks, ids,
                                        topk_w, topk, (int)size_m, dst, ldd);
   return hipGetLastError();

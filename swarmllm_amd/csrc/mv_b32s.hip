@@ -255,12 +255,12 @@ hipError_t launch_b32s(const MvTargets& t, int nb, const float* x, int64_t xstri
   const size_t lds = (b32_act_lds_bytes(NR, nb) + 15) / 16 * 16 + 16 * (size_t)kStageBytes;
   const dim3 grid((unsigned)(waves / 16));
   if (pre) {
-    auto* kfn = &mv_b32_stream_kernel<FMT, NR, false>;
-    if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+    constexpr auto* kfn = &mv_b32_stream_kernel<FMT, NR, false>;
+    if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
     kfn<<<grid, 1024, lds, st>>>(t, nb, waves, nullptr, 0, pre->codes, pre->d);
   } else {
-    auto* kfn = &mv_b32_stream_kernel<FMT, NR, true>;
-    if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+    constexpr auto* kfn = &mv_b32_stream_kernel<FMT, NR, true>;
+    if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
     kfn<<<grid, 1024, lds, st>>>(t, nb, waves, x, xstride, nullptr, nullptr);
   }
   return hipGetLastError();

@@ -304,17 +304,23 @@ __device__ __forceinline__ void load_q6_lane(const uint8_t* buf, int b, int h, i
 }
 
 // Dynamic LDS past 64 KiB needs the kernel's limit raised (to the 160 KiB of
-// a CU), once per kernel function.
-inline hipError_t set_max_dynamic_lds(const void* fn) {
-  static std::mutex mu;
-  static const void* done[64];
-  static int ndone = 0;
-  std::lock_guard<std::mutex> lock(mu);
-  for (int i = 0; i < ndone; i++)
-    if (done[i] == fn) return hipSuccess;
-  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  if (e == hipSuccess && ndone < 64) done[ndone++] = fn;
-  return e;
+// a CU), once per kernel function and device (raise_lds_limit, qmm_api.hip).
+// Each launcher names its kernel as a template argument, which registers the
+// kernel when the library loads (big_lds_register), so qmm_prepare can raise
+// every such limit before a capture begins.
+bool big_lds_register(const void* fn);
+hipError_t raise_lds_limit(const void* fn);
+template <auto F>
+struct BigLds {
+  static const bool registered;
+};
+template <auto F>
+const bool BigLds<F>::registered = big_lds_register((const void*)F);
+
+template <auto F>
+inline hipError_t set_max_dynamic_lds() {
+  (void)BigLds<F>::registered;
+  return raise_lds_limit((const void*)F);
 }
 
 }  // namespace qmm

@@ -280,12 +280,12 @@ hipError_t launch_stream_x(const MvTargets& t, int nsb, const float* x, int64_t 
   const size_t lds = act_lds_bytes(NR, nsb) + (XCHG ? (size_t)WPG * 144 * nsb : 0);
   const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
   if (pre) {
-    auto* k = mv_q4k_stream_kernel<NR, T, false, WPG, PF, XCHG>;
-    if (lds > 65536 && set_max_dynamic_lds((const void*)k) != hipSuccess) return hipErrorInvalidValue;
+    constexpr auto* k = &mv_q4k_stream_kernel<NR, T, false, WPG, PF, XCHG>;
+    if (lds > 65536 && set_max_dynamic_lds<k>() != hipSuccess) return hipErrorInvalidValue;
     k<<<grid, 64 * WPG, lds, st>>>(t, nsb, nullptr, 0, pre->codes, pre->d, (const int16_t*)pre->sums, qmax);
   } else {
-    auto* k = mv_q4k_stream_kernel<NR, T, true, WPG, PF, XCHG>;
-    if (lds > 65536 && set_max_dynamic_lds((const void*)k) != hipSuccess) return hipErrorInvalidValue;
+    constexpr auto* k = &mv_q4k_stream_kernel<NR, T, true, WPG, PF, XCHG>;
+    if (lds > 65536 && set_max_dynamic_lds<k>() != hipSuccess) return hipErrorInvalidValue;
     k<<<grid, 64 * WPG, lds, st>>>(t, nsb, x, xstride, nullptr, nullptr, nullptr, qmax);
   }
   return hipGetLastError();
@@ -421,13 +421,13 @@ hipError_t launch_glu_x(const void* wg, const void* wu, int64_t n, int nsb, cons
   const size_t lds = act_lds_bytes(NR, nsb) + (size_t)WPG * 144 * nsb;
   const dim3 grid((unsigned)((waves + WPG - 1) / WPG));
   if (pre) {
-    auto* kf = mv_q4k_glu_kernel<NR, T, false, WPG, PF, ACT>;
-    if (lds > 65536 && set_max_dynamic_lds((const void*)kf) != hipSuccess) return hipErrorInvalidValue;
+    constexpr auto* kf = &mv_q4k_glu_kernel<NR, T, false, WPG, PF, ACT>;
+    if (lds > 65536 && set_max_dynamic_lds<kf>() != hipSuccess) return hipErrorInvalidValue;
     kf<<<grid, 64 * WPG, lds, st>>>((const uint8_t*)wg, (const uint8_t*)wu, n, nsb, nullptr, 0, pre->codes, pre->d,
                                     (const int16_t*)pre->sums, qmax, dst, ldd);
   } else {
-    auto* kf = mv_q4k_glu_kernel<NR, T, true, WPG, PF, ACT>;
-    if (lds > 65536 && set_max_dynamic_lds((const void*)kf) != hipSuccess) return hipErrorInvalidValue;
+    constexpr auto* kf = &mv_q4k_glu_kernel<NR, T, true, WPG, PF, ACT>;
+    if (lds > 65536 && set_max_dynamic_lds<kf>() != hipSuccess) return hipErrorInvalidValue;
     kf<<<grid, 64 * WPG, lds, st>>>((const uint8_t*)wg, (const uint8_t*)wu, n, nsb, x, xstride, nullptr, nullptr,
                                     nullptr, qmax, dst, ldd);
   }

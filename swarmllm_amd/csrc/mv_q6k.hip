@@ -192,12 +192,12 @@ hipError_t launch_stream(const MvTargets& t, int nsb, const float* x, int64_t xs
   const size_t lds = (act_lds_bytes(NR, nsb) + 15) / 16 * 16 + 16 * (size_t)kQ6SpanBuf;
   const dim3 grid((unsigned)(waves / 16));
   if (pre) {
-    auto* kfn = &mv_q6k_stream_kernel<NR, false>;
-    if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+    constexpr auto* kfn = &mv_q6k_stream_kernel<NR, false>;
+    if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
     kfn<<<grid, 1024, lds, st>>>(t, nsb, waves, nullptr, 0, pre->codes, pre->d, (const int16_t*)pre->sums, qmax);
   } else {
-    auto* kfn = &mv_q6k_stream_kernel<NR, true>;
-    if (lds > 65536 && set_max_dynamic_lds((const void*)kfn) != hipSuccess) return hipErrorInvalidValue;
+    constexpr auto* kfn = &mv_q6k_stream_kernel<NR, true>;
+    if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
     kfn<<<grid, 1024, lds, st>>>(t, nsb, waves, x, xstride, nullptr, nullptr, nullptr, qmax);
   }
   return hipGetLastError();

@@ -6,6 +6,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <set>
+#include <utility>
+#include <vector>
 
 #include "../../include/qmm.h"
 #include "qmm_device.h"
@@ -151,6 +154,40 @@ void few_rows_line(int type, int64_t& rows, int64_t& bytes) {
   bytes = pol.few_bytes;
 }
 
+// Types prepared on a device (qmm_prepare), a bit each: the reference's
+// MMQ_FEW_ROWS_READY (quantized/cuda.rs:890-932). A product of at most 8
+// rows on a stream being captured takes a matrix-core kernel only once its
+// type is prepared on the current device; the first such product outside a
+// capture prepares it (mmq_prepare_few_rows_once).
+constexpr int kMaxDevices = 64;
+std::atomic<uint32_t> g_prepared[kMaxDevices];
+std::atomic<uint32_t> g_prepare_tried[kMaxDevices];
+
+int type_bit(int type) {
+  switch (type) {
+    case qmm::T_Q8_0: return 1;
+    case qmm::T_Q4_K: return 2;
+    case qmm::T_Q6_K: return 4;
+    case qmm::T_IQ4_NL: return 8;
+    case qmm::T_MXFP4: return 16;
+    default: return 0;
+  }
+}
+
+int current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  return dev;
+}
+
+bool prepared(int type) {
+  const int dev = current_device();
+  return dev >= 0 && (g_prepared[dev].load(std::memory_order_acquire) & (uint32_t)type_bit(type)) != 0;
+}
+
 bool stream_is_capturing(hipStream_t st) {
   hipStreamCaptureStatus s = hipStreamCaptureStatusNone;
   const hipError_t e = hipStreamIsCapturing(st, &s);
@@ -164,7 +201,13 @@ bool few_rows_take(int type, int64_t rows, int64_t wbytes, hipStream_t st) {
   int64_t fewest, least;
   few_rows_line(type, fewest, least);
   if (rows < (fewest > 2 ? fewest : 2) || wbytes < least) return false;
-  return mmq_policy().captured || !stream_is_capturing(st);
+  if (!stream_is_capturing(st)) {
+    const int dev = current_device();
+    const uint32_t bit = (uint32_t)type_bit(type);
+    if (dev >= 0 && !(g_prepare_tried[dev].fetch_or(bit, std::memory_order_acq_rel) & bit)) (void)qmm_prepare(type);
+    return true;
+  }
+  return mmq_policy().captured && prepared(type);
 }
 
 bool mmq_allows(int64_t rows) {
@@ -310,8 +353,53 @@ hipError_t launch_stream_targets(int type, int count, const void* const* w, cons
 namespace qmm {
 namespace {
 std::atomic<const char*> g_last_kernel{""};
+
+// The kernels that may ask for more than 64 KiB of LDS (registered as the
+// library loads) and the (device, kernel) pairs whose limit is raised.
+std::mutex& lds_mu() {
+  static std::mutex m;
+  return m;
 }
+std::vector<const void*>& lds_kernels() {
+  static std::vector<const void*> v;
+  return v;
+}
+std::set<std::pair<int, const void*>>& lds_raised() {
+  static std::set<std::pair<int, const void*>> s;
+  return s;
+}
+}  // namespace
 void note_launch(const char* what) { g_last_kernel.store(what, std::memory_order_relaxed); }
+
+bool big_lds_register(const void* fn) {
+  std::lock_guard<std::mutex> lock(lds_mu());
+  lds_kernels().push_back(fn);
+  return true;
+}
+
+hipError_t raise_lds_limit(const void* fn) {
+  int dev = -1;
+  const hipError_t g = hipGetDevice(&dev);
+  if (g != hipSuccess) return g;
+  std::lock_guard<std::mutex> lock(lds_mu());
+  if (lds_raised().count({dev, fn})) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (e == hipSuccess) lds_raised().insert({dev, fn});
+  return e;
+}
+
+hipError_t raise_all_lds_limits() {
+  std::vector<const void*> all;
+  {
+    std::lock_guard<std::mutex> lock(lds_mu());
+    all = lds_kernels();
+  }
+  for (const void* fn : all) {
+    const hipError_t e = raise_lds_limit(fn);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
 }  // namespace qmm
 
 extern "C" {
@@ -338,6 +426,27 @@ int qmm_available(void) {
   }
   return cached[dev];
 }
+
+int qmm_prepare(int type) {
+  const uint32_t bit = (uint32_t)type_bit(type);
+  if (!bit) return QMM_UNSUPPORTED;
+  const int dev = current_device();
+  if (dev < 0) return QMM_DEVICE_ERROR;
+  if (!qmm_available()) return QMM_NO_TILE;
+  (void)cu_count();
+  (void)mmq_policy();
+  const bool scratch = qmm::noalloc_prepare();
+  const hipError_t e = qmm::raise_all_lds_limits();
+  (void)hipGetLastError();  // not sticky: leave nothing for a later check to read
+  if (!scratch || e != hipSuccess) return QMM_DEVICE_ERROR;
+  g_prepared[dev].fetch_or(bit, std::memory_order_acq_rel);
+  return QMM_OK;
+}
+
+int qmm_prepared(int type) { return prepared(type) ? 1 : 0; }
+
+// Every product here sums in int32 / f32 (no f16 accumulator to widen).
+int qmm_accumulate_in_f32(int type) { return type_bit(type) ? QMM_OK : QMM_UNSUPPORTED; }
 
 int qmm_block_size(int type) { return block_size(type); }
 

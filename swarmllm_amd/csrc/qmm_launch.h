@@ -220,4 +220,10 @@ bool gemm_q6k_fits(int64_t n, int64_t k, int64_t rows);
 hipError_t launch_gemm_q6k(const void* w, int64_t n, int64_t k, const ActPlanes& p, int64_t rows, float* dst,
                            int64_t ldd, hipStream_t s);
 
+// Set-up a first launch would otherwise do (qmm_prepare): the LDS limit of
+// every kernel that asks for more than 64 KiB, on the current device, and
+// the no-allocation scratch's address there.
+hipError_t raise_all_lds_limits();
+bool noalloc_prepare();
+
 }  // namespace qmm

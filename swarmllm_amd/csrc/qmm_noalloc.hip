@@ -52,6 +52,12 @@ void* scratch_on_current_device() {
 
 }  // namespace
 
+namespace qmm {
+// The scratch's address on the current device looked up ahead of a first
+// call (qmm_prepare): false when the lookup failed.
+bool noalloc_prepare() { return scratch_on_current_device() != nullptr; }
+}  // namespace qmm
+
 extern "C" {
 
 size_t qmm_forward_noalloc_max_bytes(void) { return kScratchBytes; }

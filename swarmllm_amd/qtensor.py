@@ -15,6 +15,7 @@ from __future__ import annotations
 import ctypes
 import enum
 import os
+import warnings
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
@@ -169,6 +170,117 @@ class QTensor:
               lib().qmm_quantize_weights(int(dtype), _ptr(w), _ptr(q.data_), nel, _ptr(scratch), sb, _stream()))
         return q
 
+    @staticmethod
+    def quantize_onto(src: torch.Tensor, dtype: GgmlDType, device="cuda") -> "QTensor":
+        """QTensor::quantize_onto (mod.rs:907-932): `src` on the CPU, quantized
+        into a QTensor on `device` (any shape whose last dim is a whole number
+        of blocks), bit-exact to from_float; the quantization runs on the device."""
+        dtype = GgmlDType(dtype)
+        if src.device.type != "cpu":
+            raise ValueError(f"`quantize_onto` expects a `src` to be on the cpu, got {src.device}.")
+        shape = tuple(src.shape)
+        qk = dtype.block_size()
+        if not shape or shape[-1] % qk:
+            raise ValueError(f"quantized tensor must have their last dim divisible by block size {shape} {qk}")
+        if not dtype.is_quantized():
+            raise ValueError(f"quantize_onto: {dtype.name} is not a block format")
+        flat = src.to(torch.float32).contiguous().reshape(-1).to(device)
+        nel = flat.numel()
+        if nel % qk:
+            raise ValueError(f"tensor size ({shape}) is not divisible by block size {qk}")
+        q = QTensor.alloc(shape, dtype, device)
+        if nel:
+            sb = lib().qmm_quantize_scratch_bytes(int(dtype), nel)
+            scratch = torch.empty(max(sb, 1), dtype=torch.uint8, device=flat.device)
+            check("qmm_quantize_weights", lib().qmm_quantize_weights(int(dtype), _ptr(flat), _ptr(q.data_), nel,
+                                                                     _ptr(scratch), sb, _stream()))
+        return q
+
+    def gather_rows(self, ids: torch.Tensor, check_ids: bool = True) -> "QTensor":
+        """QTensor::gather_rows (mod.rs:1039-1091): the rows `ids` (u32, on
+        the table's device) of a [vocab, hidden] table, as a QTensor
+        [len(ids), hidden] holding the same blocks (qmm_gather_rows). Rows must
+        be a whole number of blocks. An id past the vocabulary raises
+        ValueError, as the reference's host path does; that check reads a
+        device counter back (a synchronization), and check_ids=False skips it
+        (such a row then holds zeros, as does a row of id 0xFFFFFFFF)."""
+        if len(self.shape) != 2:
+            raise ValueError("gather_rows expects a 2-D [vocab, hidden] tensor")
+        vocab, hidden = self.shape
+        block = self.dtype.block_size()
+        if hidden % block:
+            raise ValueError(f"gather_rows: hidden {hidden} is not a whole number of {block}-element blocks")
+        if ids.dtype != torch.uint32:
+            raise ValueError(f"gather_rows: ids must be u32, got {ids.dtype}")
+        if ids.device != self.data_.device:
+            raise ValueError("gather_rows: ids must be on the same device")
+        flat = ids.contiguous().reshape(-1)
+        n_ids = flat.numel()
+        L = lib()
+        rb = ctypes.c_size_t(0)
+        check("qmm_gather_row_bytes", L.qmm_gather_row_bytes(int(self.dtype), hidden, ctypes.byref(rb)))
+        out = QTensor.alloc((n_ids, hidden), self.dtype, self.data_.device)
+        if n_ids == 0:
+            return out
+        bad = torch.zeros(1, dtype=torch.int32, device=self.data_.device) if check_ids else None
+        check("qmm_gather_rows", L.qmm_gather_rows(int(self.dtype), _ptr(self.data_), self.data_.numel(), vocab, hidden,
+                                                   _ptr(flat), n_ids, _ptr(out.data_), out.data_.numel(),
+                                                   _ptr(bad) if bad is not None else None, _stream()))
+        if bad is not None and int(bad.item()):
+            host = flat.cpu().to(torch.int64)
+            first = int(host[(host >= vocab) & (host != 0xFFFFFFFF)][0])
+            raise ValueError(f"gather_rows: id {first} out of range for vocabulary {vocab}")
+        return out
+
+    def device_ptr(self) -> int:
+        """The device address of the blocks (QTensor::device_ptr, mod.rs:1120-1127)."""
+        return self.data_.data_ptr()
+
+    def indexed_moe_forward(self, x: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+        """QTensor::indexed_moe_forward (mod.rs:1093-1118, the card's
+        cuda.rs:1236-1376) in its layout: weights [E, n, k], x [batch, topk or
+        1, k] f32, ids [batch, topk] (u32, or int32 / int64 below 2^31)
+        naming each token's experts; returns [batch, topk, n] with
+        out[b, j] = x[b, j or 0] . W[ids[b, j]]. Served by qmm_moe_forward:
+        entry i = b * topk + j pairs slot i with expert ids[b, j] (entries
+        sorted by expert on the device, any order giving the same result);
+        per-slot inputs (x's middle dim topk) take scale 1 per slot, which
+        makes the routing read one input row per slot; a shared input (middle
+        dim 1) reads row b for every slot of token b. An expert id out of
+        range leaves its row zero, as the reference's zeroed output does."""
+        if len(self.shape) != 3:
+            raise ValueError(f"indexed_moe_forward: weights [E, n, k], not {self.shape}")
+        e, n, k = self.shape
+        if ids.dim() != 2:
+            raise ValueError(f"indexed_moe_forward: ids [batch, topk], not {tuple(ids.shape)}")
+        batch, topk = ids.shape
+        if x.dim() != 3 or x.shape[0] != batch or x.shape[1] not in (1, topk) or x.shape[2] != k:
+            raise ValueError(f"indexed_moe_forward: x [batch={batch}, {topk} or 1, {k}], not {tuple(x.shape)}")
+        if x.dtype != torch.float32:
+            raise ValueError("Expected f32")
+        out = torch.zeros((batch, topk, n), dtype=torch.float32, device=x.device)
+        if batch * topk == 0:
+            return out
+        flat_ids = ids.reshape(-1)
+        if flat_ids.dtype == torch.uint32:
+            flat_ids = flat_ids.to(torch.int64)
+        expert_ids, order = torch.sort(flat_ids.to(torch.int64), stable=True)
+        expert_ids = expert_ids.clamp(-1, 2 ** 31 - 1).to(torch.int32).contiguous()
+        sorted_ids = order.to(torch.int32).contiguous()
+        per_slot = x.shape[1] == topk and topk > 1
+        xs = x.contiguous().reshape(-1, k)
+        tw = torch.ones(batch * topk, dtype=torch.float32, device=x.device) if per_slot else None
+        L = lib()
+        st = _stream()
+        need = ctypes.c_size_t(0)
+        args = (int(self.dtype), _ptr(self.data_), e, _ptr(xs), k, _ptr(sorted_ids), _ptr(expert_ids),
+                _ptr(tw) if tw is not None else None, topk, _ptr(out), n)
+        check("qmm_moe_forward", L.qmm_moe_forward(*args, None, 0, ctypes.byref(need), k, n, batch * topk, 0, st))
+        buf = torch.empty(max(need.value, 256), dtype=torch.uint8, device=x.device)
+        check("qmm_moe_forward", L.qmm_moe_forward(*args, _ptr(buf), buf.numel(), ctypes.byref(need), k, n,
+                                                   batch * topk, 1, st))
+        return out
+
     def dequantize(self) -> torch.Tensor:
         return self._dequant(False)
 
@@ -209,16 +321,69 @@ class Workspace:
         return self.buf
 
 
+# The reference's switches for arms this build does not have, accepted and
+# without effect here (reported once, when the first QMatMul is made):
+#   CANDLE_DEQUANTIZE_ALL / CANDLE_DEQUANTIZE_ALL_F16 (mod.rs:1138-1180): the
+#     weight dequantized to f32 / f16 at QMatMul::from_arc and multiplied as
+#     a plain tensor; here every weight stays quantized;
+#   SWARMLLM_QMATMUL_CUBLAS / _MIN_ROWS / _ACC (cuda.rs:285-324, 455-470): a
+#     prompt's product dequantized to f16 for cuBLAS from 64 rows; here the
+#     int8 matrix-core kernels serve every row count, summing in int32 / f32;
+#   SWARMLLM_LOAD_PINNED / SWARMLLM_LOAD_READ act in the loader (qmm_gguf_load).
+INACTIVE_KNOBS = ("CANDLE_DEQUANTIZE_ALL", "CANDLE_DEQUANTIZE_ALL_F16", "SWARMLLM_QMATMUL_CUBLAS",
+                  "SWARMLLM_QMATMUL_CUBLAS_MIN_ROWS", "SWARMLLM_QMATMUL_CUBLAS_ACC")
+_KNOBS_REPORTED = False
+
+
+def inactive_knobs_set() -> List[str]:
+    """Those of INACTIVE_KNOBS set in the environment (the reference reads
+    CANDLE_DEQUANTIZE_ALL[_F16] as on when non-empty and not "0")."""
+    out = []
+    for name in INACTIVE_KNOBS:
+        v = os.environ.get(name)
+        if v is None:
+            continue
+        if name.startswith("CANDLE_") and (v == "" or v == "0"):
+            continue
+        out.append(name)
+    return out
+
+
+def _report_inactive_knobs() -> None:
+    global _KNOBS_REPORTED
+    if _KNOBS_REPORTED:
+        return
+    _KNOBS_REPORTED = True
+    on = inactive_knobs_set()
+    if on:
+        warnings.warn(f"{', '.join(on)}: accepted with no effect; every product here runs on the quantized "
+                      "weights' own kernels", RuntimeWarning, stacklevel=3)
+
+
 class QMatMul:
     """QMatMul::QTensor (mod.rs:1131-1273, Module::forward :1360-1383)."""
 
     def __init__(self, qtensor: QTensor):
+        _report_inactive_knobs()
         self.qtensor = qtensor
         self._ws = Workspace()
 
     @staticmethod
     def from_qtensor(qtensor: QTensor) -> "QMatMul":
         return QMatMul(qtensor)
+
+    def accumulate_in_f32(self) -> bool:
+        """QMatMul::accumulate_in_f32 (mod.rs:1181-1200): keep this weight's
+        products in f32. Every product here sums in int32 / f32 already, so
+        nothing changes (qmm_accumulate_in_f32); True, as the reference
+        answers for a weight it holds alone."""
+        if self.qtensor.dtype.is_quantized():
+            check("qmm_accumulate_in_f32", lib().qmm_accumulate_in_f32(int(self.qtensor.dtype)))
+        return True
+
+    def indexed_moe_forward(self, x: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+        """QMatMul::indexed_moe_forward (mod.rs:1265-1272): QTensor.indexed_moe_forward."""
+        return self.qtensor.indexed_moe_forward(x, ids)
 
     def forward(self, xs: torch.Tensor) -> torch.Tensor:
         """x [..., k] f32 -> [..., n]; the CustomOp1 shape rules of cpu_fwd (mod.rs:1280-1333)."""
@@ -421,6 +586,16 @@ def moe_forward(xs: torch.Tensor, experts: QTensor, sorted_ids: torch.Tensor, ex
     buf = (workspace or Workspace()).get(need.value, xs.device)
     check(fn, call(*args, _ptr(buf), buf.numel(), ctypes.byref(need), k, n, size_m, 1, st))
     return out
+
+
+def prepare(dtype: GgmlDType) -> None:
+    """The set-up a first product of `dtype` would do, done now (before a
+    graph capture): qmm_prepare (mmq_prepare_few_rows_once, cuda.rs:890-932)."""
+    check("qmm_prepare", lib().qmm_prepare(int(GgmlDType(dtype))))
+
+
+def prepared(dtype: GgmlDType) -> bool:
+    return bool(lib().qmm_prepared(int(GgmlDType(dtype))))
 
 
 def set_force_dmmv(flag: bool) -> None:

@@ -122,3 +122,19 @@ def test_padded_bytes():
     for t, bs, ts in ((12, 256, 144), (14, 256, 210), (8, 32, 34), (20, 32, 18), (39, 32, 17), (0, 1, 4), (1, 1, 2)):
         assert L.qmm_padded_bytes(t, 4 * bs) == 4 * ts + 512 // bs * ts
     assert L.qmm_padded_bytes(12, 100) == 0 and L.qmm_padded_bytes(5, 64) == 0
+
+
+def test_sizes_past_int64_are_refused(tmp_path):
+    """A tensor whose byte count passes INT64_MAX reads as 0 bytes (refused by
+    the loader), and qmm_padded_bytes answers 0 for such a count."""
+    L = lib()
+    assert L.qmm_padded_bytes(0, 2 ** 62) == 0
+    assert L.qmm_padded_bytes(0, 2 ** 60) == 2 ** 62 + 512 * 4
+    assert L.qmm_padded_bytes(15, 2 ** 62) == 2 ** 54 * 292 + 2 * 292
+    # F32 [2^22, 2^40]: 2^62 values, 2^64 bytes
+    pre = struct.pack("<II", 0x46554747, 3) + struct.pack("<QQ", 1, 0)
+    pre += tiny._str("huge", 3) + struct.pack("<I", 2) + struct.pack("<QQ", 2 ** 40, 2 ** 22) + struct.pack("<IQ", 0, 0)
+    c = Content.read(write(tmp_path, pre))
+    assert c.tensor_infos["huge"].nbytes == 0
+    with pytest.raises(ValueError):
+        c.tensor("huge")
