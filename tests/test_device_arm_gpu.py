@@ -30,6 +30,7 @@ from swarmllm_amd.gguf import (Content, load_quantized_beside, load_quantized_en
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
 V3 = f"{tiny.HERE}/tiny_v3.gguf"
 
 FORMATS = [GgmlDType.Q8_0, GgmlDType.Q4K, GgmlDType.Q6K, GgmlDType.Iq4Nl, GgmlDType.Mxfp4]
@@ -255,6 +256,18 @@ def test_pinned_chunks_and_a_truncated_file(tmp_path):
         c.tensor("big")
 
 
+def run_child(args, env=None, timeout=300):
+    """fresh_child.py in a process of its own (the package on its path), its
+    switches set: a process reads them once."""
+    full = {k: v for k, v in os.environ.items() if not k.startswith("SWARMLLM_LOAD")}
+    full.update(env or {})
+    full["PYTHONPATH"] = ROOT + (os.pathsep + full["PYTHONPATH"] if full.get("PYTHONPATH") else "")
+    print(f"child {args[0]} with {env}", flush=True)
+    res = subprocess.run([sys.executable, "-u", os.path.join(HERE, "fresh_child.py"), *args], env=full, cwd=ROOT,
+                         capture_output=True, text=True, timeout=timeout)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-2000:]
+
+
 @pytest.mark.parametrize("env", [{"SWARMLLM_LOAD_PINNED": "0"}, {"SWARMLLM_LOAD_READ": "fresh"}],
                          ids=["pinned_off", "read_fresh"])
 def test_loader_switches(tmp_path, env):
@@ -262,9 +275,7 @@ def test_loader_switches(tmp_path, env):
     p = tmp_path / "big.gguf"
     data = big_file(p)
     out = str(tmp_path / "o.npz")
-    res = subprocess.run([sys.executable, "-u", os.path.join(HERE, "fresh_child.py"), "load", str(p), "big", out],
-                         env={**os.environ, **env}, capture_output=True, text=True, timeout=300)
-    assert res.returncode == 0, res.stdout + res.stderr
+    run_child(["load", str(p), "big", out], env)
     r = np.load(out)
     assert np.array_equal(r["data"], data) and not r["pad"].any()
     assert int(r["chunks"][0]) == 0
@@ -280,13 +291,12 @@ def test_first_product_under_capture(tmp_path):
     capture and the no-allocation entry's first call under capture (after
     qmm_prepare) replay to the eager results bit for bit."""
     out = str(tmp_path / "c.npz")
-    res = subprocess.run([sys.executable, "-u", os.path.join(HERE, "fresh_child.py"), "capture", out],
-                         capture_output=True, text=True, timeout=300)
-    assert res.returncode == 0, res.stdout + res.stderr
+    run_child(["capture", out])
     r = np.load(out)
     assert not r["prepared_before"][0] and not r["prepared_after_capture"][0] and r["prepared_after_eager"][0]
-    assert "skinny" not in str(r["kernel_first"]), str(r["kernel_first"])
-    assert "skinny" in str(r["kernel_eager"]) and "skinny" in str(r["kernel_second"])
+    # launch_sk: the few-row matrix-core kernel's launcher
+    assert "launch_sk" not in str(r["kernel_first"]), str(r["kernel_first"])
+    assert "launch_sk" in str(r["kernel_eager"]) and "launch_sk" in str(r["kernel_second"])
     assert np.array_equal(r["y_second0"], r["y_eager"]) and np.array_equal(r["y_second1"], r["y_eager"])
     # the first (decode-kernel) product against the oracle
     w = QTensor.quantize(fill_normal(4096 * 4096, seed=91, std=0.02).reshape(4096, 4096), GgmlDType.Q4K)
