@@ -132,6 +132,17 @@ int qmm_mmq_few_rows_line(int type, int64_t *fewest_rows, int64_t *least_bytes);
 int64_t qmm_mmq_max_rows(void);
 int qmm_mmq_captured(void);
 
+/* SWARMLLM_QMATMUL_EXACT=1|on|true (read once; no counterpart in the
+ * reference): the exact Q4_K / Q6_K kernels only. Without it three kernels
+ * feed the matrix cores a rounded product of a code and its sub-block scale
+ * (normalised error up to about 1e-3, inside the 2e-3 bound): the
+ * single-pass Q4_K and Q6_K GEMMs (from 129 rows) and the few-row Q6_K
+ * kernel's single-product form (k >= 2048, from the few-rows line to 32 rows), so a product's bits
+ * can depend on the row count of its batch (1-2 rows are always exact). With
+ * it every row count sums exact int32 products, at the exact kernels' speed.
+ * qmm_exact_forms: 1 when the switch is on. */
+int qmm_exact_forms(void);
+
 /* set_force_dmmv (quantized/cuda.rs:29-33): while on, qmm_forward,
  * qmm_forward_shared and qmm_forward_glu dequantize each weight value (as
  * qmm_dequantize does) against the f32 activation and sum in f32, without
@@ -184,10 +195,15 @@ int qmm_forward(int type, const void *w, const float *x, int64_t x_stride, float
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc); the entry
  * point itself allocates nothing. Products whose quantized activation
- * exceeds the scratch return QMM_WORKSPACE_TOO_SMALL with nothing enqueued
- * (a GEMM whose K-split slots do not fit beside it runs uncut). All
+ * exceeds the scratch return QMM_WORKSPACE_TOO_SMALL with nothing enqueued.
+ * Results equal, bit for bit, qmm_forward's with a workspace of
+ * qmm_forward_noalloc_max_bytes() bytes: so qmm_forward's with the
+ * workspace it plans (*need) whenever that need fits the scratch. A larger
+ * planned need (a single-pass GEMM's K-split slots beside the activation,
+ * e.g. 4096 x 4096 at 512 rows) runs as qmm_forward does with a workspace
+ * that holds the activation only: Q4_K uncut, Q6_K on its exact GEMM. All
  * calls on one GPU share the scratch: calls that overlap on one GPU (other
- * streams, other threads) race on it. Results equal qmm_forward's bit for bit. */
+ * streams, other threads) race on it. */
 int qmm_forward_noalloc(int type, const void *w, const float *x, int64_t x_stride, float *dst, int64_t ldd,
                         int64_t k, int64_t n, int64_t rows, int64_t stream);
 size_t qmm_forward_noalloc_max_bytes(void);

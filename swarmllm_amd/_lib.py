@@ -38,6 +38,7 @@ SIGNATURES = {
     "qmm_mmq_few_rows_line": (_I, [_I, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "qmm_mmq_max_rows": (_I64, []),
     "qmm_mmq_captured": (_I, []),
+    "qmm_exact_forms": (_I, []),
     "qmm_set_force_dmmv": (None, [_I]),
     "qmm_force_dmmv": (_I, []),
     "qmm_matvec": (_I, [_I, _P, _P, _P, _I64, _I64, _I64, _I64, _I64]),

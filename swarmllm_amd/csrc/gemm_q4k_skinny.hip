@@ -588,7 +588,8 @@ hipError_t launch_gemm_q4k_skinny(const MvTargets& t, int64_t k, const ActPlanes
   // 7.68 -> 6.68 / 7.30 ms a forward; four a stage hold 122 KiB of LDS, one
   // workgroup a CU, 7.51 / 8.19; one a stage 6.75 / 7.41); the choice is each
   // weight's own, so a weight's bits do not depend on the weights it shares
-  // a launch with
+  // a launch with. Its lanes form weight offsets in 32 bits, so a weight of
+  // 4 GiB or more stays on the register-staged kernel (64-bit addressing).
   constexpr int kDmaSbs = 2;
   MvTargets wide{}, narrow{};
   if (rows <= 16 && nsb % kDmaSbs == 0) {
@@ -596,8 +597,9 @@ hipError_t launch_gemm_q4k_skinny(const MvTargets& t, int64_t k, const ActPlanes
     for (int i = 0; i < t.count; i++) {
       const int64_t n = t.row_end[i] - prev;
       prev = t.row_end[i];
-      MvTargets& g = n >= (int64_t)64 * cus ? wide : narrow;
-      int64_t& e = n >= (int64_t)64 * cus ? we : ne;
+      const bool to_dma = n >= (int64_t)64 * cus && n * nsb * 144 < ((int64_t)1 << 32);
+      MvTargets& g = to_dma ? wide : narrow;
+      int64_t& e = to_dma ? we : ne;
       e += n;
       g.w[g.count] = t.w[i];
       g.dst[g.count] = t.dst[i];

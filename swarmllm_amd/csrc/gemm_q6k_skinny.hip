@@ -353,8 +353,9 @@ hipError_t launch_gemm_q6k_skinny(const MvTargets& t, int64_t k, const ActPlanes
   (void)cus;
   const int nsb = (int)(k / 256);
   // the single-product form from k = 2048 (its rounding stays well inside
-  // the 2e-3 bound there); shorter rows keep the exact form
-  if (k >= 2048) {
+  // the 2e-3 bound there); shorter rows, and every row under
+  // SWARMLLM_QMATMUL_EXACT, keep the exact form
+  if (k >= 2048 && !exact_forms()) {
     if (rows <= 16) return launch_q6<1, 1, 4, true>(t, nsb, p, rows, st);
     return launch_q6<2, 1, 4, true>(t, nsb, p, rows, st);
   }

@@ -147,6 +147,16 @@ const MmqPolicy& mmq_policy() {
 
 bool is_kquant(int type) { return type == qmm::T_Q4_K || type == qmm::T_Q6_K; }
 
+// SWARMLLM_QMATMUL_EXACT=1|on|true, read once: the exact Q4_K / Q6_K kernels
+// only. Without it, three kernels feed the matrix cores a rounded product of
+// a code and its sub-block scale (the single-pass Q4_K and Q6_K GEMMs from
+// gemm_q4k_sp_min_rows() rows, the single-product form of the few-row Q6_K
+// kernel from k = 2048), so a product's bits can depend on how many rows
+// its batch has; with it, every row count sums exact int32 products.
+bool env_is_on(const char* v) {
+  return v && (std::strcmp(v, "1") == 0 || std::strcmp(v, "on") == 0 || std::strcmp(v, "true") == 0);
+}
+
 // The few-rows line of a type: (fewest rows, least weight bytes).
 void few_rows_line(int type, int64_t& rows, int64_t& bytes) {
   const MmqPolicy& pol = mmq_policy();
@@ -261,6 +271,10 @@ bool matrix_takes(int type, const void* w, const void* xq, int64_t n, int64_t k,
 // the exact two-pass kernel, whose 128-row tiles waste less on short batches.
 hipError_t launch_gemm(int type, const void* w, int64_t n, int64_t k, const qmm::ActPlanes& p, int64_t rows,
                        float* dst, int64_t ldd, hipStream_t st) {
+  if (qmm::exact_forms()) {
+    if (type == qmm::T_Q6_K) return qmm::launch_gemm_q6k(w, n, k, p, rows, dst, ldd, st);
+    if (type == qmm::T_Q4_K) return qmm::launch_gemm_q4k(w, n, k, p, rows, dst, ldd, st);
+  }
   if (type == qmm::T_Q6_K) {
     // without a workspace for K splits, the single-pass Q6_K GEMM only where
     // its tiles fill the CUs (uncut, its per-super-block work is ~1.5x the
@@ -279,7 +293,7 @@ hipError_t launch_gemm(int type, const void* w, int64_t n, int64_t k, const qmm:
 // Products the single-pass Q4_K GEMM takes: those it can cut along K and
 // launch several of at once (launch_gemm_q4k_sp_targets).
 bool sp_takes(int type, const void* w, const void* xq, int64_t n, int64_t k, int64_t rows, hipStream_t st) {
-  if (type != qmm::T_Q4_K && type != qmm::T_Q6_K) return false;
+  if ((type != qmm::T_Q4_K && type != qmm::T_Q6_K) || qmm::exact_forms()) return false;
   if (!gemm_takes(type, w, xq, n, k, rows, st) || rows < qmm::gemm_q4k_sp_min_rows()) return false;
   return type == qmm::T_Q4_K ? qmm::gemm_q4k_sp_fits(n, k, rows) : qmm::gemm_q6k_sp_fits(n, k, rows);
 }
@@ -351,6 +365,11 @@ hipError_t launch_stream_targets(int type, int count, const void* const* w, cons
 }  // namespace
 
 namespace qmm {
+bool exact_forms() {
+  static const bool on = env_is_on(std::getenv("SWARMLLM_QMATMUL_EXACT"));
+  return on;
+}
+
 namespace {
 std::atomic<const char*> g_last_kernel{""};
 
@@ -503,6 +522,8 @@ int64_t qmm_mmq_max_rows(void) {
 }
 
 int qmm_mmq_captured(void) { return mmq_policy().captured ? 1 : 0; }
+
+int qmm_exact_forms(void) { return qmm::exact_forms() ? 1 : 0; }
 
 int qmm_matvec(int type, const void* w, const void* xq, float* dst, int64_t ldd, int64_t k, int64_t n, int64_t rows,
                int64_t stream) {

@@ -224,6 +224,9 @@ hipError_t launch_gemm_q6k(const void* w, int64_t n, int64_t k, const ActPlanes&
 // every kernel that asks for more than 64 KiB, on the current device, and
 // the no-allocation scratch's address there.
 hipError_t raise_all_lds_limits();
+
+// SWARMLLM_QMATMUL_EXACT (read once): only the exact Q4_K / Q6_K forms.
+bool exact_forms();
 bool noalloc_prepare();
 
 }  // namespace qmm

@@ -4,7 +4,8 @@ switches are read once per process, so each setting runs in a fresh one.
 Reads a JSON list of products from argv[1] ({"type", "n", "k", "rows",
 "seed", "capture"}), runs each through QMatMul.forward (eagerly, or captured
 as a HIP graph and replayed), and writes to argv[2] an .npz with each
-product's output and the decode/matrix-core launch counts its call added.
+product's output, the decode/matrix-core launch counts its call added and
+the launcher of its last kernel (qmm_last_kernel).
 """
 import json
 import sys
@@ -42,7 +43,7 @@ def product(spec):
         y = mm.forward(x)
         mv, gm = L.qmm_matvec_launches() - mv0, L.qmm_gemm_launches() - gm0
         torch.cuda.synchronize()
-    return y.cpu().numpy(), mv, gm
+    return y.cpu().numpy(), mv, gm, L.qmm_last_kernel().decode()
 
 
 def main():
@@ -50,9 +51,10 @@ def main():
     out = {}
     for i, spec in enumerate(specs):
         print(f"product {i}: {spec}", flush=True)
-        y, mv, gm = product(spec)
+        y, mv, gm, kernel = product(spec)
         out[f"y{i}"] = y
         out[f"launches{i}"] = np.array([mv, gm], np.int64)
+        out[f"kernel{i}"] = np.array(kernel)
     np.savez(sys.argv[2], **out)
     print("done", flush=True)
 

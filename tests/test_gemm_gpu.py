@@ -327,9 +327,36 @@ def test_q4k_skinny_c5_gate_projection(rows):
     x = activations(rng, rows, 8192)
     qt, wq = q4k(w)
     y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    assert "launch_sk_dma" in lib().qmm_last_kernel().decode()  # the copy-staged kernel
     want = qref.matmul(qref.Q4_K, x, wq, 28672)
     wdeq = qref.to_float(qref.Q4_K, wq, 28672 * 8192).reshape(28672, 8192)
     assert normalised_error(y, want, wdeq, x) <= TIGHT
+
+
+@pytest.mark.parametrize("rows", [4, 13])
+def test_q4k_skinny_copy_staged_ragged_weight(rows):
+    """A wide weight (at least 64 rows a CU: the copy-staged kernel) whose
+    rows are not a multiple of 16 and whose 16-row tiles are not a multiple
+    of the 4 a workgroup takes (16390 rows: 1025 tiles), so the last tile
+    is ragged and the last workgroup has dead tiles; against the oracle, and
+    shared with a narrow weight equal to each weight's own forward."""
+    from swarmllm_amd import fill_normal
+
+    n, k = 16390, 2048
+    rng = np.random.default_rng(80 + rows)
+    w = weights(rng, n, k)
+    x = activations(rng, rows, k, outliers=True)
+    qt, wq = q4k(w)
+    mm = QMatMul(qt)
+    y = mm.forward(upload(x))
+    assert "launch_sk_dma" in lib().qmm_last_kernel().decode()
+    want = qref.matmul(qref.Q4_K, x, wq, n)
+    wdeq = qref.to_float(qref.Q4_K, wq, n * k).reshape(n, k)
+    assert normalised_error(y.cpu().numpy(), want, wdeq, x) <= TIGHT
+    narrow = QMatMul(QTensor.quantize(fill_normal(300 * k, seed=81, std=0.02).reshape(300, k), GgmlDType.Q4K))
+    xs = upload(x)
+    shared = QMatMul.forward_shared(xs, [mm, narrow])
+    assert torch.equal(shared[0], y) and torch.equal(shared[1], narrow.forward(xs))
 
 
 @pytest.mark.parametrize("rows", [6, 16, 30])
@@ -412,6 +439,8 @@ def test_q6k_skinny_c5_down_projection(rows):
     x = activations(rng, rows, 28672)
     qt, wq = q6k(w)
     y = QMatMul(qt).forward(upload(x)).cpu().numpy()
+    kernel = lib().qmm_last_kernel().decode()
+    assert "launch_q6" in kernel and "ONE = true" in kernel, kernel  # the single-product form
     want = qref.matmul(qref.Q6_K, x, wq, 8192)
     wdeq = qref.to_float(qref.Q6_K, wq, 8192 * 28672).reshape(8192, 28672)
     assert normalised_error(y, want, wdeq, x) <= ONE_Q6K

@@ -167,3 +167,29 @@ def test_mmq_captured_off_keeps_captured_few_rows_products_on_the_decode_kernels
     assert np.array_equal(yc.view(np.uint32), per_row(mm, x).view(np.uint32))
     assert np.array_equal(ye.view(np.uint32), mm.forward(x).cpu().numpy().view(np.uint32))
     assert oracle_error(mm, x, ye) <= TOL_GEMM
+
+
+def test_exact_forms_switch(tmp_path):
+    """SWARMLLM_QMATMUL_EXACT=1: the products the approximate-operand kernels
+    take by default (the single-pass Q4_K / Q6_K GEMMs from 129 rows, the
+    few-row Q6_K single-product form from k = 2048) run on the exact
+    kernels, within the exact kernels' bound of the oracle."""
+    specs = [{"type": 12, "n": 1024, "k": 4096, "rows": 256, "seed": 41},
+             {"type": 14, "n": 1024, "k": 4096, "rows": 256, "seed": 42},
+             {"type": 14, "n": 2048, "k": 4096, "rows": 8, "seed": 43}]
+    got = run_child({"SWARMLLM_QMATMUL_EXACT": "1"}, specs, tmp_path)
+    kernels = np.load(str(tmp_path / "child.npz"))
+    names = [str(kernels[f"kernel{i}"]) for i in range(len(specs))]
+    assert "launch_gemm_q4k(" in names[0], names[0]
+    assert "launch_gemm_q6k(" in names[1], names[1]
+    assert "launch_q6" in names[2] and "ONE = false" in names[2], names[2]
+    for (y, _), spec in zip(got, specs):
+        mm, x = same_inputs(spec)
+        assert oracle_error(mm, x, y) <= 5e-4, spec
+    # without the switch (this process) the same products take the
+    # approximate forms
+    assert lib().qmm_exact_forms() == 0
+    for spec, want in zip(specs, ("launch_gemm_q4k_sp", "launch_gemm_q6k_sp", "ONE = true")):
+        mm, x = same_inputs(spec)
+        mm.forward(x)
+        assert want in lib().qmm_last_kernel().decode(), spec
