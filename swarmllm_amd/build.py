@@ -15,4 +15,8 @@ def build_library(jobs: int = 4, force: bool = True) -> str:
     out = os.path.join(HERE, "libqmm.so")
     if not os.path.exists(out):
         raise RuntimeError("libqmm.so was not produced")
+    # the M0 invariant of csrc/lds_copy.h over the AMD assembly just built
+    from .m0_check import check_build
+
+    check_build(os.path.join(CSRC, "_build"))
     return out
