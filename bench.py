@@ -325,6 +325,38 @@ def gate_up_glu(layers, stream, reps: int) -> dict:
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def read_floor(layers, stream, reps: int) -> dict:
+    """The bare streaming read the decode launches are held against
+    (qmm_read_floor: one launch that reads the bytes once and does nothing
+    else), over the gate weight (33 MB, the single product's bytes) and the
+    gate and up weights together (66 MB, the gate+up launch's), back to back
+    over the layer copies in one graph, timed with HIP events on its stream."""
+    import torch
+
+    from swarmllm_amd._lib import check, lib
+
+    L = lib()
+    sink = torch.empty(L.qmm_read_floor_sink_bytes(), dtype=torch.uint8, device="cuda")
+    per_graph = 4 * len(layers)
+    gate_bytes = 14336 * 16 * 144
+    res = {"kernel": "read_kernel (qmm_read_floor: 1024 workgroups x 512 threads, 16-byte nontemporal loads)"}
+    for name, two in (("bytes_33mb", False), ("bytes_66mb", True)):
+        def fn(st, two=two):
+            for i in range(per_graph):
+                lay = layers[i % len(layers)]
+                check("qmm_read_floor", L.qmm_read_floor(lay.w["gate"].data_.data_ptr(), gate_bytes,
+                                                         lay.w["up"].data_.data_ptr() if two else None,
+                                                         gate_bytes if two else 0, sink.data_ptr(), st))
+
+        g = capture(fn, stream)
+        settle(g.replay, stream)
+        ms = time_gpu(lambda: [g.replay() for _ in range(reps)], stream)
+        us = ms * 1e3 / (reps * per_graph)
+        nbytes = gate_bytes * (2 if two else 1)
+        res[name] = {"bytes": nbytes, "us_per_launch": round(us, 4), "gbs": round(nbytes / (us * 1e-6) / 1e9, 2)}
+    return res
+
+
 def prefill_inputs(M: int, n: int, k: int):
     """C3's activation (N(0,1), 1% of channels x20) quantized once to Q8_K
     planes, and the output buffer."""
@@ -894,6 +926,18 @@ def profile_only(which: str, layers, outs, stream, reps: int) -> None:
         torch.cuda.synchronize()
         log(f"profile copy: {reps} copies of {COPY_BYTES} bytes")
         return
+    if which in ("read33", "read66"):
+        sink = torch.empty(L.qmm_read_floor_sink_bytes(), dtype=torch.uint8, device="cuda")
+        gate_bytes = 14336 * 16 * 144
+        two = which == "read66"
+        for i in range(reps):
+            lay = layers[i % len(layers)]
+            check("qmm_read_floor", L.qmm_read_floor(lay.w["gate"].data_.data_ptr(), gate_bytes,
+                                                     lay.w["up"].data_.data_ptr() if two else None,
+                                                     gate_bytes if two else 0, sink.data_ptr(), s))
+        torch.cuda.synchronize()
+        log(f"profile {which}: {reps} bare reads of {gate_bytes * (2 if two else 1)} bytes over {len(layers)} copies")
+        return
     if which == "single":
         x, ws = layers[0].acts["ffn_in"]
         n, k = 14336, 4096
@@ -1006,8 +1050,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="skip the C1 / C4 / C5 sections")
-    ap.add_argument("--profile", choices=["single", "dominant", "prefill", "prefill_forward", "prefill_down",
-                                          "prefill_down_forward", "copy"],
+    ap.add_argument("--profile", choices=["single", "dominant", "read33", "read66", "prefill", "prefill_forward",
+                                          "prefill_down", "prefill_down_forward", "copy"],
                     help="launch only this kernel --steps times (for rocprofv3 counter passes), print no JSON")
     args = ap.parse_args()
 
@@ -1031,6 +1075,15 @@ def main() -> int:
         return 1
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} ({getattr(props, 'gcnArchName', '?')}), {props.multi_processor_count} CUs")
+    # every timed product is captured into a graph before it first runs, so
+    # the types are prepared first, as a runtime that captures before any
+    # eager product does (qmm_prepare; the reference's
+    # mmq_prepare_few_rows_once): else captured products of up to 8 rows
+    # stay on the decode kernels
+    for t in (8, 12, 14, 20, 39):
+        if L.qmm_prepare(t) != 0:
+            print(f"bench.py: qmm_prepare({t}) failed", file=sys.stderr)
+            return 1
 
     stream = torch.cuda.Stream()  # default priority
     acts, outs = make_acts()
@@ -1071,6 +1124,9 @@ def main() -> int:
     log(f"gate+up launch: {gu['us']:.3f} us/launch, {gu['gbs']:.1f} GB/s")
     gl = gate_up_glu(layers, stream, args.kernel_reps)
     log(f"gate+up+GLU launch: {gl['us_per_launch']:.3f} us/launch, {gl['gbs']:.1f} GB/s")
+    rf = read_floor(layers, stream, args.kernel_reps)
+    log(f"bare read floor: 33 MB {rf['bytes_33mb']['us_per_launch']:.3f} us, "
+        f"66 MB {rf['bytes_66mb']['us_per_launch']:.3f} us a launch")
 
     pre = prefill_gemm(layers, stream, max(2, args.kernel_reps // 5))
     log(f"prefill GEMM (gate): {pre['us_per_launch']:.2f} us/launch, {pre['tops']:.1f} TOP/s; "
@@ -1119,6 +1175,7 @@ def main() -> int:
                     "gbs": round(gu["gbs"], 2), "frac": round(gu["gbs"] / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic("gate_up")},
         "gate_up_glu": gl,
+        "read_floor": rf,
         "cpu_baseline": cpu,
         "prefill": pre,
         "prefill_down": pre_down,

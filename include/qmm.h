@@ -454,6 +454,16 @@ size_t qmm_wire_bytes(int64_t n);
 int qmm_wire_encode(const float *x, int64_t n, void *out, int64_t stream);
 int qmm_wire_decode(const void *in, size_t in_bytes, int64_t n, float *out, int64_t stream);
 
+/* The bare streaming read a product's weight bytes are measured against (a
+ * measurement aid; no counterpart in the reference): one launch that reads
+ * a_bytes at a and b_bytes at b once (16-byte aligned spans, sizes multiples
+ * of 16), 1024 workgroups of 512 threads in 16-byte nontemporal loads, and
+ * writes one word per workgroup to sink (qmm_read_floor_sink_bytes()). Its
+ * duration over a weight's bytes is the floor a one-launch product of that
+ * weight is held against. */
+size_t qmm_read_floor_sink_bytes(void);
+int qmm_read_floor(const void *a, size_t a_bytes, const void *b, size_t b_bytes, void *sink, int64_t stream);
+
 /* Fault injection, host side (the reference's fail_the_next_mmq_allocation,
  * quantized/cuda.rs:972-991): the next qmm_forward launch returns
  * QMM_NO_ROOM without enqueuing anything, once. */

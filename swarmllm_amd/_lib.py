@@ -97,6 +97,8 @@ SIGNATURES = {
     "qmm_accumulate_in_f32": (_I, [_I]),
     "qmm_gather_row_bytes": (_I, [_I, _I64, ctypes.POINTER(_SZ)]),
     "qmm_gather_rows": (_I, [_I, _P, _SZ, _I64, _I64, _P, _I64, _P, _SZ, _P, _I64]),
+    "qmm_read_floor_sink_bytes": (_SZ, []),
+    "qmm_read_floor": (_I, [_P, _SZ, _P, _SZ, _P, _I64]),
 }
 
 _lib = None

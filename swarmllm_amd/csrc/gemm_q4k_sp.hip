@@ -241,10 +241,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kq_sp_kernel(const SpArgs a)
   const int P = Q6 ? 1 : pick(a.per);
   const int mtiles = a.mtiles;
   const int loc = idx - u0;
-  const int mt = loc % mtiles, rest = loc / mtiles;
-  const int split = (rest % (S / P)) * P, ct = rest / (S / P);
-  const uint8_t* __restrict__ W = (const uint8_t*)pick(a.w);
+  // a weight's units: row tiles fastest, then column tiles, then the split
+  // groups, so the units an XCD takes (consecutive, through the remap) share
+  // one K range: the activation columns an XCD reads are M x K/S (C3's down
+  // product, 512 x 14336 cut in 4: 1.8 MB an XCD, which its L2 holds; with
+  // the splits fastest every XCD read the whole 7.3 MB activation)
   const int64_t N = pick(a.n);
+  const int ctiles = (int)((N + kBN - 1) / kBN);
+  const int mt = loc % mtiles, rest = loc / mtiles;
+  const int ct = rest % ctiles, split = (rest / ctiles) * P;
+  const uint8_t* __restrict__ W = (const uint8_t*)pick(a.w);
   const int nsb = a.nsb;
   const int8_t* __restrict__ yq = a.yq;
   const float* __restrict__ yd = a.yd;
