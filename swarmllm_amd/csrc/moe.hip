@@ -24,9 +24,6 @@
 // (b32_common.h, wave_sum_dpp), so each pair's result is bit-identical to
 // the same product through qmm_forward (times its scale): the reference's
 // "matmul_many equals per-job forward" (quantized/mod.rs:743-745).
-#include <cstdio>
-#include <cstdlib>
-
 #include "b32_common.h"
 
 namespace qmm {
@@ -143,6 +140,7 @@ __global__ __launch_bounds__(64 * kMoeWaves) void moe_b32_kernel(
 // (mv_b32s.hip), so each entry's result is bit-identical to qmm_forward of
 // its input row, times its scale.
 constexpr int kMoeSWaves = 8;  // two workgroups a CU: one streams while the other starts
+constexpr int kMoeRing = 2;        // spans in flight per wave
 constexpr int kMoeActLoads = 4;    // 16-byte activation pieces a lane copies (k <= 4096; cv0..cv3)
 constexpr int kMoeScaleLoads = 2;  // and block scales (cd0, cd1)
 static_assert(kMoeSWaves == kMoePairs, "a wave copies each entry's activation row");
@@ -159,7 +157,7 @@ struct MoeSpan {
   int len;
 };
 
-template <int FMT, int kMoeRing>
+template <int FMT>
 __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu(4))) void moe_b32s_kernel(
     const uint8_t* __restrict__ W, int64_t n, int nb, int64_t estride, int num_experts,
     const int8_t* __restrict__ yq, const float* __restrict__ yd, const int32_t* __restrict__ runs,
@@ -374,32 +372,14 @@ hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, co
   // wave lengthen each wave's chain of two-rows-in-flight steps more than
   // fewer workgroups save in fills)
   (void)cus;
-  int ring = 2;
-  int64_t rpw = 8;
-  if (const char* tv = std::getenv("QMM_MOE_TUNE")) {
-    int a = 0, b = 0;
-    if (sscanf(tv, "%d,%d", &a, &b) == 2) { ring = a; rpw = b; }
-  }
+  const int64_t rpw = 8;
   const int64_t rows_per_wg = (int64_t)kMoeSWaves * rpw;
   const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
   const size_t lds = ((size_t)kMoePairs * (k + nb * 4) + 15) / 16 * 16 + (size_t)kMoeSWaves * MoeSpan<FMT>::kStage;
-  auto go = [&](auto kfn) {
-    kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
-                                            topk_w, topk, (int)size_m, dst, ldd, (int)rpw);
-  };
-  if (ring == 4) {
-    constexpr auto* kfn = &moe_b32s_kernel<FMT, 4>;
-    if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
-    go(kfn);
-  } else if (ring == 3) {
-    constexpr auto* kfn = &moe_b32s_kernel<FMT, 3>;
-    if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
-    go(kfn);
-  } else {
-    constexpr auto* kfn = &moe_b32s_kernel<FMT, 2>;
-    if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
-    go(kfn);
-  }
+  constexpr auto* kfn = &moe_b32s_kernel<FMT>;
+  if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
+  kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
+                                          topk_w, topk, (int)size_m, dst, ldd, (int)rpw);
   return hipGetLastError();
 }
 
