@@ -8,19 +8,22 @@
 
 namespace qmm {
 
-// 16-entry int8 table lookup of the 4 nibbles in the bytes of n (each < 16).
-__device__ __forceinline__ int32_t lut16(uint32_t n, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
-  const uint32_t sel = n & 0x07070707u;
+// 16-entry int8 table lookup of the 4 nibbles at bit sh (0 or 4) of the
+// bytes of n. Entries 0-7 (t0, t1) and 8-15 (t2, t3) are each looked up by
+// the nibble's low 3 bits, and a third byte permute takes byte i from the
+// first (selector i) or, where the nibble's bit 3 is set, from the second
+// (selector i + 4): six or seven instructions for 4 values. The selector is
+// one v_and_or_b32 (the compiler otherwise splits it into an and and an or
+// with literal operands, which a three-operand instruction cannot take on
+// gfx9); its two constants come in registers, the mask a scalar one.
+__device__ __forceinline__ int32_t lut16_at(uint32_t n, int sh, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  const uint32_t v = n >> sh;
+  const uint32_t sel = v & 0x07070707u;
   const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
   const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
-  // bit 3 of each nibble spread over its byte: t * 255 as (t << 8) - t, two
-  // full-rate instructions where the 32-bit multiply runs at quarter rate
-  // (the empty asm keeps the compiler from folding them back into it)
-  const uint32_t t = (n >> 3) & 0x01010101u;
-  uint32_t t8 = t << 8;
-  asm("" : "+v"(t8));
-  const uint32_t m = t8 - t;
-  return (int32_t)((hi & m) | (lo & ~m));
+  uint32_t pick;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(pick) : "v"(v >> 1), "s"(0x04040404u), "v"(0x03020100u));
+  return (int32_t)__builtin_amdgcn_perm(hi, lo, pick);
 }
 
 __device__ __forceinline__ uint32_t pack4(const int8_t* t) {
@@ -54,8 +57,8 @@ struct Fmt32<T_IQ4_NL> {
     lds_words<4>(L, off + 2, n);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      q[i] = (uint32_t)lut16(n[i] & 0x0F0F0F0Fu, t0, t1, t2, t3);
-      q[4 + i] = (uint32_t)lut16((n[i] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
+      q[i] = (uint32_t)lut16_at(n[i], 0, t0, t1, t2, t3);
+      q[4 + i] = (uint32_t)lut16_at(n[i], 4, t0, t1, t2, t3);
     }
   }
 };
@@ -69,13 +72,13 @@ struct Fmt32<T_MXFP4> {
     lds_words<4>(L, off + 1, n);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      q[i] = (uint32_t)lut16(n[i] & 0x0F0F0F0Fu, t0, t1, t2, t3);
-      q[4 + i] = (uint32_t)lut16((n[i] >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);
+      q[i] = (uint32_t)lut16_at(n[i], 0, t0, t1, t2, t3);
+      q[4 + i] = (uint32_t)lut16_at(n[i], 4, t0, t1, t2, t3);
     }
   }
 };
 
-// The lookup table of a format, packed for lut16.
+// The lookup table of a format, packed for lut16_at.
 template <int FMT>
 struct Lut32 {
   uint32_t t0, t1, t2, t3;

@@ -68,8 +68,8 @@ __device__ __forceinline__ void b32_lane(const uint8_t* win, int off, int kq, co
     uint32_t n[2];
     lds_words<2>(win, off + B32Shape<FMT>::Head + 8 * (kq & 1), n);
     const int sh = 4 * (kq >> 1);
-    q[0] = (uint32_t)lut16((n[0] >> sh) & 0x0F0F0F0Fu, lut.t0, lut.t1, lut.t2, lut.t3);
-    q[1] = (uint32_t)lut16((n[1] >> sh) & 0x0F0F0F0Fu, lut.t0, lut.t1, lut.t2, lut.t3);
+    q[0] = (uint32_t)lut16_at(n[0], sh, lut.t0, lut.t1, lut.t2, lut.t3);
+    q[1] = (uint32_t)lut16_at(n[1], sh, lut.t0, lut.t1, lut.t2, lut.t3);
   }
 }
 

@@ -277,8 +277,8 @@ __device__ __forceinline__ void pf_stage(const uint8_t* win, int o, int hf, int 
         if (table) {
 #pragma unroll
           for (int t = 0; t < 2; t++) {
-            const uint32_t c0 = (uint32_t)lut16(t ? (q[0] >> 4) & 0x0F0F0F0Fu : q[0] & 0x0F0F0F0Fu, t0, t1, t2, t3);
-            const uint32_t c1 = (uint32_t)lut16(t ? (q[1] >> 4) & 0x0F0F0F0Fu : q[1] & 0x0F0F0F0Fu, t0, t1, t2, t3);
+            const uint32_t c0 = (uint32_t)lut16_at(q[0], t ? 4 : 0, t0, t1, t2, t3);
+            const uint32_t c1 = (uint32_t)lut16_at(q[1], t ? 4 : 0, t0, t1, t2, t3);
             bv[t] = deq8<BF>(c0 ^ 0x80808080u, c1 ^ 0x80808080u, d, -128.0f * d);
           }
         }
