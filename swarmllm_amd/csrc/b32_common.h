@@ -122,20 +122,25 @@ __device__ __forceinline__ void load_act64(Act64& a, const int8_t* __restrict__ 
 }
 
 // acc + the unit's two block dots: (dx0 dy0) s0 + (dx1 dy1) s1 with exact
-// int32 block sums s and every f32 operation rounded explicitly (the block
+// int32 block sums s and every f32 operation rounded on its own, none
+// contracted into an fma (the block
 // dot of candle's vec_dot per type: Q8_0 k_quants.rs:1294-1312, MXFP4
 // :517-527, IQ4_NL :754-764).
 __device__ __forceinline__ float b32_unit(const uint32_t q0[8], const uint32_t q1[8], float dx0, float dx1,
                                           const Act64& a, float acc) {
+#pragma clang fp contract(off)
   int s0 = 0, s1 = 0;
 #pragma unroll
   for (int t = 0; t < 8; t++) {
     s0 = dot4((int)q0[t], a.y[0][t], s0);
     s1 = dot4((int)q1[t], a.y[1][t], s1);
   }
-  const float p0 = __fmul_rn(__fmul_rn(dx0, a.dy[0]), (float)s0);
-  const float p1 = __fmul_rn(__fmul_rn(dx1, a.dy[1]), (float)s1);
-  return __fadd_rn(acc, __fadd_rn(p0, p1));
+  // plain operators: the pragma governs only the operations written here
+  // (__fmul_rn and __fadd_rn are ordinary * and + in functions of their own,
+  // which the compiler may still fuse once inlined)
+  const float p0 = (dx0 * a.dy[0]) * (float)s0;
+  const float p1 = (dx1 * a.dy[1]) * (float)s1;
+  return acc + (p0 + p1);
 }
 
 }  // namespace qmm

@@ -160,6 +160,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q4k_skinny_kernel(MvTargets 
 
   // one super-block from the buffer: both passes, the min pass, the f32 epilogue
   auto compute = [&](const SkAct<MT>& act) {
+    // each f32 operation rounded on its own (no contraction into fma)
+#pragma clang fp contract(off)
 #pragma unroll
     for (int b = 0; b < NB; b++) {
       const uint8_t* rowp = buf + (16 * b + r16) * 144;
@@ -217,8 +219,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q4k_skinny_kernel(MvTargets 
       for (int m = 0; m < MT; m++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          accD[b][m][i] = __fadd_rn(accD[b][m][i], __fmul_rn(__fmul_rn(dw, act.dy[m][i]), (float)T[m][i]));
-          accM[b][m][i] = __fadd_rn(accM[b][m][i], __fmul_rn(__fmul_rn(dmin, act.dy[m][i]), (float)Tm[m][i]));
+          accD[b][m][i] = accD[b][m][i] + (dw * act.dy[m][i]) * (float)T[m][i];
+          accM[b][m][i] = accM[b][m][i] + (dmin * act.dy[m][i]) * (float)Tm[m][i];
         }
     }
   };
@@ -433,6 +435,8 @@ __global__ __launch_bounds__(256) void gemm_q4k_skinny_dma_kernel(const SkDmaArg
   // one super-block j of stage st: both passes, the min pass, the f32 epilogue
   // (the register-staged kernel's arithmetic)
   auto compute1 = [&](int st, int j) {
+    // each f32 operation rounded on its own (no contraction into fma)
+#pragma clang fp contract(off)
     const uint8_t* const base = smem + st * D::kStage;
     const uint8_t* rowp = base + wv * D::kWStage + r16 * (16 * D::kWSlots) + 144 * j;
     const uint4 hdr = *(const uint4*)rowp;
@@ -498,8 +502,8 @@ __global__ __launch_bounds__(256) void gemm_q4k_skinny_dma_kernel(const SkDmaArg
     for (int m = 0; m < MT; m++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        accD[m][i] = __fadd_rn(accD[m][i], __fmul_rn(__fmul_rn(dw, dy[m][i]), (float)T[m][i]));
-        accM[m][i] = __fadd_rn(accM[m][i], __fmul_rn(__fmul_rn(dmin, dy[m][i]), (float)Tm[m][i]));
+        accD[m][i] = accD[m][i] + (dw * dy[m][i]) * (float)T[m][i];
+        accM[m][i] = accM[m][i] + (dmin * dy[m][i]) * (float)Tm[m][i];
       }
   };
 

@@ -175,6 +175,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
   for (int g = 0; g < 4; g++) gmask[g] = kq == g ? 0xFFFFFFFFu : 0u;
 
   auto compute = [&](const Q6Act<MT>& act, int sb) {
+    // each f32 operation rounded on its own (no contraction into fma)
+#pragma clang fp contract(off)
 #pragma unroll
     for (int b = 0; b < NB; b++) {
       const uint8_t* rowp = buf + (16 * b + r16) * kQ6Row;
@@ -212,12 +214,12 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
           for (int m = 0; m < MT; m++) T[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(act.a[m][c], w8, T[m], 0, 0, 0);
         }
         // |T| <= 256 * 127 * 127 < 2^24: exact in f32
-        const float dq = __fmul_rn(dw, kQ6One);
+        const float dq = dw * kQ6One;
 #pragma unroll
         for (int m = 0; m < MT; m++)
 #pragma unroll
           for (int i = 0; i < 4; i++)
-            acc[b][m][i] = __fadd_rn(acc[b][m][i], __fmul_rn(__fmul_rn(dq, act.dy[m][i]), (float)T[m][i]));
+            acc[b][m][i] = acc[b][m][i] + (dq * act.dy[m][i]) * (float)T[m][i];
         continue;
       }
       i4v tot[MT], S[MT];
@@ -257,7 +259,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const int t = tot[m][i] - 32 * S[m][i];
-          acc[b][m][i] = __fadd_rn(acc[b][m][i], __fmul_rn(__fmul_rn(dw, act.dy[m][i]), (float)t));
+          acc[b][m][i] = acc[b][m][i] + (dw * act.dy[m][i]) * (float)t;
         }
     }
   };

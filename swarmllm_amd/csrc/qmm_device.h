@@ -325,10 +325,12 @@ __device__ __forceinline__ int32_t dot4(int32_t a, int32_t b, int32_t c) {
 // and code bytes qa, qb (qs[32j .. 32j+31]), against the activation's 64
 // codes y (values 64j .. 64j+63 of the block), its d (dy) and the code sums
 // of the two sub-blocks (p0, p1). Adds dy*(d*sum_sc - dmin*sum_m) to acc with
-// every f32 operation rounded explicitly, so each decode kernel that calls it
-// gets the same bits for a unit.
+// every f32 operation rounded explicitly (the products and the difference on
+// their own, the last step one fma), so each decode kernel that calls it gets
+// the same bits for a unit.
 __device__ __forceinline__ float q4k_unit(uint4 h, uint4 qa, uint4 qb, const int y[16], float dy, int32_t p0,
                                           int32_t p1, int j, float acc) {
+#pragma clang fp contract(off)
   const int sh = 16 * (j & 1);
   const uint32_t u0 = h.y, u1 = h.z, u2 = h.w;
   const uint32_t scw = j < 2 ? (u0 & 0x3f3f3f3fu) : ((u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4));
@@ -345,9 +347,9 @@ __device__ __forceinline__ float q4k_unit(uint4 h, uint4 qa, uint4 qb, const int
     shi = dot4((int)((w[q] >> 4) & 0x0F0F0F0Fu), y[8 + q], shi);
   }
   // |slo|, |shi| <= 16*15*127 and |p| <= 32*127: 24-bit products are exact
-  const float main = __fmul_rn(dx, (float)(__mul24(sc0, slo) + __mul24(sc1, shi)));
-  const float mins = __fmul_rn(mx, (float)(__mul24(m0, p0) + __mul24(m1, p1)));
-  return __fmaf_rn(dy, __fsub_rn(main, mins), acc);
+  const float main = dx * (float)(__mul24(sc0, slo) + __mul24(sc1, shi));
+  const float mins = mx * (float)(__mul24(m0, p0) + __mul24(m1, p1));
+  return __builtin_fmaf(dy, main - mins, acc);
 }
 
 // One 64-value unit of a Q6_K x Q8_K product (k_quants.rs:2598-2655): half
