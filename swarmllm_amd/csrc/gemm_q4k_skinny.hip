@@ -225,48 +225,60 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q4k_skinny_kernel(MvTargets 
     }
   };
 
-  // the loop, unrolled by two so the register buffers keep their registers:
-  // stage super-block sb, reload its registers with sb + 2, load the
-  // activation of sb + 1, compute sb. The main loop runs while both of its
-  // steps have all their loads, which it then issues unconditionally (a load
-  // issued on one path and not another makes the compiler wait for every
-  // load in flight); the last steps follow it, loading only what remains.
+  // The loop, unrolled by two so the register buffers keep their registers.
+  // A step stages super-block sb, issues the weight loads of sb + 2,
+  // computes sb and then reloads the activation registers it just used with
+  // sb + 2. A wave's loads complete in issue order, so a wait for an
+  // activation load also waits for every weight load issued before it:
+  // loading the activation of sb + 1 before computing sb (as one might)
+  // would make compute(sb + 1) wait for the weights of sb + 2 as well, and
+  // only one step of weights would stay in flight. Issued this way, both the
+  // next step's and the one after's weights are in flight while a
+  // super-block is computed (C5's few-row products take the same time either
+  // way: their bound is not the depth of the loads). The main loop runs while
+  // both of its steps have all their loads, which it then issues
+  // unconditionally (a load issued on one path and not another makes the
+  // compiler wait for every load in flight); the last steps follow it,
+  // loading only what remains.
   Pieces pa, pb;
   SkAct<MT> aa, ab;
   if (sb0 < sb1) {
     load_w(pa, sb0);
-    if (sb0 + 1 < sb1) load_w(pb, sb0 + 1);
     load_a(aa, sb0);
+    if (sb0 + 1 < sb1) {
+      load_w(pb, sb0 + 1);
+      load_a(ab, sb0 + 1);
+    }
   }
   // The matrix work runs at a raised wave priority: while the other wave of
   // a SIMD stages and issues loads, this one's MFMAs and operand work go
   // first (C5 at 8 rows: 7.27-7.31 -> 7.18 ms a forward).
-  auto step_full = [&](Pieces& pc, SkAct<MT>& cur, SkAct<MT>& nxt, int sb) {
+  auto step_full = [&](Pieces& pc, SkAct<MT>& cur, int sb) {
     wave_lds_sync();  // the previous super-block's reads are done
     stage_w(pc);
     load_w(pc, sb + 2);
-    load_a(nxt, sb + 1);
     wave_lds_sync();
     __builtin_amdgcn_s_setprio(1);
     compute(cur);
     __builtin_amdgcn_s_setprio(0);
+    load_a(cur, sb + 2);
   };
-  auto step_tail = [&](Pieces& pc, SkAct<MT>& cur, SkAct<MT>& nxt, int sb) {
+  auto step_tail = [&](Pieces& pc, SkAct<MT>& cur, int sb) {
     wave_lds_sync();
     stage_w(pc);
     if (sb + 2 < sb1) load_w(pc, sb + 2);
-    if (sb + 1 < sb1) load_a(nxt, sb + 1);
     wave_lds_sync();
     compute(cur);
+    if (sb + 2 < sb1) load_a(cur, sb + 2);
   };
   int sb = sb0;
   for (; sb + 3 < sb1; sb += 2) {
-    step_full(pa, aa, ab, sb);
-    step_full(pb, ab, aa, sb + 1);
+    step_full(pa, aa, sb);
+    step_full(pb, ab, sb + 1);
   }
-  if (sb < sb1) step_tail(pa, aa, ab, sb);
-  if (sb + 1 < sb1) step_tail(pb, ab, aa, sb + 1);
-  if (sb + 2 < sb1) step_tail(pa, aa, ab, sb + 2);
+  if (sb < sb1) step_tail(pa, aa, sb);
+  if (sb + 1 < sb1) step_tail(pb, ab, sb + 1);
+  if (sb + 2 < sb1) step_tail(pa, aa, sb + 2);
 
   // the waves' partial sums of the tiles, added in wave order
   wave_lds_sync();

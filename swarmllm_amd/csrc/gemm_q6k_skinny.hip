@@ -264,44 +264,52 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_q6k_skinny_kernel(MvTargets 
     }
   };
 
+  // A step stages super-block sb, issues the weight loads of sb + 2,
+  // computes sb and then reloads the activation registers it just used with
+  // sb + 2: a wave's loads complete in issue order, so an activation load
+  // issued ahead of the compute would make the next compute wait for the
+  // weights issued before it (see gemm_q4k_skinny.hip). The main loop runs
+  // while both of its steps have all their loads, which it then issues
+  // unconditionally (a load issued on one path and not another makes the
+  // compiler wait for every load in flight); the last steps follow it,
+  // loading only what remains.
   Pieces pa, pb;
   Q6Act<MT> aa, ab;
   if (sb0 < sb1) {
     load_w(pa, sb0);
-    if (sb0 + 1 < sb1) load_w(pb, sb0 + 1);
     load_a(aa, sb0);
+    if (sb0 + 1 < sb1) {
+      load_w(pb, sb0 + 1);
+      load_a(ab, sb0 + 1);
+    }
   }
-  // The main loop runs while both of its steps have all their loads, which
-  // it then issues unconditionally (a load issued on one path and not
-  // another makes the compiler wait for every load in flight); the last
-  // steps follow it, loading only what remains.
   // the matrix work at a raised wave priority, as in gemm_q4k_skinny.hip
-  auto step_full = [&](Pieces& pc, Q6Act<MT>& cur, Q6Act<MT>& nxt, int sb) {
+  auto step_full = [&](Pieces& pc, Q6Act<MT>& cur, int sb) {
     wave_lds_sync();
     stage_w(pc);
     load_w(pc, sb + 2);
-    load_a(nxt, sb + 1);
     wave_lds_sync();
     __builtin_amdgcn_s_setprio(1);
     compute(cur, sb);
     __builtin_amdgcn_s_setprio(0);
+    load_a(cur, sb + 2);
   };
-  auto step_tail = [&](Pieces& pc, Q6Act<MT>& cur, Q6Act<MT>& nxt, int sb) {
+  auto step_tail = [&](Pieces& pc, Q6Act<MT>& cur, int sb) {
     wave_lds_sync();
     stage_w(pc);
     if (sb + 2 < sb1) load_w(pc, sb + 2);
-    if (sb + 1 < sb1) load_a(nxt, sb + 1);
     wave_lds_sync();
     compute(cur, sb);
+    if (sb + 2 < sb1) load_a(cur, sb + 2);
   };
   int sb = sb0;
   for (; sb + 3 < sb1; sb += 2) {
-    step_full(pa, aa, ab, sb);
-    step_full(pb, ab, aa, sb + 1);
+    step_full(pa, aa, sb);
+    step_full(pb, ab, sb + 1);
   }
-  if (sb < sb1) step_tail(pa, aa, ab, sb);
-  if (sb + 1 < sb1) step_tail(pb, ab, aa, sb + 1);
-  if (sb + 2 < sb1) step_tail(pa, aa, ab, sb + 2);
+  if (sb < sb1) step_tail(pa, aa, sb);
+  if (sb + 1 < sb1) step_tail(pb, ab, sb + 1);
+  if (sb + 2 < sb1) step_tail(pa, aa, sb + 2);
 
   wave_lds_sync();
   float* part = (float*)buf;
