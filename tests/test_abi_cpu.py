@@ -68,6 +68,9 @@ def test_forward_plans_without_a_device_and_rejects_bad_shapes():
     assert L.qmm_forward(12, None, None, 256, None, 8, None, 0, None, 256, 8, 1, 0, 0) == _lib.QMM_UNSUPPORTED
     assert L.qmm_forward(12, None, None, 256, None, 4, None, 0, ctypes.byref(need), 256, 8, 1, 0, 0) == _lib.QMM_UNSUPPORTED
     assert L.qmm_forward(12, None, None, 128, None, 8, None, 0, ctypes.byref(need), 256, 8, 1, 0, 0) == _lib.QMM_UNSUPPORTED
+    # no activation rows, no weight rows (the host API returns an empty output before calling)
+    assert L.qmm_forward(12, None, None, 256, None, 8, None, 0, ctypes.byref(need), 256, 8, 0, 0, 0) == _lib.QMM_UNSUPPORTED
+    assert L.qmm_forward(12, None, None, 256, None, 8, None, 0, ctypes.byref(need), 256, 0, 1, 0, 0) == _lib.QMM_UNSUPPORTED
     # a launch with too small a workspace is refused before anything is enqueued
     assert L.qmm_forward(12, None, None, 256, None, 8, None, 0, ctypes.byref(need), 256, 8, 1, 1, 0) == \
         _lib.QMM_WORKSPACE_TOO_SMALL
