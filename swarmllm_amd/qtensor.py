@@ -311,14 +311,26 @@ class QTensor:
 
 @dataclass
 class Workspace:
-    """A caller-owned device buffer the products quantize their activation into."""
+    """The device buffers the products of one weight quantize their activation
+    into: one buffer per (device, stream), kept and grown as needed. Products
+    on one stream run in order, so they can share a buffer; products of the
+    same weight on two streams may run at once and get a buffer each, and a
+    buffer outgrown on a stream is released on that stream, after the work
+    already queued there (the reference allocates its temporaries per call)."""
 
-    buf: torch.Tensor = None
+    def __init__(self) -> None:
+        self._bufs = {}
 
     def get(self, nbytes: int, device) -> torch.Tensor:
-        if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-        return self.buf
+        device = torch.device(device)
+        stream = torch.cuda.current_stream(device)
+        key = (device.index, stream.cuda_stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            with torch.cuda.stream(stream):
+                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
 
 
 # The reference's switches for arms this build does not have, accepted and
