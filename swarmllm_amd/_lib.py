@@ -2,7 +2,9 @@
 
 The library is built in-tree (``swarmllm_amd/libqmm.so``) by
 ``swarmllm_amd.build.build_library()``. Loading fails loudly when it is
-missing: there is no fallback path.
+missing: there is no fallback path. SWARMLLM_QMM_LIB names another build of
+the same library to load instead (the host-AddressSanitizer build of
+``make asan`` in csrc/).
 """
 from __future__ import annotations
 
@@ -10,7 +12,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libqmm.so")
+LIB_PATH = os.environ.get("SWARMLLM_QMM_LIB") or os.path.join(HERE, "libqmm.so")
 
 QMM_OK, QMM_UNSUPPORTED, QMM_WORKSPACE_TOO_SMALL, QMM_DEVICE_ERROR, QMM_NO_TILE, QMM_NO_ROOM = range(6)
 STATUS_NAMES = {0: "OK", 1: "UNSUPPORTED", 2: "WORKSPACE_TOO_SMALL", 3: "DEVICE_ERROR", 4: "NO_TILE", 5: "NO_ROOM"}
