@@ -492,10 +492,11 @@ size_t qmm_act_bytes(int layout, int64_t k, int64_t rows) {
 
 int qmm_act_planes(int layout, int64_t k, int64_t rows, size_t* codes_off, size_t* scales_off, size_t* sums_off) {
   if (qmm_act_bytes(layout, k, rows) == 0) return QMM_UNSUPPORTED;
-  const qmm::ActPlanes p = qmm::act_planes(layout, nullptr, k, rows);
-  if (codes_off) *codes_off = (size_t)(uintptr_t)p.codes;
-  if (scales_off) *scales_off = (size_t)(uintptr_t)p.d;
-  if (sums_off) *sums_off = (size_t)(uintptr_t)p.sums;
+  size_t so = 0, uo = 0;
+  qmm::act_plane_offsets(layout, k, rows, &so, &uo);
+  if (codes_off) *codes_off = 0;
+  if (scales_off) *scales_off = so;
+  if (sums_off) *sums_off = uo;
   return QMM_OK;
 }
 

@@ -38,6 +38,8 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // Byte size of an activation of `rows` x `k` in `layout`, and its planes.
 size_t act_bytes(int layout, int64_t k, int64_t rows);
 ActPlanes act_planes(int layout, void* base, int64_t k, int64_t rows);
+// The byte offsets of the scales and sums planes (the codes start at 0).
+void act_plane_offsets(int layout, int64_t k, int64_t rows, size_t* scales_off, size_t* sums_off);
 
 // ---- launchers (return hipSuccess or the launch error) ---------------------
 hipError_t launch_act_quantize(int layout, const float* x, int64_t stride, int64_t k, int64_t rows,

@@ -34,18 +34,20 @@ size_t act_bytes(int layout, int64_t k, int64_t rows) {
   return codes + d + sums;
 }
 
+void act_plane_offsets(int layout, int64_t k, int64_t rows, size_t* scales_off, size_t* sums_off) {
+  const size_t codes = align_up((size_t)(rows * k), 256);
+  *scales_off = codes;
+  *sums_off = codes + align_up((size_t)(rows * (k / (layout == ACT_Q8K ? 256 : 32))) * 4, 256);
+}
+
 ActPlanes act_planes(int layout, void* base, int64_t k, int64_t rows) {
-  ActPlanes p;
+  size_t so = 0, uo = 0;
+  act_plane_offsets(layout, k, rows, &so, &uo);
   char* b = (char*)base;
+  ActPlanes p;
   p.codes = (int8_t*)b;
-  b += align_up((size_t)(rows * k), 256);
-  p.d = (float*)b;
-  if (layout == ACT_Q8K) {
-    b += align_up((size_t)(rows * (k / 256)) * 4, 256);
-  } else {
-    b += align_up((size_t)(rows * (k / 32)) * 4, 256);
-  }
-  p.sums = (void*)b;
+  p.d = (float*)(b + so);
+  p.sums = (void*)(b + uo);
   return p;
 }
 
