@@ -360,6 +360,214 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
   }
 }
 
+// The packed form, for rows of an even number of blocks from 64 to 126
+// (C4's 2880-value rows are 90 blocks: 45 units of two, so the streaming form
+// leaves 19 of 64 lanes without a unit). A wave's rows are contiguous bytes
+// and, with an even block count, a sequence of equal two-block units: step j
+// gives lane L unit 64 j + L of that sequence, in whichever row it falls, so
+// every lane holds one. A unit's value, b32_unit(..., 0), is the partial that
+// lane (unit mod units-a-row) holds in the streaming form (such a row is one
+// span, so that lane's partial is its one unit, and the lanes past the row's
+// units hold 0). When a row's last unit has been computed, lane v of the wave
+// fetches the value of the row's unit v (ds_bpermute, from this step's lanes
+// or the previous step's) and the wave sums them with wave_sum_dpp: the same
+// 64 partials in the same lanes, so each entry's result has the streaming
+// form's bits, and the decode kernel's.
+constexpr int kMoeRec = 80;  // LDS bytes of one activation unit in the packed form
+
+template <int FMT>
+__global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu(4))) void moe_b32f_kernel(
+    const uint8_t* __restrict__ W, int64_t n, int nb, int64_t estride, int num_experts,
+    const int8_t* __restrict__ yq, const float* __restrict__ yd, const int32_t* __restrict__ runs,
+    const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int topk, int size_m,
+    float* __restrict__ dst, int64_t ldd, int rpw) {
+  using F = Fmt32<FMT>;
+  using Span = MoeSpan<FMT>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int k = nb * 32;
+  const int upr = nb >> 1;      // units a row, 32..63
+  constexpr int kUB = 2 * F::B;  // bytes a unit
+  // the chunk's activation rows: per entry and unit one 80-byte record, the
+  // unit's 64 codes then its two block scales (80 bytes apart, the 16 lanes
+  // of one LDS read phase fall on distinct banks; 64 apart they met 4 ways)
+  uint8_t* const arec = smem;  // [kMoePairs][upr][80]
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t* const buf = smem + (size_t)kMoePairs * upr * kMoeRec + (size_t)wv * Span::kStage;
+
+  const int64_t rb = (int64_t)nb * F::B;
+  const int64_t r0 = ((int64_t)blockIdx.x * kMoeSWaves + wv) * rpw;
+  const int nrows = r0 < n ? (int)(n - r0 < rpw ? n - r0 : rpw) : 0;
+  const int U = nrows * upr;  // the wave's units
+  const int nsteps = (U + 63) >> 6;
+  const Lut32<FMT> lut;
+  const uint32_t t0 = lut.t0, t1 = lut.t1, t2 = lut.t2, t3 = lut.t3;
+
+  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  for (int run = blockIdx.y; run < nruns; run += gridDim.y) {
+    const int start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
+    const int len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
+    const int e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+    if (e < 0 || e >= num_experts) continue;
+    const uint8_t* Wr = W + (int64_t)e * estride + r0 * rb;  // the wave's first row
+
+    for (int c0 = 0; c0 < len; c0 += kMoePairs) {
+      const int cnt = len - c0 < kMoePairs ? len - c0 : kMoePairs;
+      // Step ls's bytes: units 64 ls .. of the wave's sequence; past the last
+      // step the loads read the first bytes of the quantized activation
+      // (cached, never used), so every step issues the same loads.
+      int ls = 0;
+      auto load_next = [&](Span& sp) {
+        const int u0 = 64 * ls;
+        const bool real = u0 < U;
+        const int units = real ? (U - u0 < 64 ? U - u0 : 64) : 1;
+        const uint8_t* pp = real ? Wr + (int64_t)u0 * kUB : (const uint8_t*)yq;
+        sp.off = (int)((uintptr_t)pp & 15);
+        sp.len = units;
+        const uint8_t* a0 = pp - sp.off;
+        const int pieces = (sp.off + units * kUB + 15) >> 4;
+  #pragma unroll
+        for (int c = 0; c < Span::kLoads; c++) {
+          const int pc = lane + 64 * c;
+          sp.p[c] = ld_stream16(a0 + 16u * (uint32_t)(pc < pieces ? pc : pieces - 1));
+        }
+        ls++;
+      };
+      Span ring[kMoeRing];
+  #pragma unroll
+      for (int j = 0; j < kMoeRing; j++) load_next(ring[j]);
+
+      int pr[kMoePairs];
+  #pragma unroll
+      for (int p = 0; p < kMoePairs; p++)
+        pr[p] = __builtin_amdgcn_readfirstlane(ids[start + c0 + (p < cnt ? p : cnt - 1)]);
+      int64_t out_row[kMoePairs];
+      float scale[kMoePairs];
+      bool use[kMoePairs];
+      int64_t in_row[kMoePairs];
+  #pragma unroll
+      for (int p = 0; p < kMoePairs; p++) {
+        use[p] = p < cnt && pr[p] >= 0 && pr[p] < size_m;
+        out_row[p] = use[p] ? pr[p] : 0;
+        in_row[p] = use[p] ? (topk_w ? pr[p] : pr[p] / topk) : 0;
+      }
+  #pragma unroll
+      for (int p = 0; p < kMoePairs; p++) scale[p] = topk_w ? topk_w[use[p] ? pr[p] : 0] : 1.0f;
+      // the chunk's activation rows into LDS, as the streaming form copies them
+      __syncthreads();
+      const int cp = wv;
+      const bool cuse = use[cp];
+      const int8_t* crow = yq + (cuse ? in_row[cp] * k : 0);
+      const float* cdrow = yd + (cuse ? in_row[cp] * nb : 0);
+      const int npc = k / 16;
+      auto ld_piece = [&](int j) {
+        const int i = lane + 64 * j;
+        return *(const uint4*)(crow + 16 * (i < npc ? i : npc - 1));
+      };
+      auto ld_scale = [&](int j) {
+        const int i = lane + 64 * j;
+        return cdrow[i < nb ? i : nb - 1];
+      };
+      const uint4 cv0 = ld_piece(0), cv1 = ld_piece(1), cv2 = ld_piece(2), cv3 = ld_piece(3);
+      const float cd0 = ld_scale(0), cd1 = ld_scale(1);
+      if (cuse) {
+        uint8_t* const mine = arec + (size_t)cp * upr * kMoeRec;
+        auto st_piece = [&](int j, const uint4& v) {
+          const int i = lane + 64 * j;  // piece i & 3 of unit i >> 2
+          if (i < npc) *(uint4*)(mine + kMoeRec * (i >> 2) + 16 * (i & 3)) = v;
+        };
+        auto st_scale = [&](int j, float v) {
+          const int i = lane + 64 * j;  // block i: scale i & 1 of unit i >> 1
+          if (i < nb) *(float*)(mine + kMoeRec * (i >> 1) + 64 + 4 * (i & 1)) = v;
+        };
+        st_piece(0, cv0);
+        st_piece(1, cv1);
+        st_piece(2, cv2);
+        st_piece(3, cv3);
+        st_scale(0, cd0);
+        st_scale(1, cd1);
+      }
+      __syncthreads();
+
+      // lane L's unit within its row (64 j + L mod upr, kept step to step)
+      int vl = lane < upr ? lane : lane - upr;
+      int rr = 0;  // the first row not yet summed
+      float prev[kMoePairs];
+  #pragma unroll
+      for (int p = 0; p < kMoePairs; p++) prev[p] = 0.0f;
+      auto step = [&](Span& cur, int j) {
+        __builtin_amdgcn_s_setprio(1);
+        wave_lds_sync();
+  #pragma unroll
+        for (int c = 0; c < Span::kLoads; c++) {
+          const int pc = lane + 64 * c;
+          *(uint4*)(buf + 16 * (pc < Span::kPieces ? pc : Span::kPieces - 1)) = cur.p[c];
+        }
+        wave_lds_sync();
+        const int off = cur.off, units = cur.len;
+        load_next(cur);
+        __builtin_amdgcn_s_setprio(0);
+        if (j >= nsteps) return;
+        float val[kMoePairs];
+  #pragma unroll
+        for (int p = 0; p < kMoePairs; p++) val[p] = 0.0f;
+        if (lane < units) {
+          uint32_t q0[8], q1[8];
+          float dx0, dx1;
+          F::decode(buf, off + lane * kUB, q0, dx0, t0, t1, t2, t3);
+          F::decode(buf, off + lane * kUB + F::B, q1, dx1, t0, t1, t2, t3);
+  #pragma unroll
+          for (int p = 0; p < kMoePairs; p++) {
+            if (p >= cnt) break;  // the chunk's entries come first
+            if (!use[p]) continue;
+            Act64 a;
+            const uint8_t* rec = arec + ((size_t)p * upr + vl) * kMoeRec;
+            const int4* yp = (const int4*)rec;
+            const int4 a0 = yp[0], a1 = yp[1], b0 = yp[2], b1 = yp[3];
+            const float2 dd = *(const float2*)(rec + 64);
+            a.y[0][0] = a0.x; a.y[0][1] = a0.y; a.y[0][2] = a0.z; a.y[0][3] = a0.w;
+            a.y[0][4] = a1.x; a.y[0][5] = a1.y; a.y[0][6] = a1.z; a.y[0][7] = a1.w;
+            a.y[1][0] = b0.x; a.y[1][1] = b0.y; a.y[1][2] = b0.z; a.y[1][3] = b0.w;
+            a.y[1][4] = b1.x; a.y[1][5] = b1.y; a.y[1][6] = b1.z; a.y[1][7] = b1.w;
+            a.dy[0] = dd.x;
+            a.dy[1] = dd.y;
+            val[p] = b32_unit(q0, q1, dx0, dx1, a, 0.0f);
+          }
+        }
+        // the rows whose last unit is in this step (at most two: upr >= 32);
+        // row r's unit v sits in lane r upr - 64 j + v of this step, or, where
+        // that is negative, 64 lanes on in the previous step
+        const int u0 = 64 * j;
+        for (; rr < nrows && (rr + 1) * upr <= u0 + 64; rr++) {
+          const int base = rr * upr - u0;  // > -64
+          const int s = base + lane;
+          const bool mine = lane < upr;
+  #pragma unroll
+          for (int p = 0; p < kMoePairs; p++) {
+            if (p >= cnt) break;  // the chunk's entries come first
+            if (!use[p]) continue;
+            const float fc = __int_as_float(__builtin_amdgcn_ds_bpermute((s & 63) << 2, __float_as_int(val[p])));
+            float v = fc;
+            if (base < 0) {
+              const float fp = __int_as_float(__builtin_amdgcn_ds_bpermute(((s + 64) & 63) << 2, __float_as_int(prev[p])));
+              v = s < 0 ? fp : fc;
+            }
+            v = wave_sum_dpp(mine ? v : 0.0f);
+            if (lane == 0) dst[out_row[p] * ldd + r0 + rr] = __fmul_rn(v, scale[p]);
+          }
+        }
+  #pragma unroll
+        for (int p = 0; p < kMoePairs; p++) prev[p] = val[p];
+        vl += 64 - upr;
+        if (vl >= upr) vl -= upr;
+      };
+      for (int j = 0; j < nsteps; j += kMoeRing) {
+  #pragma unroll
+        for (int jj = 0; jj < kMoeRing; jj++) step(ring[jj], j + jj);
+      }
+    }
+  }
+}
+
 template <int FMT>
 hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                         const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
@@ -381,6 +589,34 @@ hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, co
   kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
                                           topk_w, topk, (int)size_m, dst, ldd, (int)rpw);
   return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch_moe_f(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
+                        const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
+                        float* dst, int64_t ldd, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  const int nb = (int)(k / 32);
+  const int64_t estride = n * nb * Fmt32<FMT>::B;
+  const int64_t gy = size_m < num_experts ? size_m : num_experts;
+  // rows a wave: 16 (C4: 720 units, 12 steps of 64, no step partly empty
+  // but the last; 8 rows measured 1% slower, 10 and 12 rows, whose last
+  // steps hold few units, 10-15% slower)
+  const int64_t rpw = 16;
+  const int64_t rows_per_wg = (int64_t)kMoeSWaves * rpw;
+  const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
+  const size_t lds = (size_t)kMoePairs * (nb / 2) * kMoeRec + (size_t)kMoeSWaves * MoeSpan<FMT>::kStage;
+  constexpr auto* kfn = &moe_b32f_kernel<FMT>;
+  if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
+  kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
+                                          topk_w, topk, (int)size_m, dst, ldd, (int)rpw);
+  return hipGetLastError();
+}
+
+// Rows the packed form takes: an even number of blocks, 64 to 126.
+inline bool moe_packed_takes(int64_t k) {
+  const int64_t nb = k / 32;
+  return nb % 2 == 0 && nb >= 64 && nb <= 126;
 }
 
 // The streaming form's LDS: the chunk's activation rows and the waves' stage buffers.
@@ -419,6 +655,14 @@ size_t moe_runs_bytes(int64_t size_m) { return (size_t)(1 + 3 * size_m) * sizeof
 hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                       const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                       float* dst, int64_t ldd, int cus, hipStream_t st) {
+  if (moe_stream_fits(k) && moe_packed_takes(k)) {
+    switch (type) {
+      case T_Q8_0: return launch_moe_f<T_Q8_0>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, st);
+      case T_IQ4_NL: return launch_moe_f<T_IQ4_NL>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, st);
+      case T_MXFP4: return launch_moe_f<T_MXFP4>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (moe_stream_fits(k)) {
     switch (type) {
       case T_Q8_0: return launch_moe_s<T_Q8_0>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);

@@ -107,8 +107,10 @@ def test_moe_c4_gpt_oss_shapes():
     before = lib().qmm_moe_launches()
     gate_up = expert_stack(qtype, E, 5760, 2880, 41)
     x = np.random.default_rng(40).standard_normal((tokens, 2880)).astype(np.float32)
-    y1 = moe_forward(t32(x), gate_up, t32(sorted_ids), t32(expert_ids), None, topk).cpu().numpy()
+    xs = t32(x)
+    y1 = moe_forward(xs, gate_up, t32(sorted_ids), t32(expert_ids), None, topk).cpu().numpy()
     check_against_oracle(qtype, gate_up, x, y1, sorted_ids, expert_ids, None, topk)
+    check_against_forward(gate_up, xs, y1, sorted_ids, expert_ids, None, topk)
     del gate_up
     down = expert_stack(qtype, E, 2880, 2880, 42)
     x2 = np.random.default_rng(43).standard_normal((tokens * topk, 2880)).astype(np.float32)
@@ -117,6 +119,30 @@ def test_moe_c4_gpt_oss_shapes():
     check_against_oracle(qtype, down, x2, y2, sorted_ids, expert_ids, topk_w, topk)
     check_against_forward(down, xs2, y2, sorted_ids, expert_ids, topk_w, topk)
     assert lib().qmm_moe_launches() >= before + 2
+
+
+@pytest.mark.parametrize("name", ["MXFP4", "Q8_0", "IQ4_NL"])
+@pytest.mark.parametrize("k", [2048, 2880, 4032])
+def test_moe_packed_lane_rows(name, k):
+    """Rows of 64-126 blocks, an even number, take the packed form (each lane
+    a two-block unit of the wave's contiguous rows, whichever row it falls
+    in); each entry must still equal qmm_forward of its pair bit for bit.
+    n = 203 leaves the last workgroup and the last wave partly empty, and the
+    routing gives runs of one to several entries."""
+    qtype = MOE_TYPES[name]
+    E, n, tokens, topk = 5, 203, 7, 3
+    seed = zlib.crc32(f"packed-{name}-{k}".encode())
+    sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, seed)
+    stack = expert_stack(qtype, E, n, k, seed & 0xFFFF)
+    for weighted in (False, True):
+        rows = tokens * topk if weighted else tokens
+        x = np.random.default_rng(seed + weighted).standard_normal((rows, k)).astype(np.float32)
+        xs = t32(x)
+        tw = topk_w if weighted else None
+        out = moe_forward(xs, stack, t32(sorted_ids), t32(expert_ids), t32(topk_w) if weighted else None, topk)
+        out = out.cpu().numpy()
+        check_against_oracle(qtype, stack, x, out, sorted_ids, expert_ids, tw, topk)
+        check_against_forward(stack, xs, out, sorted_ids, expert_ids, tw, topk)
 
 
 def moe_into(stack, xs, x_stride, sorted_ids, expert_ids, topk_w, topk, rows_out, fill=float("nan")):
