@@ -577,6 +577,222 @@ hipError_t launch_sk_dma(const MvTargets& t, int nsb, const ActPlanes& p, int64_
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// The register-staged kernel's product for narrow weights and up to 16 rows
+// with each wave's operands copied straight to LDS: a workgroup owns one
+// 16-row tile, its 4 waves split the super-blocks of K as that kernel's do
+// and add their partial sums in wave order, and each super-block's
+// arithmetic is that kernel's, so a row's bits are the same. A wave copies
+// its own super-blocks (the tile's 16 x 144 bytes, MR activation rows and
+// their scales) into a ring of NS stages, NS - 1 in flight while it computes
+// one, without holding them in registers, so more waves fit a CU. MR (4, 8
+// or 16) activation rows are copied, M <= MR; fragment rows past them read
+// row MR - 1 and their outputs are never stored. Tiles are numbered weight
+// after weight (a ragged last tile reads its weight's last row again).
+// ---------------------------------------------------------------------------
+template <int MR, int NS>
+struct SkKs {
+  static constexpr int kWSlots = 10;                           // 16-byte slots a staged weight row (9 + 1: banks)
+  static constexpr int kWCopies = (16 * kWSlots + 63) / 64;    // 3
+  static constexpr int kASlots = 17;                           // a staged activation row (16 + 1)
+  static constexpr int kACopies = (MR * kASlots + 63) / 64;
+  static constexpr int kW = kWCopies * 1024;
+  static constexpr int kA = kACopies * 1024;
+  static constexpr int kStage = kW + kA + 256;                 // + the MR scales (one dword copy)
+  static constexpr int kCopies = kWCopies + kACopies + 1;      // copies a stage
+  static constexpr int kWave = NS * kStage;
+  static_assert(MR <= 64 && (NS - 1) * kCopies <= 63, "vmcnt");
+  static_assert(kWave >= 4 * 64 * 4, "the partial sums fit a wave's ring");
+};
+
+template <int MR, int NS>
+__global__ __launch_bounds__(256) void gemm_q4k_skinny_ks_kernel(const SkDmaArgs a, int nsb,
+                                                                 const int8_t* __restrict__ yq,
+                                                                 const float* __restrict__ yd, int M) {
+  using D = SkKs<MR, NS>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+  const bool hin = kq >= 2;
+  const int hb = 16 * (kq & 1);
+  const uint32_t K = (uint32_t)nsb * 256u;
+  const uint32_t rowbytes = (uint32_t)nsb * 144u;
+  uint8_t* const ring = smem + wv * D::kWave;
+
+  // the workgroup's tile: weight t (by selects), its first row there
+  const int tile = (int)blockIdx.x;
+  const int t = tile < a.tile_end[0] ? 0 : tile < a.tile_end[1] ? 1 : tile < a.tile_end[2] ? 2 : 3;
+  auto pick = [&](const auto& arr) { return t == 0 ? arr[0] : t == 1 ? arr[1] : t == 2 ? arr[2] : arr[3]; };
+  const int tb = t == 0 ? 0 : t == 1 ? a.tile_end[0] : t == 2 ? a.tile_end[1] : a.tile_end[2];
+  const int64_t wbeg = t == 0 ? 0 : t == 1 ? a.tg.row_end[0] : t == 2 ? a.tg.row_end[1] : a.tg.row_end[2];
+  const int64_t wrows = pick(a.tg.row_end) - wbeg;
+  const int64_t r0 = (int64_t)(tile - tb) * 16;
+  const uint8_t* __restrict__ W = (const uint8_t*)pick(a.tg.w);
+
+  // the wave's super-blocks (the register-staged kernel's split)
+  const int per = (nsb + 3) / 4;
+  const int sb0 = wv * per;
+  const int sb1 = sb0 + per < nsb ? sb0 + per : nsb;
+  const int len = sb1 > sb0 ? sb1 - sb0 : 0;
+
+  uint32_t woff[D::kWCopies];
+#pragma unroll
+  for (int u = 0; u < D::kWCopies; u++) {
+    const int sl = 64 * u + lane;
+    const int row = sl / D::kWSlots, q = sl - row * D::kWSlots;
+    int64_t gr = r0 + (row < 16 ? row : 0);
+    gr = gr < wrows ? gr : wrows - 1;
+    woff[u] = (uint32_t)gr * rowbytes + 16u * (uint32_t)(q < 9 ? q : 0);
+  }
+  uint32_t aoff[D::kACopies];
+#pragma unroll
+  for (int u = 0; u < D::kACopies; u++) {
+    const int sl = 64 * u + lane;
+    const int row = sl / D::kASlots, q = sl - row * D::kASlots;
+    const int ar = row < MR ? (row < M ? row : M - 1) : 0;
+    aoff[u] = (uint32_t)ar * K + 16u * (uint32_t)(q < 16 ? q : 0);
+  }
+  const uint32_t doff = 4u * (uint32_t)(lane < MR ? (lane < M ? lane : M - 1) : 0) * (uint32_t)nsb;
+  // stage s (super-block sb0 + s, clamped into the wave's range: past it the
+  // copies repeat its last super-block, so every step issues the same copies)
+  auto issue = [&](int s) {
+    const int sb = len == 0 ? 0 : (s < len ? sb0 + s : sb1 - 1);
+    uint8_t* const base = ring + (s % NS) * D::kStage;
+#pragma unroll
+    for (int u = 0; u < D::kWCopies; u++) dma16(W + 144 * (int64_t)sb, woff[u], lds_addr(base + 1024 * u));
+#pragma unroll
+    for (int u = 0; u < D::kACopies; u++) dma16(yq + 256 * (int64_t)sb, aoff[u], lds_addr(base + D::kW + 1024 * u));
+    dma4(yd + sb, doff, lds_addr(base + D::kW + D::kA));
+  };
+
+  float accD[4], accM[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) accD[i] = accM[i] = 0.0f;
+  const int arow = r16 < MR ? r16 : MR - 1;
+  auto compute = [&](int s) {
+    // each f32 operation rounded on its own (no contraction into fma)
+#pragma clang fp contract(off)
+    const uint8_t* const base = ring + (s % NS) * D::kStage;
+    const uint8_t* rowp = base + r16 * (16 * D::kWSlots);
+    const uint4 hdr = *(const uint4*)rowp;
+    uint4 code[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) code[c] = *(const uint4*)(rowp + 16 + 32 * c + hb);
+    i4v am[4];
+    float dy[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) am[c] = *(const i4v*)(base + D::kW + arow * (16 * D::kASlots) + 64 * c + 16 * kq);
+    const float* const db = (const float*)(base + D::kW + D::kA);
+#pragma unroll
+    for (int i = 0; i < 4; i++) dy[i] = db[4 * kq + i < MR ? 4 * kq + i : MR - 1];
+    // scales and mins (get_scale_min_k4, utils.rs:50-60)
+    const uint32_t u0 = hdr.y, u1 = hdr.z, u2 = hdr.w;
+    const uint32_t s03 = u0 & 0x3f3f3f3fu, m03 = u1 & 0x3f3f3f3fu;
+    const uint32_t s47 = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
+    const uint32_t m47 = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
+    const float dw = h2f((uint16_t)(hdr.x & 0xFFFF));
+    const float dmin = h2f((uint16_t)(hdr.x >> 16));
+    i4v T, Tm;
+    const i4v zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int sj = 2 * c + (hin ? 1 : 0);
+        const uint32_t scv = ((sj < 4 ? s03 : s47) >> (8 * (sj & 3))) & 0xFF;
+        const uint32_t f = sk_dup16(pass == 0 ? scv >> 3 : scv & 7);
+        i4v bq;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t w = sk_word(code[c], e);
+          bq[e] = (int)sk_pkmul(hin ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu, f);
+        }
+        T = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[c], bq, (pass == 0 && c == 0) ? zero : T, 0, 0, 0);
+      }
+      if (pass == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) T[i] <<= 3;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int sj = 2 * c + (hin ? 1 : 0);
+      const uint32_t mv = ((sj < 4 ? m03 : m47) >> (8 * (sj & 3))) & 0xFF;
+      const int mb = (int)(mv * 0x01010101u);
+      const i4v bm = {mb, mb, mb, mb};
+      Tm = __builtin_amdgcn_mfma_i32_16x16x64_i8(am[c], bm, c == 0 ? zero : Tm, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      accD[i] = accD[i] + (dw * dy[i]) * (float)T[i];
+      accM[i] = accM[i] + (dmin * dy[i]) * (float)Tm[i];
+    }
+  };
+
+  // The ring: stages 0 .. NS - 2 in flight before the loop; step s issues
+  // stage s + NS - 1 into the buffer stage s - 1 used (read by now), waits
+  // for stage s (the NS - 1 stages issued after it may stay in flight) and
+  // computes it.
+#pragma unroll
+  for (int s = 0; s < NS - 1; s++) issue(s);
+  for (int s = 0; s < len; s++) {
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0): stage s - 1's reads done
+    asm volatile("" ::: "memory");
+    issue(s + NS - 1);
+    wait_vm<(NS - 1) * D::kCopies>();
+    asm volatile("" ::: "memory");
+    compute(s);
+  }
+  // every copy landed before the ring holds the partial sums
+  wait_vm<0>();
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+  asm volatile("" ::: "memory");
+  float* const part = (float*)ring;
+#pragma unroll
+  for (int i = 0; i < 4; i++) part[i * 64 + lane] = __fsub_rn(accD[i], accM[i]);
+  __syncthreads();
+  if (wv == 0 && r0 + r16 < wrows) {
+    float* const out = pick(a.tg.dst) + r0 + r16;
+    const int64_t ldd = pick(a.tg.ldd);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float v = ((const float*)smem)[i * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < 4; w++) v = __fadd_rn(v, ((const float*)(smem + w * D::kWave))[i * 64 + lane]);
+      const int ar = 4 * kq + i;
+      if (ar < M) out[(int64_t)ar * ldd] = v;
+    }
+  }
+}
+
+template <int MR, int NS>
+hipError_t launch_sk_ks(const MvTargets& t, int nsb, const ActPlanes& p, int64_t rows, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  using D = SkKs<MR, NS>;
+  SkDmaArgs a{};
+  a.tg = t;
+  int tiles = 0;
+  for (int i = 0; i < kMaxTargets; i++) {
+    if (i < t.count) {
+      const int64_t n = t.row_end[i] - (i ? t.row_end[i - 1] : 0);
+      tiles += (int)((n + 15) / 16);
+    }
+    a.tile_end[i] = tiles;
+  }
+  for (int i = t.count; i < kMaxTargets; i++) {
+    a.tg.w[i] = t.w[t.count - 1];
+    a.tg.dst[i] = t.dst[t.count - 1];
+    a.tg.ldd[i] = t.ldd[t.count - 1];
+    a.tg.row_end[i] = t.row_end[t.count - 1];
+  }
+  const size_t lds = 4 * (size_t)D::kWave;
+  constexpr auto* kfn = &gemm_q4k_skinny_ks_kernel<MR, NS>;
+  if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
+  kfn<<<dim3((unsigned)tiles), 256, lds, st>>>(a, nsb, p.codes, p.d, (int)rows);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 int gemm_q4k_skinny_max_rows() { return 32; }
@@ -592,6 +808,18 @@ static hipError_t launch_gemm_q4k_skinny_reg(const MvTargets& t, int nsb, const 
   // two 16-row tiles a workgroup where the rows fill the CUs twice over
   const int64_t n_total = t.row_end[t.count - 1];
   const bool wide = n_total >= (int64_t)cus * 32 * 2;
+  // narrow weights of up to 16 rows: the same product with copies to LDS
+  // (weights under 4 GiB: its lanes form weight offsets in 32 bits)
+  bool small = !wide && rows <= 16;
+  for (int i = 0; i < t.count && small; i++)
+    small = (t.row_end[i] - (i ? t.row_end[i - 1] : 0)) * nsb * 144 < ((int64_t)1 << 32);
+  // (two stages a wave: three workgroups a CU at 8 rows; C5 at 8 / 16 rows
+  // 6.51 / 7.20 -> 6.39 / 7.02 ms a forward, three stages 6.43 / 7.21)
+  if (small) {
+    if (rows <= 4) return launch_sk_ks<4, 2>(t, nsb, p, rows, st);
+    if (rows <= 8) return launch_sk_ks<8, 2>(t, nsb, p, rows, st);
+    return launch_sk_ks<16, 2>(t, nsb, p, rows, st);
+  }
   if (rows <= 16) return wide ? launch_sk<1, 2, 4>(t, nsb, p, rows, st) : launch_sk<1, 1, 4>(t, nsb, p, rows, st);
   return wide ? launch_sk<2, 2, 4>(t, nsb, p, rows, st) : launch_sk<2, 1, 4>(t, nsb, p, rows, st);
 }

@@ -333,6 +333,34 @@ def test_q4k_skinny_c5_gate_projection(rows):
     assert normalised_error(y, want, wdeq, x) <= TIGHT
 
 
+@pytest.mark.parametrize("rows", [4, 8, 13, 16])
+def test_q4k_skinny_narrow_c5_products(rows):
+    """BASELINE C5's narrow Q4_K products (q 8192 x 8192, k and v 1024 x 8192
+    through one shared launch, o 8192 x 8192) at the few-row widths: the
+    narrow-weight kernel that copies each wave's operands to LDS, against the
+    oracle, and shared equal to each weight's own forward."""
+    from swarmllm_amd import fill_normal
+
+    k = 8192
+    mats, wqs = [], []
+    for n in (8192, 1024, 1024):
+        qt = QTensor.quantize(fill_normal(n * k, seed=600 + n, std=0.02).reshape(n, k), GgmlDType.Q4K)
+        mats.append(QMatMul(qt))
+        wqs.append(qt.data_.cpu().numpy())
+    rng = np.random.default_rng(610 + rows)
+    x = activations(rng, rows, k, outliers=True)
+    xs = upload(x)
+    shared = QMatMul.forward_shared(xs, mats)
+    assert "launch_sk_ks" in lib().qmm_last_kernel().decode()
+    for m, wq, y in zip(mats, wqs, shared):
+        n = y.shape[-1]
+        assert torch.equal(y, m.forward(xs))
+        assert "launch_sk_ks" in lib().qmm_last_kernel().decode()
+        want = qref.matmul(qref.Q4_K, x, wq, n)
+        wdeq = qref.to_float(qref.Q4_K, wq, n * k).reshape(n, k)
+        assert normalised_error(y.cpu().numpy(), want, wdeq, x) <= TIGHT
+
+
 @pytest.mark.parametrize("rows", [4, 13])
 def test_q4k_skinny_copy_staged_ragged_weight(rows):
     """A wide weight (at least 64 rows a CU: the copy-staged kernel) whose
