@@ -576,14 +576,15 @@ def c5_shard(stream, rows_list=(1, 8, 16), reps: int = 5) -> dict:
 MXFP4 = 39
 
 
-def c4_moe(stream, reps: int = 20, copies: int = 2) -> dict:
+def c4_moe(stream, reps: int = 20, copies: int = 2, profile_reps: int = 0) -> dict:
     """BASELINE C4: gpt-oss-20b-shaped experts, 32 MXFP4 experts with gate_up
     [5760, 2880] and down [2880, 2880]; 8 tokens routed top-4 from seeded
     N(0,1) logits (ties to the lower index), entries sorted by (expert,
     pair). One step = the gate_up grouped product (per-token inputs) and the
     down grouped product (per-pair inputs, routing weights), back to back
     over `copies` weight stacks. Algorithmic bytes = the touched experts'
-    weights + f32 inputs and outputs."""
+    weights + f32 inputs and outputs. With profile_reps, the step runs that
+    many times outside any graph and nothing is timed (rocprofv3 passes)."""
     import numpy as np
     import torch
 
@@ -636,6 +637,12 @@ def c4_moe(stream, reps: int = 20, copies: int = 2) -> dict:
                 topk_w.data_ptr(), topk, y2.data_ptr(), hidden, ws2.data_ptr(), ws2.numel(), ctypes.byref(need),
                 inter, hidden, size_m, 1, s))
 
+    if profile_reps:
+        for _ in range(profile_reps):
+            fn(stream.cuda_stream)
+        torch.cuda.synchronize()
+        log(f"profile c4: {profile_reps} MoE steps over {copies} weight stacks ({touched} experts touched)")
+        return {}
     g = capture(fn, stream)
     if L.qmm_moe_launches() < before + 2 * copies:
         raise RuntimeError("the C4 step did not run the grouped expert kernels")
@@ -1051,7 +1058,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="skip the C1 / C4 / C5 sections")
     ap.add_argument("--profile", choices=["single", "dominant", "read33", "read66", "prefill", "prefill_forward",
-                                          "prefill_down", "prefill_down_forward", "copy"],
+                                          "prefill_down", "prefill_down_forward", "copy", "c4"],
                     help="launch only this kernel --steps times (for rocprofv3 counter passes), print no JSON")
     args = ap.parse_args()
 
@@ -1093,6 +1100,9 @@ def main() -> int:
     log(f"{args.copies} layer copies quantized on the device in {time.perf_counter() - t0:.1f} s "
         f"({args.copies * lb['weights'] / 2**30:.2f} GiB of weights)")
 
+    if args.profile == "c4":
+        c4_moe(stream, profile_reps=args.steps)
+        return 0
     if args.profile:
         profile_only(args.profile, layers, outs, stream, args.steps)
         return 0
