@@ -164,11 +164,12 @@ def moe_into(stack, xs, x_stride, sorted_ids, expert_ids, topk_w, topk, rows_out
     return out.cpu().numpy()
 
 
-def test_moe_order_of_entries_does_not_change_results():
+@pytest.mark.parametrize("k", [256, 2880])  # 2880: the packed form
+def test_moe_order_of_entries_does_not_change_results(k):
     """Any order of the routing entries gives the same bits; out of expert
     order there are more runs than experts, and every one is computed (the
     output starts as NaN, so a run left out shows)."""
-    qtype, E, n, k, tokens, topk = 39, 6, 64, 256, 5, 2
+    qtype, E, n, tokens, topk = 39, 6, 64, 5, 2
     sorted_ids, expert_ids, topk_w = routing(tokens, E, topk, 7)
     stack = expert_stack(qtype, E, n, k, 77)
     xs = t32(np.random.default_rng(7).standard_normal((tokens, k)).astype(np.float32))
@@ -181,9 +182,10 @@ def test_moe_order_of_entries_does_not_change_results():
     assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
 
 
-def test_moe_more_runs_than_experts():
+@pytest.mark.parametrize("k", [128, 2048])  # 2048: the packed form
+def test_moe_more_runs_than_experts(k):
     """Entries alternating between two experts: six runs over two experts."""
-    qtype, E, n, k, topk = 8, 2, 48, 128, 1
+    qtype, E, n, topk = 8, 2, 48, 1
     stack = expert_stack(qtype, E, n, k, 13)
     x = np.random.default_rng(13).standard_normal((6, k)).astype(np.float32)
     xs = t32(x)
@@ -224,8 +226,9 @@ def test_moe_prepass_form_matches_one_launch_form(name):
     assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
 
 
-def test_moe_out_of_range_entries_write_nothing():
-    qtype, E, n, k, topk = 39, 4, 32, 64, 1
+@pytest.mark.parametrize("k", [64, 2880])  # 2880: the packed form
+def test_moe_out_of_range_entries_write_nothing(k):
+    qtype, E, n, topk = 39, 4, 32, 1
     stack = expert_stack(qtype, E, n, k, 9)
     x = np.random.default_rng(9).standard_normal((6, k)).astype(np.float32)
     sorted_ids = np.array([0, 1, 2, 3, 4, 5], np.int32)
