@@ -24,6 +24,9 @@
 // (b32_common.h, wave_sum_dpp), so each pair's result is bit-identical to
 // the same product through qmm_forward (times its scale): the reference's
 // "matmul_many equals per-job forward" (quantized/mod.rs:743-745).
+// Three kernels by row length: moe_b32f_kernel (the packed form: an even
+// number of blocks from 64 to 126), moe_b32s_kernel (the other rows of up to
+// 4096 values) and moe_b32_kernel (longer rows).
 #include "b32_common.h"
 
 namespace qmm {
