@@ -24,9 +24,10 @@
 // (b32_common.h, wave_sum_dpp), so each pair's result is bit-identical to
 // the same product through qmm_forward (times its scale): the reference's
 // "matmul_many equals per-job forward" (quantized/mod.rs:743-745).
-// Three kernels by row length: moe_b32f_kernel (the packed form: an even
-// number of blocks from 64 to 126), moe_b32s_kernel (the other rows of up to
-// 4096 values) and moe_b32_kernel (longer rows).
+// MXFP4 rows of up to 128 blocks take moe_fp4_kernel (the matrix-core form);
+// the other rows take one of three kernels by row length: moe_b32f_kernel
+// (the packed form: an even number of blocks from 64 to 126), moe_b32s_kernel
+// (the other rows of up to 4096 values) and moe_b32_kernel (longer rows).
 #include "b32_common.h"
 
 namespace qmm {
@@ -571,6 +572,276 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
   }
 }
 
+// The matrix-core form, for MXFP4 rows of up to 128 blocks. The weight's
+// nibbles are E2M1 codes, so a block's integer dot with the Q8_0 codes is a
+// product on the matrix cores (v_mfma_scale_f32_16x16x128_f8f6f4: B the
+// weight bytes as they lie in the block, A E4M3, both scales 2^0) once each
+// activation code y = 16 h + l (h in [-8, 7], l in [0, 15]) is given as two
+// exact E4M3 codes:
+//     sum_i t(w_i) y_i = 2 (16 H + L),  H = sum_i e2m1(w_i) h_i,  L = sum_i e2m1(w_i) l_i
+// (t = kMxfp4Values = 2 e2m1). Every product and partial sum is a multiple
+// of 1/2 below 2^12, so the matrix-core sums are exact and s_b = 2 (16 H + L)
+// is the decode kernel's integer sum. The product's 16 columns are 16 weight
+// rows and its 128 K values 4 blocks; its 16 rows are 4 entries x 4 block
+// slots, row (p, s) holding entry p's codes in slot s's 32 K values and zeros
+// in the other 96, so output (p, s; j) is block s's sum alone. The weight
+// block's byte i holds values i (low nibble) and i + 16 (high), and the
+// matrix cores read byte i as K 2i, 2i+1, so the activation codes are laid
+// out in that order. Output lane (p, j) forms each block's
+// p_b = (dx_b dy_b) s_b and each unit's 0 + (p_2u + p_2u+1) as b32_unit
+// does, and sums the row's units in wave_sum_dpp's tree (pairs, pairs of
+// pairs, ..., over 64 leaves, +0 past the row's units), so each entry's
+// result has the decode kernel's bits.
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+constexpr int kFp4Pairs = 4;       // entries a pass: the product's 4 row groups
+constexpr int kFp4Rows = 16;       // weight rows a wave: the product's 16 columns
+constexpr int kFp4SegPieces = 10;  // 16-byte pieces holding 8 blocks of a row (136 bytes) at any alignment
+constexpr int kFp4Slots = kFp4Rows * kFp4SegPieces;  // pieces a step: 160
+constexpr int kFp4Loads = (kFp4Slots + 63) / 64;     // a lane's: 3
+constexpr int kFp4Stage = kFp4Slots * 16 + 16;       // and the dword past the last that lds_words reads
+constexpr int kFp4Rec = 128;  // LDS bytes of an entry's block: h0 0 h1 0 l0 0 l1 0, 16 bytes each
+
+struct Fp4Span {
+  uint4 p[kFp4Loads];
+};
+
+inline size_t moe_fp4_lds(int64_t nb) {
+  return 32 + (size_t)kFp4Pairs * kFp4Rec * nb + 16 * (size_t)((nb + 7) & ~7) + (size_t)kMoeSWaves * kFp4Stage;
+}
+
+__global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu(4))) void moe_fp4_kernel(
+    const uint8_t* __restrict__ W, int64_t n, int nb, int64_t estride, int num_experts,
+    const int8_t* __restrict__ yq, const float* __restrict__ yd, const int32_t* __restrict__ runs,
+    const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int topk, int size_m,
+    float* __restrict__ dst, int64_t ldd) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  // LDS: 32 zero bytes; the chunk's codes, record (p, b) at 32 + 128 (p nb + b);
+  // the block scales dy[p][b] (rows of dys floats); the waves' stage buffers
+  const int k = nb * 32;
+  const int dys = (nb + 7) & ~7;
+  float* const dyt = (float*)(smem + 32 + kFp4Pairs * kFp4Rec * nb);
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t* const buf = (uint8_t*)(dyt + kFp4Pairs * dys) + wv * kFp4Stage;
+  const int64_t rb = (int64_t)nb * 17;
+  const int64_t r0 = ((int64_t)blockIdx.x * kMoeSWaves + wv) * kFp4Rows;
+  const int nrows = r0 < n ? (int)(n - r0 < kFp4Rows ? n - r0 : kFp4Rows) : 0;
+  const int nsteps = (nb + 7) >> 3;  // a step: 8 blocks of each of the wave's rows
+
+  // the zeros: 32 bytes at 0 and the gaps of every record (never written after)
+  for (int i = threadIdx.x; i < 2 + 4 * kFp4Pairs * nb; i += blockDim.x) {
+    const int o = i < 2 ? 16 * i : 32 + kFp4Rec * ((i - 2) >> 2) + 16 + 32 * ((i - 2) & 3);
+    *(uint4*)(smem + o) = make_uint4(0u, 0u, 0u, 0u);
+  }
+  // E4M3 codes of l = nibble and of h = nibble - 16 (nibble >= 8), for lut16_at
+  const uint32_t cl0 = 0x44403800u, cl1 = 0x4E4C4A48u, cl2 = 0x53525150u, cl3 = 0x57565554u;
+  const uint32_t ch2 = 0xCACCCED0u, ch3 = 0xB8C0C4C8u;
+
+  const int jn = lane & 15;    // the lane's weight row: its B column and output column
+  const int gk = lane >> 4;    // B: the block slot of the lane's 16 bytes; A: its K group
+  const int pa = jn >> 2, sa = lane & 3;  // A: the entry and block slot of the lane's row
+  // A's K group gk holds K [16 gk, +16) in bytes 0-15 (block slot gk / 2) and
+  // K [64 + 16 gk, +16) in bytes 16-31 (slot 2 + gk / 2): the lane's row has
+  // codes in one of them exactly when (sa & 1) == gk / 2; reading 16 bytes
+  // early puts them in bytes 16-31 with the record's zeros before them
+  const bool aslot = (sa & 1) == (gk >> 1);
+  const int aoff = 32 * (gk & 1) - (sa >= 2 ? 16 : 0);
+  const int po = gk;  // output: the lane's entry
+  const int rowc = jn < nrows ? jn : nrows - 1;
+  int lrow[kFp4Loads], lpc[kFp4Loads];  // each load's row and piece
+#pragma unroll
+  for (int c = 0; c < kFp4Loads; c++) {
+    const int s = lane + 64 * c < kFp4Slots ? lane + 64 * c : kFp4Slots - 1;
+    lrow[c] = s / kFp4SegPieces;
+    lpc[c] = s - lrow[c] * kFp4SegPieces;
+    lrow[c] = lrow[c] < nrows ? lrow[c] : nrows - 1;
+  }
+
+  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  for (int run = blockIdx.y; run < nruns; run += gridDim.y) {
+    const int start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
+    const int len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
+    const int e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+    if (e < 0 || e >= num_experts) continue;
+    const uint8_t* Wr = W + (int64_t)e * estride + r0 * rb;  // the wave's first row
+
+    for (int c0 = 0; c0 < len; c0 += kFp4Pairs) {
+      const int cnt = len - c0 < kFp4Pairs ? len - c0 : kFp4Pairs;
+      int pr[kFp4Pairs];
+      bool use[kFp4Pairs];
+      int64_t in_row[kFp4Pairs];
+#pragma unroll
+      for (int p = 0; p < kFp4Pairs; p++) {
+        pr[p] = __builtin_amdgcn_readfirstlane(ids[start + c0 + (p < cnt ? p : cnt - 1)]);
+        use[p] = p < cnt && pr[p] >= 0 && pr[p] < size_m;
+        in_row[p] = use[p] ? (topk_w ? pr[p] : pr[p] / topk) : 0;
+      }
+      // step ls's bytes: 8 blocks of each row, the pieces of row r in LDS
+      // slots 10 r ..; past the last step the loads read the first bytes of
+      // the quantized activation (cached, never used). The first steps' loads
+      // are issued before the chunk's codes are laid out.
+      int ls = 0;
+      auto load_next = [&](Fp4Span& sp) {
+        const int b0 = 8 * ls;
+        const bool real = ls < nsteps;
+        const int blen = real ? (nb - b0 < 8 ? nb - b0 : 8) : 1;
+#pragma unroll
+        for (int c = 0; c < kFp4Loads; c++) {
+          const uint8_t* pp = real ? Wr + lrow[c] * rb + 17 * b0 : (const uint8_t*)yq;
+          const int off = (int)((uintptr_t)pp & 15);
+          const int pieces = (off + 17 * blen + 15) >> 4;
+          sp.p[c] = ld_stream16(pp - off + 16 * (lpc[c] < pieces ? lpc[c] : pieces - 1));
+        }
+        ls++;
+      };
+      Fp4Span ring[kMoeRing];
+      if (nrows > 0) {
+#pragma unroll
+        for (int j = 0; j < kMoeRing; j++) load_next(ring[j]);
+      }
+
+      // the chunk's codes into LDS, as E4M3 h and l codes in the weight's K order
+      __syncthreads();
+      for (int t = threadIdx.x; t < kFp4Pairs * nb * 2; t += blockDim.x) {
+        const int p = t / (2 * nb), b = (t - p * 2 * nb) >> 1, q = t & 1;
+        bool u = false;
+        int64_t ir = 0;
+#pragma unroll
+        for (int pp = 0; pp < kFp4Pairs; pp++)
+          if (p == pp) u = use[pp], ir = in_row[pp];
+        if (!u) continue;
+        const int8_t* src = yq + ir * k + 32 * b + 8 * q;
+        const uint2 lo = *(const uint2*)src, hi = *(const uint2*)(src + 16);  // values 8q.., 16+8q..
+        uint32_t x[4];  // K 16q + 2i: value 8q + i; K 16q + 2i + 1: value 16 + 8q + i
+        x[0] = __builtin_amdgcn_perm(hi.x, lo.x, 0x05010400u);
+        x[1] = __builtin_amdgcn_perm(hi.x, lo.x, 0x07030602u);
+        x[2] = __builtin_amdgcn_perm(hi.y, lo.y, 0x05010400u);
+        x[3] = __builtin_amdgcn_perm(hi.y, lo.y, 0x07030602u);
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          h[i] = (uint32_t)lut16_at(x[i], 4, cl0, cl1, ch2, ch3);
+          l[i] = (uint32_t)lut16_at(x[i], 0, cl0, cl1, cl2, cl3);
+        }
+        uint8_t* rec = smem + 32 + kFp4Rec * (p * nb + b);
+        *(uint4*)(rec + 32 * q) = make_uint4(h[0], h[1], h[2], h[3]);
+        *(uint4*)(rec + 64 + 32 * q) = make_uint4(l[0], l[1], l[2], l[3]);
+      }
+      for (int t = threadIdx.x; t < kFp4Pairs * nb; t += blockDim.x) {
+        const int p = t / nb, b = t - p * nb;
+        bool u = false;
+        int64_t ir = 0;
+#pragma unroll
+        for (int pp = 0; pp < kFp4Pairs; pp++)
+          if (p == pp) u = use[pp], ir = in_row[pp];
+        if (u) dyt[p * dys + b] = yd[ir * nb + b];
+      }
+      __syncthreads();
+      if (nrows == 0) continue;
+
+      bool a_on = false, o_use = false;
+      int64_t o_row = 0;
+#pragma unroll
+      for (int p = 0; p < kFp4Pairs; p++) {
+        if (pa == p) a_on = aslot && use[p];
+        if (po == p) o_use = use[p], o_row = use[p] ? pr[p] : 0;
+      }
+      const float o_scale = topk_w ? topk_w[o_row] : 1.0f;
+
+      // wave_sum_dpp's tree over the row's 64 leaves (lane L's leaf is unit L):
+      // node G of two leaves is group G's units; v2 .. v32 keep the pending
+      // node of 2 .. 32 leaves (G is uniform: the branches are the wave's)
+      float v2 = 0.0f, v4 = 0.0f, v8 = 0.0f, v16 = 0.0f, v32 = 0.0f, res = 0.0f;
+      auto push = [&](float x, int G) {
+        if (!(G & 1)) {
+          v2 = x;
+        } else if (x = v2 + x, !(G & 2)) {
+          v4 = x;
+        } else if (x = v4 + x, !(G & 4)) {
+          v8 = x;
+        } else if (x = v8 + x, !(G & 8)) {
+          v16 = x;
+        } else if (x = v16 + x, !(G & 16)) {
+          v32 = x;
+        } else {
+          res = v32 + x;
+        }
+      };
+      auto step = [&](Fp4Span& cur, int j) {
+        wave_lds_sync();
+#pragma unroll
+        for (int c = 0; c < kFp4Loads; c++)
+          if (lane + 64 * c < kFp4Slots) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
+        wave_lds_sync();
+        load_next(cur);
+        if (j >= nsteps) return;
+        const int b0 = 8 * j;
+        const int off = (int)(((uintptr_t)(Wr + rowc * rb) + 17 * b0) & 15);
+        const int rbase = 16 * kFp4SegPieces * jn + off;  // row jn's block b0 in the stage buffer
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          const int bg = b0 + 4 * t;  // the group's first block
+          if (bg >= nb) {
+            push(0.0f, 2 * j + t);
+            continue;
+          }
+          uint32_t bw[4];
+          lds_words<4>(buf, rbase + 17 * (4 * t + gk) + 1, bw);
+          const v8i_t bv = {(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3], 0, 0, 0, 0};
+          const int ab = bg + sa;
+          const int ao = a_on && ab < nb ? 32 + kFp4Rec * (pa * nb + ab) + aoff : 0;
+          const int lo = ao ? ao + 64 : 0;
+          const uint4 h0 = *(const uint4*)(smem + ao), h1 = *(const uint4*)(smem + ao + 16);
+          const uint4 l0 = *(const uint4*)(smem + lo), l1 = *(const uint4*)(smem + lo + 16);
+          const v8i_t ah = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+          const v8i_t al = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+          const v4f_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+          const v4f_t sh = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ah, bv, z, 0, 4, 0, 127, 0, 127);
+          const v4f_t sl = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al, bv, z, 0, 4, 0, 127, 0, 127);
+          const float4 dy = *(const float4*)(dyt + po * dys + bg);
+          const float dyv[4] = {dy.x, dy.y, dy.z, dy.w};
+          float pb[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float dx = e8m0_half(buf[rbase + 17 * (4 * t + i)]);
+            const float s = __builtin_fmaf(sh[i], 16.0f, sl[i]) * 2.0f;  // exact
+            pb[i] = bg + i < nb ? (dx * dyv[i]) * s : 0.0f;
+          }
+          push((0.0f + (pb[0] + pb[1])) + (0.0f + (pb[2] + pb[3])), 2 * j + t);
+        }
+      };
+      for (int j = 0; j < nsteps; j += kMoeRing) {
+#pragma unroll
+        for (int jj = 0; jj < kMoeRing; jj++) step(ring[jj], j + jj);
+      }
+      for (int G = 2 * nsteps; G < 32; G++) push(0.0f, G);
+      if (o_use && jn < nrows) dst[o_row * ldd + r0 + jn] = __fmul_rn(res, o_scale);
+    }
+  }
+}
+
+hipError_t launch_moe_fp4(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
+                          const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
+                          float* dst, int64_t ldd, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  const int nb = (int)(k / 32);
+  const int64_t estride = n * nb * 17;
+  const int64_t gy = size_m < num_experts ? size_m : num_experts;
+  const int64_t rows_per_wg = (int64_t)kMoeSWaves * kFp4Rows;
+  const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
+  const size_t lds = moe_fp4_lds(nb);
+  constexpr auto* kfn = &moe_fp4_kernel;
+  if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
+  kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
+                                          topk_w, topk, (int)size_m, dst, ldd);
+  return hipGetLastError();
+}
+
+// Rows the matrix-core form takes: up to 128 blocks (the tree's 64 leaves).
+inline bool moe_fp4_takes(int64_t k) { return k / 32 <= 128 && moe_fp4_lds(k / 32) <= 160 * 1024; }
+
 template <int FMT>
 hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                         const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
@@ -658,6 +929,8 @@ size_t moe_runs_bytes(int64_t size_m) { return (size_t)(1 + 3 * size_m) * sizeof
 hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                       const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                       float* dst, int64_t ldd, int cus, hipStream_t st) {
+  if (type == T_MXFP4 && moe_fp4_takes(k))
+    return launch_moe_fp4(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, st);
   if (moe_stream_fits(k) && moe_packed_takes(k)) {
     switch (type) {
       case T_Q8_0: return launch_moe_f<T_Q8_0>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, st);

@@ -126,7 +126,8 @@ def test_moe_c4_gpt_oss_shapes():
 def test_moe_packed_lane_rows(name, k):
     """Rows of 64-126 blocks, an even number, take the packed form (each lane
     a two-block unit of the wave's contiguous rows, whichever row it falls
-    in); each entry must still equal qmm_forward of its pair bit for bit.
+    in; MXFP4 takes the matrix-core form); each entry must still equal
+    qmm_forward of its pair bit for bit.
     n = 203 leaves the last workgroup and the last wave partly empty, and the
     routing gives runs of one to several entries."""
     qtype = MOE_TYPES[name]
@@ -140,6 +141,37 @@ def test_moe_packed_lane_rows(name, k):
         xs = t32(x)
         tw = topk_w if weighted else None
         out = moe_forward(xs, stack, t32(sorted_ids), t32(expert_ids), t32(topk_w) if weighted else None, topk)
+        out = out.cpu().numpy()
+        check_against_oracle(qtype, stack, x, out, sorted_ids, expert_ids, tw, topk)
+        check_against_forward(stack, xs, out, sorted_ids, expert_ids, tw, topk)
+
+
+@pytest.mark.parametrize("k", [32, 96, 1056, 2880, 4096])
+def test_moe_fp4_matrix_core_rows(k):
+    """MXFP4 rows of up to 128 blocks take the matrix-core form (block sums
+    on v_mfma_scale_f32_16x16x128_f8f6f4, the codes split as 16 h + l): one
+    block, odd block counts (a group of four blocks partly past the row), the
+    128-block maximum; a run of 10 entries (three passes of up to 4), n = 203
+    (the last wave's 16 columns partly past the rows). Each entry must equal
+    qmm_forward of its pair bit for bit."""
+    qtype = MOE_TYPES["MXFP4"]
+    E, n, tokens, topk = 3, 203, 10, 2
+    seed = zlib.crc32(f"fp4-mc-{k}".encode())
+    rng = np.random.default_rng(seed)
+    # expert 1 takes every token's first choice: a run of 10 entries
+    pairs = sorted((1 if j == 0 else (0, 2)[int(rng.integers(2))], t * topk + j)
+                   for t in range(tokens) for j in range(topk))
+    expert_ids = np.array([e for e, _ in pairs], np.int32)
+    sorted_ids = np.array([p for _, p in pairs], np.int32)
+    topk_w = rng.random(tokens * topk).astype(np.float32)
+    stack = expert_stack(qtype, E, n, k, seed & 0xFFFF)
+    for weighted in (False, True):
+        rows = tokens * topk if weighted else tokens
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        xs = t32(x)
+        tw = topk_w if weighted else None
+        out = moe_forward(xs, stack, t32(sorted_ids), t32(expert_ids), t32(topk_w) if weighted else None, topk)
+        assert "launch_moe_fp4" in lib().qmm_last_kernel().decode()
         out = out.cpu().numpy()
         check_against_oracle(qtype, stack, x, out, sorted_ids, expert_ids, tw, topk)
         check_against_forward(stack, xs, out, sorted_ids, expert_ids, tw, topk)
@@ -164,7 +196,7 @@ def moe_into(stack, xs, x_stride, sorted_ids, expert_ids, topk_w, topk, rows_out
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("k", [256, 2880])  # 2880: the packed form
+@pytest.mark.parametrize("k", [256, 2880])  # MXFP4 (type 39): the matrix-core form
 def test_moe_order_of_entries_does_not_change_results(k):
     """Any order of the routing entries gives the same bits; out of expert
     order there are more runs than experts, and every one is computed (the
@@ -226,7 +258,7 @@ def test_moe_prepass_form_matches_one_launch_form(name):
     assert np.array_equal(one.view(np.uint32), two.view(np.uint32))
 
 
-@pytest.mark.parametrize("k", [64, 2880])  # 2880: the packed form
+@pytest.mark.parametrize("k", [64, 2880])  # MXFP4 (type 39): the matrix-core form
 def test_moe_out_of_range_entries_write_nothing(k):
     qtype, E, n, topk = 39, 4, 32, 1
     stack = expert_stack(qtype, E, n, k, 9)

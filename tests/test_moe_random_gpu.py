@@ -1,9 +1,10 @@
 """Grouped expert products (qmm_moe_forward) at seeded random shapes and
 routings: the type, the experts E, the weight rows n, the row length k, the
 tokens and top-k, per-token or per-pair inputs with routing weights, drawn
-from a fixed seed, so the grouped kernels' lines are crossed (rows of fewer
-than 64 blocks, 64-126 blocks of an even count: the packed form, odd
-counts, past 4096 values: the per-row form; the K-quants' run kernels).
+from a fixed seed, so the grouped kernels' lines are crossed (MXFP4 rows of
+up to 128 blocks: the matrix-core form; rows of fewer than 64 blocks, 64-126
+blocks of an even count: the packed form, odd counts, past 4096 values: the
+per-row form; the K-quants' run kernels).
 Each entry is checked against the oracle's product of its pair (1e-3
 normalised, the decode bound) and against qmm_forward of its pair bit for
 bit (the reference's matmul_many equals per-job forward,
