@@ -592,23 +592,38 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
 // does, and sums the row's units in wave_sum_dpp's tree (pairs, pairs of
 // pairs, ..., over 64 leaves, +0 past the row's units), so each entry's
 // result has the decode kernel's bits.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef int v8i_t __attribute__((ext_vector_type(8)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 constexpr int kFp4Pairs = 4;       // entries a pass: the product's 4 row groups
 constexpr int kFp4Rows = 16;       // weight rows a wave: the product's 16 columns
-constexpr int kFp4SegPieces = 10;  // 16-byte pieces holding 8 blocks of a row (136 bytes) at any alignment
+// A step takes 8 blocks (136 bytes) of each of the wave's rows: the
+// 16-byte pieces from the one holding its first byte to the one holding its
+// last, row r's in slots 10 r .. of the wave's stage buffer.
+constexpr int kFp4StepBlocks = 8;
+constexpr int kFp4SegPieces = 10;  // 136 bytes at any alignment
 constexpr int kFp4Slots = kFp4Rows * kFp4SegPieces;  // pieces a step: 160
 constexpr int kFp4Loads = (kFp4Slots + 63) / 64;     // a lane's: 3
-constexpr int kFp4Stage = kFp4Slots * 16 + 16;       // and the dword past the last that lds_words reads
-constexpr int kFp4Rec = 128;  // LDS bytes of an entry's block: h0 0 h1 0 l0 0 l1 0, 16 bytes each
+constexpr int kFp4Stage = kFp4Slots * 16 + 16;  // and the dword past the last that lds_words reads
+constexpr int kFp4Rec = 64;  // LDS bytes of an entry's block: h0 h1 l0 l1, 16 bytes each
+constexpr int kFp4Ring = 2;  // steps in flight per wave
+// LDS: 64 zero bytes, then entry p's records at kFp4Codes + p P (P = 64 nb
+// rounded up to 64 mod 256): in each 16-lane phase of an A read the four
+// lanes that read codes fall on distinct banks, and the others read zeros
+// (at 32 for the h codes, at 0 for the l codes) on banks of their own
+constexpr int kFp4Codes = 64;
+__host__ __device__ inline int fp4_entry_stride(int nb) { return 64 * nb + (64 - 64 * (nb % 4) + 256) % 256; }
+// the scales' rows: whole steps, the blocks past the row zero
+__host__ __device__ inline int fp4_dy_stride(int nb) { return (nb + kFp4StepBlocks - 1) / kFp4StepBlocks * kFp4StepBlocks; }
 
 struct Fp4Span {
   uint4 p[kFp4Loads];
 };
 
 inline size_t moe_fp4_lds(int64_t nb) {
-  return 32 + (size_t)kFp4Pairs * kFp4Rec * nb + 16 * (size_t)((nb + 7) & ~7) + (size_t)kMoeSWaves * kFp4Stage;
+  return kFp4Codes + (size_t)kFp4Pairs * fp4_entry_stride((int)nb) + 16 * (size_t)fp4_dy_stride((int)nb) +
+         (size_t)kMoeSWaves * kFp4Stage;
 }
 
 __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu(4))) void moe_fp4_kernel(
@@ -618,23 +633,23 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
     float* __restrict__ dst, int64_t ldd) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  // LDS: 32 zero bytes; the chunk's codes, record (p, b) at 32 + 128 (p nb + b);
+  // LDS: zeros; the chunk's codes, record (p, b) at kFp4Codes + p P + 64 b;
   // the block scales dy[p][b] (rows of dys floats); the waves' stage buffers
   const int k = nb * 32;
-  const int dys = (nb + 7) & ~7;
-  float* const dyt = (float*)(smem + 32 + kFp4Pairs * kFp4Rec * nb);
+  const int dys = fp4_dy_stride(nb);
+  const int P = fp4_entry_stride(nb);
+  float* const dyt = (float*)(smem + kFp4Codes + kFp4Pairs * P);
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint8_t* const buf = (uint8_t*)(dyt + kFp4Pairs * dys) + wv * kFp4Stage;
   const int64_t rb = (int64_t)nb * 17;
   const int64_t r0 = ((int64_t)blockIdx.x * kMoeSWaves + wv) * kFp4Rows;
   const int nrows = r0 < n ? (int)(n - r0 < kFp4Rows ? n - r0 : kFp4Rows) : 0;
-  const int nsteps = (nb + 7) >> 3;  // a step: 8 blocks of each of the wave's rows
+  const int nsteps = (nb + kFp4StepBlocks - 1) / kFp4StepBlocks;
 
-  // the zeros: 32 bytes at 0 and the gaps of every record (never written after)
-  for (int i = threadIdx.x; i < 2 + 4 * kFp4Pairs * nb; i += blockDim.x) {
-    const int o = i < 2 ? 16 * i : 32 + kFp4Rec * ((i - 2) >> 2) + 16 + 32 * ((i - 2) & 3);
-    *(uint4*)(smem + o) = make_uint4(0u, 0u, 0u, 0u);
-  }
+  // the zeros, and the scales past the row (blocks past the row then give
+  // (dx * 0) * s = +-0)
+  for (int i = threadIdx.x; i < kFp4Codes / 16 + kFp4Pairs * dys / 4; i += blockDim.x)
+    *(uint4*)(i < kFp4Codes / 16 ? smem + 16 * i : (uint8_t*)dyt + 16 * (i - kFp4Codes / 16)) = make_uint4(0u, 0u, 0u, 0u);
   // E4M3 codes of l = nibble and of h = nibble - 16 (nibble >= 8), for lut16_at
   const uint32_t cl0 = 0x44403800u, cl1 = 0x4E4C4A48u, cl2 = 0x53525150u, cl3 = 0x57565554u;
   const uint32_t ch2 = 0xCACCCED0u, ch3 = 0xB8C0C4C8u;
@@ -644,19 +659,22 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
   const int pa = jn >> 2, sa = lane & 3;  // A: the entry and block slot of the lane's row
   // A's K group gk holds K [16 gk, +16) in bytes 0-15 (block slot gk / 2) and
   // K [64 + 16 gk, +16) in bytes 16-31 (slot 2 + gk / 2): the lane's row has
-  // codes in one of them exactly when (sa & 1) == gk / 2; reading 16 bytes
-  // early puts them in bytes 16-31 with the record's zeros before them
+  // codes in one of them exactly when (sa & 1) == gk / 2, the low half for
+  // slots 0 and 1; the other half is zeros
   const bool aslot = (sa & 1) == (gk >> 1);
-  const int aoff = 32 * (gk & 1) - (sa >= 2 ? 16 : 0);
+  const bool alow = sa < 2;
+  const int aoff = 16 * (gk & 1);
   const int po = gk;  // output: the lane's entry
   const int rowc = jn < nrows ? jn : nrows - 1;
-  int lrow[kFp4Loads], lpc[kFp4Loads];  // each load's row and piece
+  // load c of a step: piece lpc of the row at byte lro from the wave's
+  // first (packed: lro in bits 0-15, as the wave's rows span < 32 KiB, lpc
+  // 16-19)
+  uint32_t lpk[kFp4Loads];
 #pragma unroll
   for (int c = 0; c < kFp4Loads; c++) {
     const int s = lane + 64 * c < kFp4Slots ? lane + 64 * c : kFp4Slots - 1;
-    lrow[c] = s / kFp4SegPieces;
-    lpc[c] = s - lrow[c] * kFp4SegPieces;
-    lrow[c] = lrow[c] < nrows ? lrow[c] : nrows - 1;
+    const int r = s / kFp4SegPieces;
+    lpk[c] = (uint32_t)((r < nrows ? r : nrows - 1) * (int)rb) | (uint32_t)(s - r * kFp4SegPieces) << 16;
   }
 
   const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
@@ -678,28 +696,33 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
         use[p] = p < cnt && pr[p] >= 0 && pr[p] < size_m;
         in_row[p] = use[p] ? (topk_w ? pr[p] : pr[p] / topk) : 0;
       }
-      // step ls's bytes: 8 blocks of each row, the pieces of row r in LDS
-      // slots 10 r ..; past the last step the loads read the first bytes of
-      // the quantized activation (cached, never used). The first steps' loads
-      // are issued before the chunk's codes are laid out.
+      // step ls's loads; past the last step they read the first bytes of the
+      // quantized activation (cached, never used). The first steps' loads
+      // are issued before the chunk's codes are laid out. (32-bit offsets
+      // from the 16-byte aligned address at or below the uniform base, so
+      // none is negative; a piece past the step's last is replaced by its
+      // last, so no load touches bytes of another step.)
       int ls = 0;
       auto load_next = [&](Fp4Span& sp) {
-        const int b0 = 8 * ls;
         const bool real = ls < nsteps;
-        const int blen = real ? (nb - b0 < 8 ? nb - b0 : 8) : 1;
+        const uint8_t* base = real ? Wr : (const uint8_t*)yq;
+        const uint32_t bofs = (uint32_t)(uintptr_t)base & 15u;
+        const uint8_t* const ba = base - bofs;
+        const int blen = real ? (nb - 8 * ls < 8 ? nb - 8 * ls : 8) : 1;
+        const uint32_t st = bofs + (real ? 136u * (uint32_t)ls : 0u);
 #pragma unroll
         for (int c = 0; c < kFp4Loads; c++) {
-          const uint8_t* pp = real ? Wr + lrow[c] * rb + 17 * b0 : (const uint8_t*)yq;
-          const int off = (int)((uintptr_t)pp & 15);
-          const int pieces = (off + 17 * blen + 15) >> 4;
-          sp.p[c] = ld_stream16(pp - off + 16 * (lpc[c] < pieces ? lpc[c] : pieces - 1));
+          const uint32_t rel = (real ? lpk[c] & 0xFFFFu : 0u) + st;  // the step's first byte, from ba
+          const uint32_t pieces = ((rel & 15u) + 17u * (uint32_t)blen + 15u) >> 4;
+          const uint32_t pc = lpk[c] >> 16;
+          sp.p[c] = ld_stream16(ba + ((rel & ~15u) + 16u * (pc < pieces ? pc : pieces - 1u)));
         }
         ls++;
       };
-      Fp4Span ring[kMoeRing];
+      Fp4Span ring[kFp4Ring];
       if (nrows > 0) {
 #pragma unroll
-        for (int j = 0; j < kMoeRing; j++) load_next(ring[j]);
+        for (int j = 0; j < kFp4Ring; j++) load_next(ring[j]);
       }
 
       // the chunk's codes into LDS, as E4M3 h and l codes in the weight's K order
@@ -725,9 +748,9 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
           h[i] = (uint32_t)lut16_at(x[i], 4, cl0, cl1, ch2, ch3);
           l[i] = (uint32_t)lut16_at(x[i], 0, cl0, cl1, cl2, cl3);
         }
-        uint8_t* rec = smem + 32 + kFp4Rec * (p * nb + b);
-        *(uint4*)(rec + 32 * q) = make_uint4(h[0], h[1], h[2], h[3]);
-        *(uint4*)(rec + 64 + 32 * q) = make_uint4(l[0], l[1], l[2], l[3]);
+        uint8_t* rec = smem + kFp4Codes + P * p + kFp4Rec * b;
+        *(uint4*)(rec + 16 * q) = make_uint4(h[0], h[1], h[2], h[3]);
+        *(uint4*)(rec + 32 + 16 * q) = make_uint4(l[0], l[1], l[2], l[3]);
       }
       for (int t = threadIdx.x; t < kFp4Pairs * nb; t += blockDim.x) {
         const int p = t / nb, b = t - p * nb;
@@ -741,35 +764,29 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
       __syncthreads();
       if (nrows == 0) continue;
 
-      bool a_on = false, o_use = false;
-      int64_t o_row = 0;
+      bool a_on = false;
 #pragma unroll
-      for (int p = 0; p < kFp4Pairs; p++) {
+      for (int p = 0; p < kFp4Pairs; p++)
         if (pa == p) a_on = aslot && use[p];
-        if (po == p) o_use = use[p], o_row = use[p] ? pr[p] : 0;
-      }
-      const float o_scale = topk_w ? topk_w[o_row] : 1.0f;
+      const uint32_t browlo = (uint32_t)(uintptr_t)Wr + (uint32_t)(rowc * (int)rb);  // row rowc's address, low bits
 
-      // wave_sum_dpp's tree over the row's 64 leaves (lane L's leaf is unit L):
-      // node G of two leaves is group G's units; v2 .. v32 keep the pending
-      // node of 2 .. 32 leaves (G is uniform: the branches are the wave's)
-      float v2 = 0.0f, v4 = 0.0f, v8 = 0.0f, v16 = 0.0f, v32 = 0.0f, res = 0.0f;
-      auto push = [&](float x, int G) {
-        if (!(G & 1)) {
-          v2 = x;
-        } else if (x = v2 + x, !(G & 2)) {
-          v4 = x;
-        } else if (x = v4 + x, !(G & 4)) {
-          v8 = x;
-        } else if (x = v8 + x, !(G & 8)) {
-          v16 = x;
-        } else if (x = v16 + x, !(G & 16)) {
-          v32 = x;
-        } else {
-          res = v32 + x;
-        }
+      // wave_sum_dpp's tree over the row's 64 leaves (lane L's leaf is unit
+      // L): group t's node holds 2 leaves, step j's two groups give its node
+      // of 4, x = g0 + g1, and push(x, j) folds it in as a binary counter
+      // over j: v4 .. v32 keep the pending nodes of 4 .. 32 leaves (every sum
+      // formed, the stores selected: j is uniform)
+      float v4 = 0.0f, v8 = 0.0f, v16 = 0.0f, v32 = 0.0f, res = 0.0f;
+      auto push = [&](float x, int j) {
+        const bool b0 = j & 1, b1 = (j & 3) == 3, b2 = (j & 7) == 7, b3 = (j & 15) == 15;
+        const float x8 = v4 + x, x16 = v8 + x8, x32 = v16 + x16, x64 = v32 + x32;
+        v4 = b0 ? v4 : x;
+        v8 = b0 && !(j & 2) ? x8 : v8;
+        v16 = b1 && !(j & 4) ? x16 : v16;
+        v32 = b2 && !(j & 8) ? x32 : v32;
+        res = b3 ? x64 : res;
       };
       auto step = [&](Fp4Span& cur, int j) {
+        __builtin_amdgcn_sched_barrier(0);
         wave_lds_sync();
 #pragma unroll
         for (int c = 0; c < kFp4Loads; c++)
@@ -777,47 +794,58 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
         wave_lds_sync();
         load_next(cur);
         if (j >= nsteps) return;
-        const int b0 = 8 * j;
-        const int off = (int)(((uintptr_t)(Wr + rowc * rb) + 17 * b0) & 15);
+        const int b0 = kFp4StepBlocks * j;
+        const int off = (int)((browlo + 17u * (uint32_t)b0) & 15u);
         const int rbase = 16 * kFp4SegPieces * jn + off;  // row jn's block b0 in the stage buffer
+        float g[kFp4StepBlocks / 4];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-          const int bg = b0 + 4 * t;  // the group's first block
-          if (bg >= nb) {
-            push(0.0f, 2 * j + t);
-            continue;
-          }
+        for (int t = 0; t < kFp4StepBlocks / 4; t++) {
+          // group t: blocks bg .. bg + 3 (past the row: zero codes, zero scales)
+          const int bg = b0 + 4 * t;
           uint32_t bw[4];
           lds_words<4>(buf, rbase + 17 * (4 * t + gk) + 1, bw);
-          const v8i_t bv = {(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3], 0, 0, 0, 0};
+          const v4i_t b4 = {(int)bw[0], (int)bw[1], (int)bw[2], (int)bw[3]};
+          const v8i_t bv = __builtin_shufflevector(b4, b4, 0, 1, 2, 3, -1, -1, -1, -1);  // E2M1: 4 registers read
           const int ab = bg + sa;
-          const int ao = a_on && ab < nb ? 32 + kFp4Rec * (pa * nb + ab) + aoff : 0;
-          const int lo = ao ? ao + 64 : 0;
-          const uint4 h0 = *(const uint4*)(smem + ao), h1 = *(const uint4*)(smem + ao + 16);
-          const uint4 l0 = *(const uint4*)(smem + lo), l1 = *(const uint4*)(smem + lo + 16);
-          const v8i_t ah = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-          const v8i_t al = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+          const bool on = a_on && ab < nb;
+          const int ao = kFp4Codes + P * pa + kFp4Rec * ab + aoff;  // the h codes; the l codes 32 on
+          const bool lo_on = on && alow, hi_on = on && !alow;
+          // s_b = 32 H + 2 L = sum_i t(w_i) y_i, exact: the A scales 2^5 and 2^1
           const v4f_t z = {0.0f, 0.0f, 0.0f, 0.0f};
-          const v4f_t sh = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ah, bv, z, 0, 4, 0, 127, 0, 127);
-          const v4f_t sl = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al, bv, z, 0, 4, 0, 127, 0, 127);
+          const v4i_t h0 = *(const v4i_t*)(smem + (lo_on ? ao : 32)), h1 = *(const v4i_t*)(smem + (hi_on ? ao : 32));
+          const v8i_t ah = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+          v4f_t sb = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ah, bv, z, 0, 4, 0, 132, 0, 127);
+          __builtin_amdgcn_sched_barrier(0);  // one A operand live at a time
+          const v4i_t l0 = *(const v4i_t*)(smem + (lo_on ? ao + 32 : 0)), l1 = *(const v4i_t*)(smem + (hi_on ? ao + 32 : 0));
+          const v8i_t al = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
+          sb = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al, bv, sb, 0, 4, 0, 128, 0, 127);
           const float4 dy = *(const float4*)(dyt + po * dys + bg);
           const float dyv[4] = {dy.x, dy.y, dy.z, dy.w};
           float pb[4];
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            const float dx = e8m0_half(buf[rbase + 17 * (4 * t + i)]);
-            const float s = __builtin_fmaf(sh[i], 16.0f, sl[i]) * 2.0f;  // exact
-            pb[i] = bg + i < nb ? (dx * dyv[i]) * s : 0.0f;
+            // e8m0_half: 2^(e - 128), exact (subnormal for e < 2)
+            const float dx = __builtin_amdgcn_ldexpf(1.0f, (int)buf[rbase + 17 * (4 * t + i)] - 128);
+            pb[i] = (dx * dyv[i]) * sb[i];
           }
-          push((0.0f + (pb[0] + pb[1])) + (0.0f + (pb[2] + pb[3])), 2 * j + t);
+          // = (0 + (p0 + p1)) + (0 + (p2 + p3)) bit for bit: a p here differs
+          // from the decode kernel's only in the sign of a zero
+          g[t] = 0.0f + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
+          __builtin_amdgcn_sched_barrier(0);  // one group's operands live at a time
         }
+        push(g[0] + g[1], j);
       };
-      for (int j = 0; j < nsteps; j += kMoeRing) {
+      for (int j = 0; j < nsteps; j += kFp4Ring) {
 #pragma unroll
-        for (int jj = 0; jj < kMoeRing; jj++) step(ring[jj], j + jj);
+        for (int jj = 0; jj < kFp4Ring; jj++) step(ring[jj], j + jj);
       }
-      for (int G = 2 * nsteps; G < 32; G++) push(0.0f, G);
-      if (o_use && jn < nrows) dst[o_row * ldd + r0 + jn] = __fmul_rn(res, o_scale);
+      for (int j = nsteps; j < 64 / (kFp4StepBlocks / 2); j++) push(0.0f + 0.0f, j);
+      bool o_use = false;
+      int64_t o_row = 0;
+#pragma unroll
+      for (int p = 0; p < kFp4Pairs; p++)
+        if (po == p) o_use = use[p], o_row = use[p] ? pr[p] : 0;
+      if (o_use && jn < nrows) dst[o_row * ldd + r0 + jn] = __fmul_rn(res, topk_w ? topk_w[o_row] : 1.0f);
     }
   }
 }
