@@ -600,12 +600,16 @@ constexpr int kFp4Pairs = 4;       // entries a pass: the product's 4 row groups
 constexpr int kFp4Rows = 16;       // weight rows a wave: the product's 16 columns
 // A step takes 8 blocks (136 bytes) of each of the wave's rows: the
 // 16-byte pieces from the one holding its first byte to the one holding its
-// last, row r's in slots 10 r .. of the wave's stage buffer.
+// last, row r's at piece 11 r .. of the wave's stage buffer.
 constexpr int kFp4StepBlocks = 8;
 constexpr int kFp4SegPieces = 10;  // 136 bytes at any alignment
 constexpr int kFp4Slots = kFp4Rows * kFp4SegPieces;  // pieces a step: 160
 constexpr int kFp4Loads = (kFp4Slots + 63) / 64;     // a lane's: 3
-constexpr int kFp4Stage = kFp4Slots * 16 + 16;  // and the dword past the last that lds_words reads
+// a row's 10 pieces 176 bytes apart (44 banks: the 16 rows of a read on
+// distinct banks; 160 bytes put rows 8 apart, whose bytes also share their
+// alignment, on the same ones)
+constexpr int kFp4RowStride = 11;
+constexpr int kFp4Stage = kFp4Rows * kFp4RowStride * 16 + 16;  // and the dword past the last that lds_words reads
 constexpr int kFp4Rec = 64;  // LDS bytes of an entry's block: h0 h1 l0 l1, 16 bytes each
 constexpr int kFp4Ring = 2;  // steps in flight per wave
 // LDS: 64 zero bytes, then entry p's records at kFp4Codes + p P (P = 64 nb
@@ -790,13 +794,13 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
         wave_lds_sync();
 #pragma unroll
         for (int c = 0; c < kFp4Loads; c++)
-          if (lane + 64 * c < kFp4Slots) *(uint4*)(buf + 16 * (lane + 64 * c)) = cur.p[c];
+          if (lane + 64 * c < kFp4Slots) *(uint4*)(buf + 16 * (lane + 64 * c + (lane + 64 * c) / kFp4SegPieces)) = cur.p[c];
         wave_lds_sync();
         load_next(cur);
         if (j >= nsteps) return;
         const int b0 = kFp4StepBlocks * j;
         const int off = (int)((browlo + 17u * (uint32_t)b0) & 15u);
-        const int rbase = 16 * kFp4SegPieces * jn + off;  // row jn's block b0 in the stage buffer
+        const int rbase = 16 * kFp4RowStride * jn + off;  // row jn's block b0 in the stage buffer
         float g[kFp4StepBlocks / 4];
 #pragma unroll
         for (int t = 0; t < kFp4StepBlocks / 4; t++) {
