@@ -596,6 +596,7 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 typedef int v8i_t __attribute__((ext_vector_type(8)));
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 
+constexpr int kMoeFusedMaxEntries = 256;  // routings the fused form takes (each wave scans them)
 constexpr int kFp4Pairs = 4;       // entries a pass: the product's 4 row groups
 constexpr int kFp4Rows = 16;       // weight rows a wave: the product's 16 columns
 // A step takes 8 blocks (136 bytes) of each of the wave's rows: the
@@ -630,9 +631,17 @@ inline size_t moe_fp4_lds(int64_t nb) {
          (size_t)kMoeSWaves * kFp4Stage;
 }
 
+// kFused: the kernel takes the f32 input rows and the routing's expert ids
+// itself (the one launch of a small routing): each wave finds its runs in
+// expert_ids, and the chunk's codes and scales are quantized in the set-up
+// with the quantizer's own arithmetic (q8_0_kernel, quantize.hip), so they
+// have its bits. Otherwise the quantized planes (yq, yd) and the run table
+// come from launch_act_quantize_moe.
+template <bool kFused>
 __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu(4))) void moe_fp4_kernel(
     const uint8_t* __restrict__ W, int64_t n, int nb, int64_t estride, int num_experts,
     const int8_t* __restrict__ yq, const float* __restrict__ yd, const int32_t* __restrict__ runs,
+    const float* __restrict__ xa, int64_t x_stride, const int32_t* __restrict__ expert_ids, int xvec,
     const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int topk, int size_m,
     float* __restrict__ dst, int64_t ldd) {
 #pragma clang fp contract(off)
@@ -681,11 +690,39 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
     lpk[c] = (uint32_t)((r < nrows ? r : nrows - 1) * (int)rb) | (uint32_t)(s - r * kFp4SegPieces) << 16;
   }
 
-  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  // fused: a run starts at entry 0 and wherever the expert differs from the
+  // entry before (moe_runs_block's table, found by ballots over 64 entries)
+  auto run_start = [&](int i) { return i < size_m && (i == 0 || expert_ids[i] != expert_ids[i - 1]); };
+  int nruns;
+  if (kFused) {
+    int c = 0;
+    for (int c0 = 0; c0 < size_m; c0 += 64) c += __builtin_popcountll(__ballot(run_start(c0 + lane)));
+    nruns = __builtin_amdgcn_readfirstlane(c);
+  } else {
+    nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  }
   for (int run = blockIdx.y; run < nruns; run += gridDim.y) {
-    const int start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
-    const int len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
-    const int e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+    int start, len, e;
+    if (kFused) {
+      // the run-th and (run + 1)-th starts (size_m past the last)
+      int s0 = size_m, s1 = size_m, cum = 0;
+      for (int c0 = 0; c0 < size_m; c0 += 64) {
+        const bool f = run_start(c0 + lane);
+        const uint64_t m = __ballot(f);
+        const int rank = cum + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        const uint64_t m0 = __ballot(f && rank == run), m1 = __ballot(f && rank == run + 1);
+        if (m0 && s0 == size_m) s0 = c0 + __builtin_ctzll(m0);
+        if (m1 && s1 == size_m) s1 = c0 + __builtin_ctzll(m1);
+        cum += __builtin_popcountll(m);
+      }
+      start = __builtin_amdgcn_readfirstlane(s0);
+      len = __builtin_amdgcn_readfirstlane(s1 - s0);
+      e = __builtin_amdgcn_readfirstlane(expert_ids[start]);
+    } else {
+      start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
+      len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
+      e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+    }
     if (e < 0 || e >= num_experts) continue;
     const uint8_t* Wr = W + (int64_t)e * estride + r0 * rb;  // the wave's first row
 
@@ -700,8 +737,8 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
         use[p] = p < cnt && pr[p] >= 0 && pr[p] < size_m;
         in_row[p] = use[p] ? (topk_w ? pr[p] : pr[p] / topk) : 0;
       }
-      // step ls's loads; past the last step they read the first bytes of the
-      // quantized activation (cached, never used). The first steps' loads
+      // step ls's loads; past the last step they read the wave's first bytes
+      // again (cached, never used). The first steps' loads
       // are issued before the chunk's codes are laid out. (32-bit offsets
       // from the 16-byte aligned address at or below the uniform base, so
       // none is negative; a piece past the step's last is replaced by its
@@ -709,7 +746,7 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
       int ls = 0;
       auto load_next = [&](Fp4Span& sp) {
         const bool real = ls < nsteps;
-        const uint8_t* base = real ? Wr : (const uint8_t*)yq;
+        const uint8_t* base = Wr;
         const uint32_t bofs = (uint32_t)(uintptr_t)base & 15u;
         const uint8_t* const ba = base - bofs;
         const int blen = real ? (nb - 8 * ls < 8 ? nb - 8 * ls : 8) : 1;
@@ -739,8 +776,44 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
         for (int pp = 0; pp < kFp4Pairs; pp++)
           if (p == pp) u = use[pp], ir = in_row[pp];
         if (!u) continue;
-        const int8_t* src = yq + ir * k + 32 * b + 8 * q;
-        const uint2 lo = *(const uint2*)src, hi = *(const uint2*)(src + 16);  // values 8q.., 16+8q..
+        uint2 lo, hi;  // the codes of values 8q .., 16 + 8q ..
+        if (kFused) {
+          // q8_0_kernel's block: the maximum over 4-value groups as bits,
+          // across the pair of lanes of this block (both run this task)
+          const float* xr = xa + ir * x_stride + 32 * b + 8 * q;
+          float v[16];
+          if (xvec) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+              const float4 f = *(const float4*)(xr + (g < 2 ? 4 * g : 8 + 4 * g));
+              v[4 * g] = f.x, v[4 * g + 1] = f.y, v[4 * g + 2] = f.z, v[4 * g + 3] = f.w;
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = xr[i < 8 ? i : 8 + i];
+          }
+          uint32_t ab = 0u;
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            const float a = fmaxf(fmaxf(fabsf(v[4 * g]), fabsf(v[4 * g + 1])), fmaxf(fabsf(v[4 * g + 2]), fabsf(v[4 * g + 3])));
+            ab = max(ab, __float_as_uint(fmaxf(a, 0.0f)));
+          }
+          ab = max(ab, (uint32_t)__shfl_xor((int)ab, 1, 64));
+          const float d = __uint_as_float(ab) / 127.0f;
+          const float id = d != 0.0f ? 1.0f / d : 0.0f;
+          uint32_t cw[4];
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+            cw[g] = pack4_i8(q8_0_code(v[4 * g] * id), q8_0_code(v[4 * g + 1] * id), q8_0_code(v[4 * g + 2] * id),
+                             q8_0_code(v[4 * g + 3] * id));
+          lo = make_uint2(cw[0], cw[1]);
+          hi = make_uint2(cw[2], cw[3]);
+          if (q == 0) dyt[p * dys + b] = h2f(f2h(d));  // Q8_0's block scale is an f16
+        } else {
+          const int8_t* src = yq + ir * k + 32 * b + 8 * q;
+          lo = *(const uint2*)src;
+          hi = *(const uint2*)(src + 16);
+        }
         uint32_t x[4];  // K 16q + 2i: value 8q + i; K 16q + 2i + 1: value 16 + 8q + i
         x[0] = __builtin_amdgcn_perm(hi.x, lo.x, 0x05010400u);
         x[1] = __builtin_amdgcn_perm(hi.x, lo.x, 0x07030602u);
@@ -756,7 +829,7 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
         *(uint4*)(rec + 16 * q) = make_uint4(h[0], h[1], h[2], h[3]);
         *(uint4*)(rec + 32 + 16 * q) = make_uint4(l[0], l[1], l[2], l[3]);
       }
-      for (int t = threadIdx.x; t < kFp4Pairs * nb; t += blockDim.x) {
+      for (int t = threadIdx.x; !kFused && t < kFp4Pairs * nb; t += blockDim.x) {
         const int p = t / nb, b = t - p * nb;
         bool u = false;
         int64_t ir = 0;
@@ -864,15 +937,41 @@ hipError_t launch_moe_fp4(const void* w, int num_experts, int64_t n, int64_t k, 
   const int64_t rows_per_wg = (int64_t)kMoeSWaves * kFp4Rows;
   const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
   const size_t lds = moe_fp4_lds(nb);
-  constexpr auto* kfn = &moe_fp4_kernel;
+  constexpr auto* kfn = &moe_fp4_kernel<false>;
   if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
-  kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs, ids,
-                                          topk_w, topk, (int)size_m, dst, ldd);
+  kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, p.codes, p.d, runs,
+                                          nullptr, 0, nullptr, 0, ids, topk_w, topk, (int)size_m, dst, ldd);
   return hipGetLastError();
 }
 
 // Rows the matrix-core form takes: up to 128 blocks (the tree's 64 leaves).
 inline bool moe_fp4_takes(int64_t k) { return k / 32 <= 128 && moe_fp4_lds(k / 32) <= 160 * 1024; }
+
+}  // namespace
+
+bool moe_fp4_fused_takes(int type, int64_t k, int64_t size_m) {
+  return type == T_MXFP4 && moe_fp4_takes(k) && size_m <= kMoeFusedMaxEntries;
+}
+
+hipError_t launch_moe_fp4_fused(const void* w, int num_experts, int64_t n, int64_t k, const float* x,
+                                int64_t x_stride, const int32_t* expert_ids, const int32_t* ids, const float* topk_w,
+                                int topk, int64_t size_m, float* dst, int64_t ldd, hipStream_t st) {
+  QMM_NOTE_LAUNCH();
+  const int nb = (int)(k / 32);
+  const int64_t estride = n * nb * 17;
+  const int64_t gy = size_m < num_experts ? size_m : num_experts;
+  const int64_t rows_per_wg = (int64_t)kMoeSWaves * kFp4Rows;
+  const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
+  const size_t lds = moe_fp4_lds(nb);
+  const int xvec = ((uintptr_t)x % 16 == 0) && (x_stride % 4 == 0);
+  constexpr auto* kfn = &moe_fp4_kernel<true>;
+  if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
+  kfn<<<grid, 64 * kMoeSWaves, lds, st>>>((const uint8_t*)w, n, nb, estride, num_experts, nullptr, nullptr, nullptr,
+                                          x, x_stride, expert_ids, xvec, ids, topk_w, topk, (int)size_m, dst, ldd);
+  return hipGetLastError();
+}
+
+namespace {
 
 template <int FMT>
 hipError_t launch_moe_s(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,

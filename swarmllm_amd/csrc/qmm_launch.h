@@ -129,6 +129,14 @@ hipError_t launch_moe_kq(int type, const void* w, int num_experts, int64_t n, in
 hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                       const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                       float* dst, int64_t ldd, int cus, hipStream_t st);
+// MXFP4 routings of up to 256 entries, rows of up to 128 blocks: the grouped
+// product in one launch, the kernel finding the runs and quantizing the f32
+// input rows itself (the same codes, scales and result bits as the two-launch
+// form).
+bool moe_fp4_fused_takes(int type, int64_t k, int64_t size_m);
+hipError_t launch_moe_fp4_fused(const void* w, int num_experts, int64_t n, int64_t k, const float* x,
+                                int64_t x_stride, const int32_t* expert_ids, const int32_t* ids, const float* topk_w,
+                                int topk, int64_t size_m, float* dst, int64_t ldd, hipStream_t st);
 
 // Grouped expert products of prompt-size routings on the f16 / bf16 matrix
 // cores (moe_pf.hip): the types and row lengths covered, a weight row's

@@ -152,8 +152,11 @@ def test_moe_fp4_matrix_core_rows(k):
     on v_mfma_scale_f32_16x16x128_f8f6f4, the codes split as 16 h + l): one
     block, odd block counts (a group of four blocks partly past the row), the
     128-block maximum; a run of 10 entries (three passes of up to 4), n = 203
-    (the last wave's 16 columns partly past the rows). Each entry must equal
-    qmm_forward of its pair bit for bit."""
+    (the last wave's 16 columns partly past the rows). A routing this small
+    takes the one-launch form, the kernel quantizing its input rows and
+    finding the runs itself. Each entry must equal qmm_forward of its pair
+    bit for bit (the two-launch form of larger routings is checked the same
+    way in test_moe_prepass_form_matches_one_launch_form)."""
     qtype = MOE_TYPES["MXFP4"]
     E, n, tokens, topk = 3, 203, 10, 2
     seed = zlib.crc32(f"fp4-mc-{k}".encode())
@@ -171,7 +174,7 @@ def test_moe_fp4_matrix_core_rows(k):
         xs = t32(x)
         tw = topk_w if weighted else None
         out = moe_forward(xs, stack, t32(sorted_ids), t32(expert_ids), t32(topk_w) if weighted else None, topk)
-        assert "launch_moe_fp4" in lib().qmm_last_kernel().decode()
+        assert "launch_moe_fp4_fused" in lib().qmm_last_kernel().decode()
         out = out.cpu().numpy()
         check_against_oracle(qtype, stack, x, out, sorted_ids, expert_ids, tw, topk)
         check_against_forward(stack, xs, out, sorted_ids, expert_ids, tw, topk)
