@@ -599,17 +599,18 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 constexpr int kMoeFusedMaxEntries = 256;  // routings the fused form takes (each wave scans them)
 constexpr int kFp4Pairs = 4;       // entries a pass: the product's 4 row groups
 constexpr int kFp4Rows = 16;       // weight rows a wave: the product's 16 columns
-// A step takes 8 blocks (136 bytes) of each of the wave's rows: the
+// A step takes 16 blocks (272 bytes) of each of the wave's rows: the
 // 16-byte pieces from the one holding its first byte to the one holding its
-// last, row r's at piece 11 r .. of the wave's stage buffer.
-constexpr int kFp4StepBlocks = 8;
-constexpr int kFp4SegPieces = 10;  // 136 bytes at any alignment
-constexpr int kFp4Slots = kFp4Rows * kFp4SegPieces;  // pieces a step: 160
-constexpr int kFp4Loads = (kFp4Slots + 63) / 64;     // a lane's: 3
-// a row's 10 pieces 176 bytes apart (44 banks: the 16 rows of a read on
-// distinct banks; 160 bytes put rows 8 apart, whose bytes also share their
-// alignment, on the same ones)
-constexpr int kFp4RowStride = 11;
+// last, row r's at piece 19 r .. of the wave's stage buffer.
+constexpr int kFp4StepBlocks = 16;
+constexpr int kFp4StepBytes = 17 * kFp4StepBlocks;
+constexpr int kFp4SegPieces = (15 + kFp4StepBytes + 15) / 16;  // 272 bytes at any alignment: 18
+constexpr int kFp4Slots = kFp4Rows * kFp4SegPieces;  // pieces a step: 288
+constexpr int kFp4Loads = (kFp4Slots + 63) / 64;     // a lane's: 5
+// a row's 18 pieces 304 bytes apart (12 banks on: the 16 rows of a read on
+// distinct banks; a stride of 10 pieces to 8 blocks put rows 8 apart, whose
+// bytes also share their alignment, on the same ones)
+constexpr int kFp4RowStride = 19;
 constexpr int kFp4Stage = kFp4Rows * kFp4RowStride * 16 + 16;  // and the dword past the last that lds_words reads
 constexpr int kFp4Rec = 64;  // LDS bytes of an entry's block: h0 h1 l0 l1, 16 bytes each
 constexpr int kFp4Ring = 2;  // steps in flight per wave
@@ -749,8 +750,8 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
         const uint8_t* base = Wr;
         const uint32_t bofs = (uint32_t)(uintptr_t)base & 15u;
         const uint8_t* const ba = base - bofs;
-        const int blen = real ? (nb - 8 * ls < 8 ? nb - 8 * ls : 8) : 1;
-        const uint32_t st = bofs + (real ? 136u * (uint32_t)ls : 0u);
+        const int blen = real ? (nb - kFp4StepBlocks * ls < kFp4StepBlocks ? nb - kFp4StepBlocks * ls : kFp4StepBlocks) : 1;
+        const uint32_t st = bofs + (real ? (uint32_t)kFp4StepBytes * (uint32_t)ls : 0u);
 #pragma unroll
         for (int c = 0; c < kFp4Loads; c++) {
           const uint32_t rel = (real ? lpk[c] & 0xFFFFu : 0u) + st;  // the step's first byte, from ba
@@ -848,26 +849,26 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
       const uint32_t browlo = (uint32_t)(uintptr_t)Wr + (uint32_t)(rowc * (int)rb);  // row rowc's address, low bits
 
       // wave_sum_dpp's tree over the row's 64 leaves (lane L's leaf is unit
-      // L): group t's node holds 2 leaves, step j's two groups give its node
-      // of 4, x = g0 + g1, and push(x, j) folds it in as a binary counter
-      // over j: v4 .. v32 keep the pending nodes of 4 .. 32 leaves (every sum
-      // formed, the stores selected: j is uniform)
-      float v4 = 0.0f, v8 = 0.0f, v16 = 0.0f, v32 = 0.0f, res = 0.0f;
+      // L): group t's node holds 2 leaves, step j's four groups give its node
+      // of 8, x = (g0 + g1) + (g2 + g3), and push(x, j) folds it in as a
+      // binary counter over j: v8 .. v32 keep the pending nodes of 8 .. 32
+      // leaves (every sum formed, the stores selected: j is uniform)
+      float v8 = 0.0f, v16 = 0.0f, v32 = 0.0f, res = 0.0f;
       auto push = [&](float x, int j) {
-        const bool b0 = j & 1, b1 = (j & 3) == 3, b2 = (j & 7) == 7, b3 = (j & 15) == 15;
-        const float x8 = v4 + x, x16 = v8 + x8, x32 = v16 + x16, x64 = v32 + x32;
-        v4 = b0 ? v4 : x;
-        v8 = b0 && !(j & 2) ? x8 : v8;
-        v16 = b1 && !(j & 4) ? x16 : v16;
-        v32 = b2 && !(j & 8) ? x32 : v32;
-        res = b3 ? x64 : res;
+        const bool b0 = j & 1, b1 = (j & 3) == 3, b2 = (j & 7) == 7;
+        const float x16 = v8 + x, x32 = v16 + x16, x64 = v32 + x32;
+        v8 = b0 ? v8 : x;
+        v16 = b0 && !(j & 2) ? x16 : v16;
+        v32 = b1 && !(j & 4) ? x32 : v32;
+        res = b2 ? x64 : res;
       };
       auto step = [&](Fp4Span& cur, int j) {
         __builtin_amdgcn_sched_barrier(0);
         wave_lds_sync();
 #pragma unroll
         for (int c = 0; c < kFp4Loads; c++)
-          if (lane + 64 * c < kFp4Slots) *(uint4*)(buf + 16 * (lane + 64 * c + (lane + 64 * c) / kFp4SegPieces)) = cur.p[c];
+          if (lane + 64 * c < kFp4Slots)
+            *(uint4*)(buf + 16 * (lane + 64 * c + (kFp4RowStride - kFp4SegPieces) * ((lane + 64 * c) / kFp4SegPieces))) = cur.p[c];
         wave_lds_sync();
         load_next(cur);
         if (j >= nsteps) return;
@@ -910,7 +911,7 @@ __global__ __launch_bounds__(64 * kMoeSWaves) __attribute__((amdgpu_waves_per_eu
           g[t] = 0.0f + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
           __builtin_amdgcn_sched_barrier(0);  // one group's operands live at a time
         }
-        push(g[0] + g[1], j);
+        push((g[0] + g[1]) + (g[2] + g[3]), j);
       };
       for (int j = 0; j < nsteps; j += kFp4Ring) {
 #pragma unroll
