@@ -180,6 +180,28 @@ def test_moe_fp4_matrix_core_rows(k):
         check_against_forward(stack, xs, out, sorted_ids, expert_ids, tw, topk)
 
 
+@pytest.mark.parametrize("size_m", [256, 257])
+def test_moe_fp4_one_launch_boundary(size_m):
+    """MXFP4 routings of up to 256 entries take the one-launch form (the
+    kernel quantizing its input rows and finding the runs), 257 and more the
+    quantizing launch and its run table; on both sides of the line every
+    entry equals qmm_forward of its pair bit for bit, with per-pair inputs
+    and routing weights (2880-value rows, runs of many entries)."""
+    qtype = MOE_TYPES["MXFP4"]
+    E, n, k, topk = 6, 48, 2880, 1
+    sorted_ids, expert_ids, topk_w = routing(size_m, E, topk, 257 + size_m)
+    stack = expert_stack(qtype, E, n, k, size_m)
+    x = np.random.default_rng(size_m).standard_normal((size_m, k)).astype(np.float32)
+    xs = t32(x)
+    out = moe_forward(xs, stack, t32(sorted_ids), t32(expert_ids), t32(topk_w), topk)
+    kernel = lib().qmm_last_kernel().decode()
+    assert ("launch_moe_fp4_fused" in kernel) == (size_m <= 256) and "launch_moe_fp4" in kernel, kernel
+    out = out.cpu().numpy()
+    check_against_forward(stack, xs, out, sorted_ids, expert_ids, topk_w, topk)
+    sel = slice(0, size_m, 16)
+    check_against_oracle(qtype, stack, x, out, sorted_ids[sel], expert_ids[sel], topk_w, topk)
+
+
 def moe_into(stack, xs, x_stride, sorted_ids, expert_ids, topk_w, topk, rows_out, fill=float("nan")):
     """qmm_moe_forward through the C ABI into an output prefilled with `fill`
     (rows the routing does not reach keep it)."""
