@@ -35,6 +35,7 @@ namespace {
 
 constexpr int kKqWaves = 8;  // waves per workgroup
 constexpr int kKqPairs = 8;  // most entries a chunk holds
+constexpr int kKqFusedMaxEntries = 256;  // routings the fused form takes (each wave scans them)
 constexpr size_t kKqLdsBudget = 64 * 1024;
 
 // The chunk's activation rows in LDS: codes int8 [P][k], group sums int16
@@ -104,12 +105,19 @@ __host__ __device__ inline size_t kq_stage_bytes() {
 // the 1-row kernel's wave sum (a + b) + (c + d) over the same units, whose
 // other rows of lanes hold no unit and add +0 (a sum of units is never -0:
 // every lane's sum starts at +0), so each row's result is bit-identical.
-template <int TYPE, int T, int P>
+// kFused: the kernel takes the f32 input rows and the routing's expert ids
+// itself (the one launch of a small routing): each wave finds its runs in
+// expert_ids, and the chunk's Q8_K codes, group sums and scales are made in
+// LDS by q8k_block_group16, act_q8k_kernel's routine (quantize.hip), so they
+// have its bits. Otherwise they come from launch_act_quantize_moe.
+template <int TYPE, int T, int P, bool kFused>
 __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
     const uint8_t* __restrict__ W, int64_t n, int nsb, int64_t estride, int num_experts,
     const int8_t* __restrict__ yq, const float* __restrict__ yd, const int16_t* __restrict__ ybs,
-    const int32_t* __restrict__ runs, const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int topk,
-    int size_m, float* __restrict__ dst, int64_t ldd, int rpw, int npairs) {
+    const int32_t* __restrict__ runs, const float* __restrict__ xa, int64_t x_stride,
+    const int32_t* __restrict__ expert_ids, int xvec, float qmax, const int32_t* __restrict__ ids,
+    const float* __restrict__ topk_w, int topk, int size_m, float* __restrict__ dst, int64_t ldd, int rpw,
+    int npairs) {
   static_assert(P == 1 || T == 1, "packed rows take one unit a lane");
   constexpr int G = 64 / P;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -137,11 +145,39 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
 
   // Runs blockIdx.y, blockIdx.y + gridDim.y, ...; the loop and its barriers
   // are uniform over the workgroup.
-  const int nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  // fused: a run starts at entry 0 and wherever the expert differs from the
+  // entry before (moe_runs_block's table, found by ballots over 64 entries)
+  auto run_start = [&](int i) { return i < size_m && (i == 0 || expert_ids[i] != expert_ids[i - 1]); };
+  int nruns;
+  if (kFused) {
+    int c = 0;
+    for (int c0 = 0; c0 < size_m; c0 += 64) c += __builtin_popcountll(__ballot(run_start(c0 + lane)));
+    nruns = __builtin_amdgcn_readfirstlane(c);
+  } else {
+    nruns = __builtin_amdgcn_readfirstlane(runs[0]);
+  }
   for (int run = blockIdx.y; run < nruns; run += gridDim.y) {
-    const int start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
-    const int len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
-    const int e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+    int start, len, e;
+    if (kFused) {
+      // the run-th and (run + 1)-th starts (size_m past the last)
+      int s0 = size_m, s1 = size_m, cum = 0;
+      for (int c0 = 0; c0 < size_m; c0 += 64) {
+        const bool f = run_start(c0 + lane);
+        const uint64_t m = __ballot(f);
+        const int rank = cum + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        const uint64_t m0 = __ballot(f && rank == run), m1 = __ballot(f && rank == run + 1);
+        if (m0 && s0 == size_m) s0 = c0 + __builtin_ctzll(m0);
+        if (m1 && s1 == size_m) s1 = c0 + __builtin_ctzll(m1);
+        cum += __builtin_popcountll(m);
+      }
+      start = __builtin_amdgcn_readfirstlane(s0);
+      len = __builtin_amdgcn_readfirstlane(s1 - s0);
+      e = __builtin_amdgcn_readfirstlane(expert_ids[start]);
+    } else {
+      start = __builtin_amdgcn_readfirstlane(runs[1 + 3 * run]);
+      len = __builtin_amdgcn_readfirstlane(runs[2 + 3 * run]);
+      e = __builtin_amdgcn_readfirstlane(runs[3 + 3 * run]);
+    }
     if (e < 0 || e >= num_experts) continue;
     const uint8_t* We = W + (int64_t)e * estride;
 
@@ -158,7 +194,7 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
           load_q6_span(spn, We + (r0 + lr) * rowbytes + (int64_t)s0 * 210, nsb - s0 < kQ6SpanSb ? nsb - s0 : kQ6SpanSb,
                        lane);
         } else {
-          load_q6_span(spn, (const uint8_t*)yq, 1, lane);
+          load_q6_span(spn, We, 1, lane);  // (the expert's first super-block: cached, never used)
         }
         if (++lsp == nspan) {
           lsp = 0;
@@ -190,7 +226,38 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
 
       // the chunk's activation rows into LDS, after the previous chunk's reads
       __syncthreads();
-      {
+      if (kFused) {
+        // 16 lanes a super-block of an entry's input row, as act_q8k_kernel
+        const int gl = lane & 15;
+        for (int t = threadIdx.x >> 4; t < npairs * nsb; t += 4 * kKqWaves) {
+          const int p = t / nsb, b = t - p * nsb;  // uniform over the 16 lanes
+          bool u = false;
+          int64_t ir = 0;
+#pragma unroll
+          for (int pp = 0; pp < kKqPairs; pp++)
+            if (p == pp) u = use[pp], ir = in_row[pp];
+          if (!u) continue;
+          const float* xp = xa + ir * x_stride + (int64_t)b * 256 + 16 * gl;
+          float v[16];
+          if (xvec) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const float4 f = ((const float4*)xp)[i];
+              v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = xp[i];
+          }
+          uint32_t c[4];
+          int32_t sum16;
+          float d;
+          q8k_block_group16(v, gl, qmax, c, sum16, d);
+          *(uint4*)(acodes + (size_t)p * k + 256 * b + 16 * gl) = make_uint4(c[0], c[1], c[2], c[3]);
+          asums[(size_t)p * 16 * nsb + 16 * b + gl] = (int16_t)sum16;
+          if (gl == 0) ad[p * nsb + b] = d;
+        }
+      } else {
         const int cpr = k / 16, spr = 2 * nsb;  // 16-byte pieces a row: codes, group sums
 #pragma unroll
         for (int p = 0; p < kKqPairs; p++) {
@@ -364,10 +431,19 @@ __global__ __launch_bounds__(64 * kKqWaves) void moe_kq_kernel(
   }
 }
 
-template <int TYPE, int T, int P>
+// The fused form (fx set: the f32 input rows, expert ids, quantizer scale)
+// or the form that reads launch_act_quantize_moe's planes and run table.
+struct KqFused {
+  const float* x;
+  int64_t x_stride;
+  const int32_t* expert_ids;
+  float qmax;
+};
+
+template <int TYPE, int T, int P, bool kFused = false>
 hipError_t launch_kq(const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p, const int32_t* runs,
                      const int32_t* ids, const float* topk_w, int topk, int64_t size_m, float* dst, int64_t ldd,
-                     int cus, hipStream_t st) {
+                     int cus, hipStream_t st, const KqFused& fx = KqFused{}) {
   QMM_NOTE_LAUNCH();
   const int nsb = (int)(k / 256);
   const int64_t estride = n * nsb * (TYPE == T_Q4_K ? 144 : 210);
@@ -383,12 +459,34 @@ hipError_t launch_kq(const void* w, int num_experts, int64_t n, int64_t k, const
   const int64_t rows_per_wg = (int64_t)kKqWaves * rpw;
   const dim3 grid((unsigned)((n + rows_per_wg - 1) / rows_per_wg), (unsigned)(gy < 1 ? 1 : gy));
   const size_t lds = kq_act_bytes(nsb, (int)pairs) + kq_stage_bytes<TYPE>();
-  constexpr auto* kfn = &moe_kq_kernel<TYPE, T, P>;
+  constexpr auto* kfn = &moe_kq_kernel<TYPE, T, P, kFused>;
   if (lds > 65536 && set_max_dynamic_lds<kfn>() != hipSuccess) return hipErrorInvalidValue;
+  const int xvec = ((uintptr_t)fx.x % 16 == 0) && (fx.x_stride % 4 == 0);
   kfn<<<grid, 64 * kKqWaves, lds, st>>>((const uint8_t*)w, n, nsb, estride, num_experts, p.codes, p.d,
-                                        (const int16_t*)p.sums, runs, ids, topk_w, topk, (int)size_m, dst, ldd,
-                                        (int)rpw, (int)pairs);
+                                        (const int16_t*)p.sums, runs, fx.x, fx.x_stride, fx.expert_ids, xvec, fx.qmax,
+                                        ids, topk_w, topk, (int)size_m, dst, ldd, (int)rpw, (int)pairs);
   return hipGetLastError();
+}
+
+template <bool kFused>
+hipError_t launch_moe_kq_form(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
+                              const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
+                              float* dst, int64_t ldd, int cus, hipStream_t st, const KqFused& fx) {
+  if (!moe_kq_supported(type, k)) return hipErrorInvalidValue;
+  const int64_t nsb = k / 256;
+#define KQ(TY, T, P) launch_kq<TY, T, P, kFused>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st, fx)
+  if (type == T_Q6_K) {
+    if (nsb <= 4) return KQ(T_Q6_K, 1, 4);
+    if (nsb <= 8) return KQ(T_Q6_K, 1, 2);
+    return KQ(T_Q6_K, 1, 1);
+  }
+  if (nsb <= 4) return KQ(T_Q4_K, 1, 4);
+  if (nsb <= 8) return KQ(T_Q4_K, 1, 2);
+  const int64_t T = (nsb + 15) / 16;
+  if (T <= 1) return KQ(T_Q4_K, 1, 1);
+  if (T <= 2) return KQ(T_Q4_K, 2, 1);
+  return KQ(T_Q4_K, 4, 1);
+#undef KQ
 }
 
 }  // namespace
@@ -403,19 +501,20 @@ bool moe_kq_supported(int type, int64_t k) {
 hipError_t launch_moe_kq(int type, const void* w, int num_experts, int64_t n, int64_t k, const ActPlanes& p,
                          const int32_t* runs, const int32_t* ids, const float* topk_w, int topk, int64_t size_m,
                          float* dst, int64_t ldd, int cus, hipStream_t st) {
-  if (!moe_kq_supported(type, k)) return hipErrorInvalidValue;
-  const int64_t nsb = k / 256;
-  if (type == T_Q6_K) {
-    if (nsb <= 4) return launch_kq<T_Q6_K, 1, 4>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-    if (nsb <= 8) return launch_kq<T_Q6_K, 1, 2>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-    return launch_kq<T_Q6_K, 1, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-  }
-  if (nsb <= 4) return launch_kq<T_Q4_K, 1, 4>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-  if (nsb <= 8) return launch_kq<T_Q4_K, 1, 2>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-  const int64_t T = (nsb + 15) / 16;
-  if (T <= 1) return launch_kq<T_Q4_K, 1, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-  if (T <= 2) return launch_kq<T_Q4_K, 2, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
-  return launch_kq<T_Q4_K, 4, 1>(w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st);
+  return launch_moe_kq_form<false>(type, w, num_experts, n, k, p, runs, ids, topk_w, topk, size_m, dst, ldd, cus, st,
+                                   KqFused{});
+}
+
+bool moe_kq_fused_takes(int type, int64_t k, int64_t size_m) {
+  return moe_kq_supported(type, k) && size_m <= kKqFusedMaxEntries;
+}
+
+hipError_t launch_moe_kq_fused(int type, const void* w, int num_experts, int64_t n, int64_t k, const float* x,
+                               int64_t x_stride, const int32_t* expert_ids, const int32_t* ids, const float* topk_w,
+                               int topk, int64_t size_m, float* dst, int64_t ldd, float qmax, int cus,
+                               hipStream_t st) {
+  return launch_moe_kq_form<true>(type, w, num_experts, n, k, ActPlanes{}, nullptr, ids, topk_w, topk, size_m, dst,
+                                  ldd, cus, st, KqFused{x, x_stride, expert_ids, qmax});
 }
 
 }  // namespace qmm

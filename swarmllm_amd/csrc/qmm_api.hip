@@ -837,6 +837,13 @@ int qmm_moe_forward(int type, const void* w, int num_experts, const float* x, in
     g_moe_launches.fetch_add(1, std::memory_order_relaxed);
     return QMM_OK;
   }
+  if (layout == qmm::ACT_Q8K && qmm::moe_kq_fused_takes(type, k, size_m)) {
+    if (qmm::launch_moe_kq_fused(type, w, num_experts, n, k, x, x_stride, expert_ids, sorted_ids, topk_w, topk, size_m,
+                                 dst, ldd, q8k_scale(), (int)cu_count(), st) != hipSuccess)
+      return QMM_DEVICE_ERROR;
+    g_moe_launches.fetch_add(1, std::memory_order_relaxed);
+    return QMM_OK;
+  }
   // the activation's planes (Q8_K for Q4_K / Q6_K, else Q8_0) and the run
   // table, one launch; then the grouped kernel
   int32_t* runs = (int32_t*)((char*)workspace + act);

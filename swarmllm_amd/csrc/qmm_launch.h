@@ -134,6 +134,13 @@ hipError_t launch_moe(int type, const void* w, int num_experts, int64_t n, int64
 // input rows itself (the same codes, scales and result bits as the two-launch
 // form).
 bool moe_fp4_fused_takes(int type, int64_t k, int64_t size_m);
+// The same for Q4_K and Q6_K routings of up to 256 entries (moe_kq.hip: the
+// input rows quantized to Q8_K in LDS with qmax as launch_act_quantize_moe).
+bool moe_kq_fused_takes(int type, int64_t k, int64_t size_m);
+hipError_t launch_moe_kq_fused(int type, const void* w, int num_experts, int64_t n, int64_t k, const float* x,
+                               int64_t x_stride, const int32_t* expert_ids, const int32_t* ids, const float* topk_w,
+                               int topk, int64_t size_m, float* dst, int64_t ldd, float qmax, int cus,
+                               hipStream_t st);
 hipError_t launch_moe_fp4_fused(const void* w, int num_experts, int64_t n, int64_t k, const float* x,
                                 int64_t x_stride, const int32_t* expert_ids, const int32_t* ids, const float* topk_w,
                                 int topk, int64_t size_m, float* dst, int64_t ldd, hipStream_t st);
