@@ -202,6 +202,28 @@ def test_moe_fp4_one_launch_boundary(size_m):
     check_against_oracle(qtype, stack, x, out, sorted_ids[sel], expert_ids[sel], topk_w, topk)
 
 
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("size_m", [256, 257])
+def test_moe_kq_one_launch_boundary(name, size_m):
+    """Q4_K and Q6_K routings of up to 256 entries take the one-launch form
+    (the kernel quantizing its input rows to Q8_K in LDS and finding the
+    runs), larger ones the quantizing launch and its run table; on both sides
+    every entry equals qmm_forward of its pair bit for bit."""
+    qtype = MOE_TYPES[name]
+    E, n, k, topk = 6, 48, 2048, 1
+    sorted_ids, expert_ids, topk_w = routing(size_m, E, topk, 911 + size_m)
+    stack = expert_stack(qtype, E, n, k, 3 * size_m)
+    x = np.random.default_rng(size_m + 5).standard_normal((size_m, k)).astype(np.float32)
+    xs = t32(x)
+    out = moe_forward(xs, stack, t32(sorted_ids), t32(expert_ids), t32(topk_w), topk)
+    kernel = lib().qmm_last_kernel().decode()
+    assert ("kFused = true" in kernel) == (size_m <= 256), kernel
+    out = out.cpu().numpy()
+    check_against_forward(stack, xs, out, sorted_ids, expert_ids, topk_w, topk)
+    sel = slice(0, size_m, 16)
+    check_against_oracle(qtype, stack, x, out, sorted_ids[sel], expert_ids[sel], topk_w, topk)
+
+
 def moe_into(stack, xs, x_stride, sorted_ids, expert_ids, topk_w, topk, rows_out, fill=float("nan")):
     """qmm_moe_forward through the C ABI into an output prefilled with `fill`
     (rows the routing does not reach keep it)."""
