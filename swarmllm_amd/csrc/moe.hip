@@ -21,7 +21,8 @@
 // one extra workgroup of the launch that quantizes the activation
 // (launch_act_quantize_moe), so a product is two launches; MXFP4 routings of
 // up to 256 entries take one (launch_moe_fp4_fused: the kernel quantizes its
-// input rows and finds the runs itself).
+// input rows and finds the runs itself; moe_kq.hip does the same for Q4_K and
+// Q6_K).
 // The per-unit arithmetic and the reduction are the decode kernel's
 // (b32_common.h, wave_sum_dpp), so each pair's result is bit-identical to
 // the same product through qmm_forward (times its scale): the reference's
